@@ -1,0 +1,131 @@
+/*
+ * pitch_amd.h - C ABI of the MI355X (gfx950) KV-cache codec library libpitch_amd.so.
+ *
+ * Drop-in boundary for the codec path of SwiftCham/PITCH. Each entry point below replaces one operator of
+ * the reference's Swift surface (file:line in /root/reference) with the same argument meaning, the same
+ * validation and the same error categories. Buffers are device pointers owned by the caller; every offset
+ * is in bytes and must be a non-negative multiple of 4; every length is the byte size of the whole buffer
+ * starting at the pointer, so the library can perform the reference's "needs N bytes after offset" check.
+ * The enqueue functions validate, launch on the given HIP stream and return without waiting, as the
+ * reference's enqueue* calls encode into the caller's command buffer (Sources/PITCH/PITCH.swift:136-165).
+ *
+ * Deviation: counts and offsets are 64-bit, so a single call may cover count * dim >= 2^32 elements,
+ * which the reference rejects (Sources/PITCH/Core/Codec.swift:30-32). Per-channel calls require
+ * count < 2^32 tokens.
+ */
+#ifndef PITCH_AMD_H
+#define PITCH_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes, mirroring PITCHError (Sources/PITCH/Core/PITCHError.swift:10-19). */
+#define PITCH_OK 0
+#define PITCH_ERR_INVALID_INPUT (-1)          /* PITCHError.invalidInput */
+#define PITCH_ERR_INVALID_BIT_WIDTH (-2)      /* PITCHError.invalidBitWidth */
+#define PITCH_ERR_INVALID_DIMENSION (-3)      /* PITCHError.invalidDimension */
+#define PITCH_ERR_CONFIGURATION_MISMATCH (-4) /* PITCHError.configurationMismatch */
+#define PITCH_ERR_ENCODING_FAILED (-5)        /* PITCHError.encodingFailed */
+#define PITCH_ERR_DECODING_FAILED (-6)        /* PITCHError.decodingFailed */
+#define PITCH_ERR_DEVICE_UNAVAILABLE (-7)     /* PITCHError.metalNotSupported (no usable GPU) */
+
+/* QuantMethod (Sources/PITCH/Models/QuantMethod.swift:8-11). */
+#define PITCH_METHOD_TURBO 0u
+#define PITCH_METHOD_POLAR 1u
+
+/* Default rotation seed, PITCH.defaultSeed = 0x50495443 (Sources/PITCH/PITCH.swift:18). */
+#define PITCH_DEFAULT_SEED 0x50495443u
+
+/* QuantConfig (Sources/PITCH/Models/QuantConfig.swift:11-60); same 16-byte layout as BatchParams minus
+ * count (Sources/PITCH/Core/Codec.swift:12-17). */
+typedef struct pitch_config {
+  uint32_t method; /* PITCH_METHOD_TURBO or PITCH_METHOD_POLAR */
+  uint32_t dim;    /* power of two, 2..1024 */
+  uint32_t bits;   /* 2..8 */
+  uint32_t seed;   /* rotation seed */
+} pitch_config_t;
+
+/* ChannelQuantConfig (Sources/PITCH/PerChannel.swift:15-70). */
+typedef struct pitch_channel_config {
+  uint32_t dim;        /* channels per token, 1..1024 (any value) */
+  uint32_t bits;       /* 2..8 */
+  uint32_t group_size; /* tokens per group, 1..65536 */
+  uint32_t reserved;   /* 0 */
+} pitch_channel_config_t;
+
+/* Library version as 0xMMmmpp. */
+uint32_t pitch_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* pitch_last_error(void);
+
+/* Validates and fills a QuantConfig; *code_stride = ceil(dim * bits / 32) * 4 bytes.
+ * Replaces PITCH.config(method:dim:bits:) / QuantConfig.init (Sources/PITCH/PITCH.swift:53-55,
+ * Sources/PITCH/Models/QuantConfig.swift:24-35,47). code_stride may be NULL. */
+int pitch_config(uint32_t method, uint32_t dim, uint32_t bits, uint32_t seed, pitch_config_t* out,
+                 uint32_t* code_stride);
+
+/* Validates and fills a ChannelQuantConfig; *code_stride = ceil(dim * bits / 32) * 4 bytes and
+ * *range_stride = 4 * dim bytes (fp16 minima then maxima per group).
+ * Replaces PITCH.channelConfig(dim:bits:groupSize:) / ChannelQuantConfig.init
+ * (Sources/PITCH/PerChannel.swift:184-187,30-43,55,58). Either output stride may be NULL. */
+int pitch_channel_config(uint32_t dim, uint32_t bits, uint32_t group_size, pitch_channel_config_t* out,
+                         uint32_t* code_stride, uint32_t* range_stride);
+
+/* Encodes count contiguous fp32 vectors: writes count * code_stride bytes of packed codes and count fp32
+ * scales (the norm for TurboQuant, the largest pair radius for PolarQuant).
+ * Replaces PITCH.enqueueEncode(input:inputOffset:codes:codesOffset:scales:scalesOffset:count:config:
+ * commandBuffer:) (Sources/PITCH/PITCH.swift:144-153 -> Sources/PITCH/Core/Codec.swift:70-103). */
+int pitch_enqueue_encode(const pitch_config_t* config, const void* input, uint64_t input_bytes,
+                         uint64_t input_offset, void* codes, uint64_t codes_bytes, uint64_t codes_offset,
+                         void* scales, uint64_t scales_bytes, uint64_t scales_offset, uint64_t count,
+                         void* stream /* hipStream_t; NULL = default stream */);
+
+/* Decodes count vectors into count * dim fp32 values.
+ * Replaces PITCH.enqueueDecode(codes:codesOffset:scales:scalesOffset:output:outputOffset:count:config:
+ * commandBuffer:) (Sources/PITCH/PITCH.swift:156-165 -> Sources/PITCH/Core/Codec.swift:107-140). */
+int pitch_enqueue_decode(const pitch_config_t* config, const void* codes, uint64_t codes_bytes,
+                         uint64_t codes_offset, const void* scales, uint64_t scales_bytes,
+                         uint64_t scales_offset, void* output, uint64_t output_bytes, uint64_t output_offset,
+                         uint64_t count, void* stream);
+
+/* Encodes count tokens of one head's keys (token-major, dim channels) per channel over groups of
+ * group_size tokens: writes count * code_stride bytes of codes and ceil(count / group_size) * range_stride
+ * bytes of fp16 ranges laid out [group][min row of dim][max row of dim].
+ * Replaces PITCH.enqueuePerChannelEncode(input:inputOffset:codes:codesOffset:ranges:rangesOffset:count:
+ * config:commandBuffer:) (Sources/PITCH/PerChannel.swift:251-260 -> :338-363). */
+int pitch_enqueue_channel_encode(const pitch_channel_config_t* config, const void* input,
+                                 uint64_t input_bytes, uint64_t input_offset, void* codes,
+                                 uint64_t codes_bytes, uint64_t codes_offset, void* ranges,
+                                 uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count,
+                                 void* stream);
+
+/* Decodes count per-channel tokens into count * dim fp32 values.
+ * Replaces PITCH.enqueuePerChannelDecode(codes:codesOffset:ranges:rangesOffset:output:outputOffset:count:
+ * config:commandBuffer:) (Sources/PITCH/PerChannel.swift:261-270 -> :365-389). */
+int pitch_enqueue_channel_decode(const pitch_channel_config_t* config, const void* codes,
+                                 uint64_t codes_bytes, uint64_t codes_offset, const void* ranges,
+                                 uint64_t ranges_bytes, uint64_t ranges_offset, void* output,
+                                 uint64_t output_bytes, uint64_t output_offset, uint64_t count,
+                                 void* stream);
+
+/* Packs count rows of dim unpacked codes (one uint8 per code, each < 2^bits) into count * code_stride
+ * bytes, code i at bits [i * bits, i * bits + bits) of the row's little-endian 32-bit words.
+ * Replaces pack_codes (reference/pitch_reference.py:68-78). */
+int pitch_enqueue_pack_codes(uint32_t dim, uint32_t bits, const void* unpacked, uint64_t unpacked_bytes,
+                             uint64_t unpacked_offset, void* packed, uint64_t packed_bytes,
+                             uint64_t packed_offset, uint64_t count, void* stream);
+
+/* Inverse of pitch_enqueue_pack_codes. Replaces unpack_codes (reference/pitch_reference.py:80-90). */
+int pitch_enqueue_unpack_codes(uint32_t dim, uint32_t bits, const void* packed, uint64_t packed_bytes,
+                               uint64_t packed_offset, void* unpacked, uint64_t unpacked_bytes,
+                               uint64_t unpacked_offset, uint64_t count, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PITCH_AMD_H */

@@ -1,0 +1,81 @@
+"""ctypes binding of libpitch_amd.so (the C ABI in include/pitch_amd.h).
+
+There is no fallback: if the library is missing or fails to load, every codec call raises
+DeviceUnavailable with the reason.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libpitch_amd.so"
+
+PITCH_OK = 0
+ERR_INVALID_INPUT = -1
+ERR_INVALID_BIT_WIDTH = -2
+ERR_INVALID_DIMENSION = -3
+ERR_CONFIGURATION_MISMATCH = -4
+ERR_ENCODING_FAILED = -5
+ERR_DECODING_FAILED = -6
+ERR_DEVICE_UNAVAILABLE = -7
+
+
+class PitchConfigC(ctypes.Structure):
+    _fields_ = [("method", ctypes.c_uint32), ("dim", ctypes.c_uint32), ("bits", ctypes.c_uint32),
+                ("seed", ctypes.c_uint32)]
+
+
+class PitchChannelConfigC(ctypes.Structure):
+    _fields_ = [("dim", ctypes.c_uint32), ("bits", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32)]
+
+
+_u32, _u64, _vp, _int = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
+
+# name -> (restype, argtypes); every symbol declared in include/pitch_amd.h
+SIGNATURES = {
+    "pitch_version": (_u32, []),
+    "pitch_last_error": (ctypes.c_char_p, []),
+    "pitch_config": (_int, [_u32, _u32, _u32, _u32, ctypes.POINTER(PitchConfigC), ctypes.POINTER(_u32)]),
+    "pitch_channel_config": (_int, [_u32, _u32, _u32, ctypes.POINTER(PitchChannelConfigC),
+                                    ctypes.POINTER(_u32), ctypes.POINTER(_u32)]),
+    "pitch_enqueue_encode": (_int, [ctypes.POINTER(PitchConfigC), _vp, _u64, _u64, _vp, _u64, _u64,
+                                    _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_decode": (_int, [ctypes.POINTER(PitchConfigC), _vp, _u64, _u64, _vp, _u64, _u64,
+                                    _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_channel_encode": (_int, [ctypes.POINTER(PitchChannelConfigC), _vp, _u64, _u64, _vp,
+                                            _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_channel_decode": (_int, [ctypes.POINTER(PitchChannelConfigC), _vp, _u64, _u64, _vp,
+                                            _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_pack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_unpack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_load_error: str | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads the library once; raises RuntimeError with the reason if it cannot."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                _load_error = (f"HIP extension {LIB_PATH.name} is not built (expected at {LIB_PATH}); "
+                               "run `python -m pitch_amd.build`")
+                raise RuntimeError(_load_error)
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().pitch_last_error().decode("utf-8", "replace")

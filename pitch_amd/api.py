@@ -1,0 +1,810 @@
+"""Host-side operator surface of the MI355X codec, mirroring SwiftCham/PITCH's public API.
+
+Types and methods keep the reference's names and meaning (Sources/PITCH/PITCH.swift, PerChannel.swift,
+Models/*.swift): ``QuantConfig``, ``ChannelQuantConfig``, ``CompressedBatch``, ``ChannelCompressedBlock``,
+``PITCH.config/encode/decode/enqueueEncode/enqueueDecode`` and the per-channel forms. Tensors are
+PyTorch-ROCm device tensors; the GPU-resident ``enqueue*`` forms take caller-owned tensors with byte
+offsets and launch on a HIP stream without waiting, like the reference's command-buffer forms. The array
+forms copy, launch, wait and copy back.
+
+All arithmetic runs in libpitch_amd.so (hand-written HIP kernels); this module only validates, allocates
+and calls through the C ABI.
+"""
+from __future__ import annotations
+
+import base64
+import ctypes
+import enum
+import json
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+
+DEFAULT_SEED = 0x50495443                 # PITCH.defaultSeed (Sources/PITCH/PITCH.swift:18)
+
+
+# ----------------------------------------------------------------------------------------- errors
+class PITCHError(Exception):
+    """Base of the error enum PITCHError (Sources/PITCH/Core/PITCHError.swift:10-19)."""
+
+
+class InvalidInput(PITCHError, ValueError):
+    pass
+
+
+class InvalidBitWidth(PITCHError, ValueError):
+    def __init__(self, bits, message: str | None = None):
+        super().__init__(message or f"Invalid bit width {bits}. Must be in 2...8.")
+        self.bits = bits
+
+
+class InvalidDimension(PITCHError, ValueError):
+    def __init__(self, dim, message: str | None = None):
+        super().__init__(message or f"Invalid dimension {dim}. Must be a power of two in [2, 1024].")
+        self.dim = dim
+
+
+class ConfigurationMismatch(PITCHError):
+    pass
+
+
+class EncodingFailed(PITCHError, RuntimeError):
+    pass
+
+
+class DecodingFailed(PITCHError, RuntimeError):
+    pass
+
+
+class DeviceUnavailable(PITCHError, RuntimeError):
+    """No usable GPU or HIP library (the reference's metalNotSupported)."""
+
+
+def _lib_or_raise():
+    try:
+        return _lib.load()
+    except (RuntimeError, OSError) as e:
+        raise DeviceUnavailable(str(e)) from e
+
+
+def _raise_for(rc: int, what: str = "") -> None:
+    if rc == _lib.PITCH_OK:
+        return
+    msg = _lib.last_error() or what
+    if rc == _lib.ERR_INVALID_BIT_WIDTH:
+        raise InvalidBitWidth(None, msg)
+    if rc == _lib.ERR_INVALID_DIMENSION:
+        raise InvalidDimension(None, msg)
+    raise {
+        _lib.ERR_INVALID_INPUT: InvalidInput,
+        _lib.ERR_CONFIGURATION_MISMATCH: ConfigurationMismatch,
+        _lib.ERR_ENCODING_FAILED: EncodingFailed,
+        _lib.ERR_DECODING_FAILED: DecodingFailed,
+        _lib.ERR_DEVICE_UNAVAILABLE: DeviceUnavailable,
+    }.get(rc, PITCHError)(msg)
+
+
+# ----------------------------------------------------------------------------------------- configs
+class QuantMethod(str, enum.Enum):
+    """Sources/PITCH/Models/QuantMethod.swift:8-11."""
+    turboQuant = "turboQuant"
+    polarQuant = "polarQuant"
+
+    @property
+    def code(self) -> int:
+        return 0 if self is QuantMethod.turboQuant else 1
+
+
+def _method(m) -> QuantMethod:
+    try:
+        return m if isinstance(m, QuantMethod) else QuantMethod(m)
+    except ValueError:
+        raise InvalidInput(f"unknown method {m!r}") from None
+
+
+@dataclass(frozen=True)
+class QuantConfig:
+    """Everything needed to interpret a batch of compressed vectors (Models/QuantConfig.swift:11-60)."""
+    method: QuantMethod
+    dim: int
+    bits: int
+    seed: int = DEFAULT_SEED
+
+    supportedBits = range(2, 9)
+    maxDimension = 1024
+    maxInputMagnitude = 1e17
+
+    def __post_init__(self):
+        object.__setattr__(self, "method", _method(self.method))
+        if not isinstance(self.dim, (int, np.integer)) or not isinstance(self.bits, (int, np.integer)):
+            raise InvalidInput("dim and bits must be integers")
+        if not (0 <= int(self.seed) <= 0xFFFFFFFF):
+            raise InvalidInput(f"seed {self.seed} must fit in 32 bits")
+        if int(self.dim) < 0 or int(self.dim) > 0xFFFFFFFF:
+            raise InvalidDimension(self.dim)
+        if int(self.bits) < 0 or int(self.bits) > 0xFFFFFFFF:
+            raise InvalidBitWidth(self.bits)
+        c = _lib.PitchConfigC()
+        cs = ctypes.c_uint32()
+        _raise_for(_lib_or_raise().pitch_config(self.method.code, int(self.dim), int(self.bits),
+                                                int(self.seed), ctypes.byref(c), ctypes.byref(cs)))
+        object.__setattr__(self, "dim", int(self.dim))
+        object.__setattr__(self, "bits", int(self.bits))
+        object.__setattr__(self, "seed", int(self.seed))
+        object.__setattr__(self, "_cs", int(cs.value))
+
+    def _c(self) -> _lib.PitchConfigC:
+        return _lib.PitchConfigC(self.method.code, self.dim, self.bits, self.seed)
+
+    @property
+    def codeStride(self) -> int:
+        """Bytes of packed codes per vector: ceil(dim * bits / 32) * 4 (QuantConfig.swift:47)."""
+        return self._cs
+
+    @property
+    def bytesPerVector(self) -> int:
+        return self.codeStride + 4
+
+    @property
+    def bitsPerCoordinate(self) -> float:
+        return self.bytesPerVector * 8 / self.dim
+
+    @property
+    def compressionRatio(self) -> float:
+        return 32.0 / self.bitsPerCoordinate
+
+    @property
+    def compressionRatioVsFloat16(self) -> float:
+        return 16.0 / self.bitsPerCoordinate
+
+    def to_dict(self) -> dict:
+        return {"method": self.method.value, "dim": self.dim, "bits": self.bits, "seed": self.seed}
+
+
+@dataclass(frozen=True)
+class ChannelQuantConfig:
+    """Per-channel (KIVI-style) key configuration (Sources/PITCH/PerChannel.swift:15-70)."""
+    dim: int
+    bits: int
+    groupSize: int = 64
+
+    supportedBits = range(2, 9)
+    maxDimension = 1024
+    supportedGroupSizes = range(1, 65537)
+    defaultGroupSize = 64
+    maxInputMagnitude = 65504.0
+
+    def __post_init__(self):
+        for name in ("dim", "bits", "groupSize"):
+            v = getattr(self, name)
+            if not isinstance(v, (int, np.integer)) or not (0 <= int(v) <= 0xFFFFFFFF):
+                raise InvalidInput(f"{name} {v!r} must be a non-negative integer")
+            object.__setattr__(self, name, int(v))
+        c = _lib.PitchChannelConfigC()
+        cs, rs = ctypes.c_uint32(), ctypes.c_uint32()
+        _raise_for(_lib_or_raise().pitch_channel_config(self.dim, self.bits, self.groupSize, ctypes.byref(c),
+                                                        ctypes.byref(cs), ctypes.byref(rs)))
+        object.__setattr__(self, "_cs", int(cs.value))
+        object.__setattr__(self, "_rs", int(rs.value))
+
+    def _c(self) -> _lib.PitchChannelConfigC:
+        return _lib.PitchChannelConfigC(self.dim, self.bits, self.groupSize, 0)
+
+    @property
+    def codeStride(self) -> int:
+        return self._cs
+
+    @property
+    def rangeStride(self) -> int:
+        """Bytes of fp16 ranges per group: dim minima then dim maxima (PerChannel.swift:58)."""
+        return self._rs
+
+    def groupCount(self, tokens: int) -> int:
+        return (int(tokens) + self.groupSize - 1) // self.groupSize
+
+    @property
+    def bitsPerCoordinate(self) -> float:
+        return self.codeStride * 8 / self.dim + self.rangeStride * 8 / (self.dim * self.groupSize)
+
+    @property
+    def compressionRatio(self) -> float:
+        return 32.0 / self.bitsPerCoordinate
+
+    @property
+    def compressionRatioVsFloat16(self) -> float:
+        return 16.0 / self.bitsPerCoordinate
+
+    def to_dict(self) -> dict:
+        return {"dim": self.dim, "bits": self.bits, "groupSize": self.groupSize}
+
+
+# ----------------------------------------------------------------------------------------- containers
+def half_to_float(h: int) -> float:
+    """IEEE fp16 bits to float (PerChannel.swift:171-180)."""
+    return float(np.array([h], dtype=np.uint16).view(np.float16)[0])
+
+
+@dataclass
+class CompressedBatch:
+    """Vectors sharing one QuantConfig: codes of vector i at bytes [i*codeStride, (i+1)*codeStride), scale
+    scales[i] (Sources/PITCH/Models/CompressedBatch.swift:13-121)."""
+    config: QuantConfig
+    codes: bytes
+    scales: np.ndarray
+    _checked: bool = field(default=True, repr=False, compare=False)
+
+    headerByteCount = 16
+    formatVersion = 3
+
+    def __post_init__(self):
+        self.codes = bytes(self.codes)
+        self.scales = np.ascontiguousarray(np.asarray(self.scales, dtype=np.float32).reshape(-1))
+        if self._checked:
+            self.validate()
+
+    def __eq__(self, other):
+        return (isinstance(other, CompressedBatch) and self.config == other.config and self.codes == other.codes
+                and np.array_equal(self.scales.view(np.uint32), other.scales.view(np.uint32)))
+
+    @property
+    def count(self) -> int:
+        return int(self.scales.shape[0])
+
+    def validate(self) -> None:
+        """CompressedBatch.swift:35-47."""
+        if self.count == 0:
+            raise InvalidInput("a batch must contain at least one vector")
+        expected = self.count * self.config.codeStride
+        if len(self.codes) != expected:
+            raise InvalidInput(f"codes is {len(self.codes)} bytes; expected {expected} for {self.count} vectors")
+        if not (np.isfinite(self.scales).all() and (self.scales >= 0).all()):
+            raise InvalidInput("scales must be finite and non-negative")
+
+    def append(self, other: "CompressedBatch") -> None:
+        if other.config != self.config:
+            raise ConfigurationMismatch("cannot append a batch with a different config")
+        self.codes = self.codes + other.codes
+        self.scales = np.concatenate([self.scales, other.scales])
+
+    def vectors(self, rng) -> "CompressedBatch":
+        """The vectors in range(lo, hi) as a new batch (CompressedBatch.swift:59-70)."""
+        lo, hi = (rng.start, rng.stop) if isinstance(rng, (range, slice)) else rng
+        lo = 0 if lo is None else lo
+        hi = self.count if hi is None else hi
+        if lo < 0 or hi > self.count or hi <= lo:
+            raise InvalidInput(f"range {lo}..<{hi} is outside 0..<{self.count}")
+        s = self.config.codeStride
+        return CompressedBatch(self.config, self.codes[lo * s:hi * s], self.scales[lo:hi].copy(), _checked=False)
+
+    @property
+    def payloadByteCount(self) -> int:
+        return len(self.codes)
+
+    @property
+    def sideInformationByteCount(self) -> int:
+        return self.count * 4 + self.headerByteCount
+
+    @property
+    def storedByteCount(self) -> int:
+        return self.payloadByteCount + self.sideInformationByteCount
+
+    @property
+    def originalByteCount(self) -> int:
+        return self.count * self.config.dim * 4
+
+    @property
+    def compressionRatio(self) -> float:
+        return self.originalByteCount / self.storedByteCount
+
+    @property
+    def compressionRatioVsFloat16(self) -> float:
+        return self.compressionRatio / 2
+
+    @property
+    def bitsPerCoordinate(self) -> float:
+        return self.storedByteCount * 8 / (self.count * self.config.dim)
+
+    # Codable form v3 (CompressedBatch.swift:95-121): {"formatVersion", "config", "codes" (base64), "scales"}
+    def to_json(self) -> str:
+        return json.dumps({"formatVersion": self.formatVersion, "config": self.config.to_dict(),
+                           "codes": base64.b64encode(self.codes).decode(),
+                           "scales": [float(s) for s in self.scales]})
+
+    @classmethod
+    def from_json(cls, text: str) -> "CompressedBatch":
+        obj = json.loads(text)
+        if obj.get("formatVersion") != cls.formatVersion:
+            raise InvalidInput(f"Unsupported PITCH format version {obj.get('formatVersion')}; "
+                               f"expected {cls.formatVersion}")
+        c = obj["config"]
+        cfg = QuantConfig(c["method"], c["dim"], c["bits"], c["seed"])
+        return cls(cfg, base64.b64decode(obj["codes"]), np.array(obj["scales"], dtype=np.float32))
+
+
+@dataclass
+class ChannelCompressedBlock:
+    """Per-channel compressed keys: codes per token plus fp16 ranges [group][min row][max row]
+    (Sources/PITCH/PerChannel.swift:72-168)."""
+    config: ChannelQuantConfig
+    codes: bytes
+    ranges: np.ndarray
+    _checked: bool = field(default=True, repr=False, compare=False)
+
+    headerByteCount = 16
+    formatVersion = 1
+
+    def __post_init__(self):
+        self.codes = bytes(self.codes)
+        self.ranges = np.ascontiguousarray(np.asarray(self.ranges, dtype=np.uint16).reshape(-1))
+        if self._checked:
+            self.validate()
+
+    def __eq__(self, other):
+        return (isinstance(other, ChannelCompressedBlock) and self.config == other.config
+                and self.codes == other.codes and np.array_equal(self.ranges, other.ranges))
+
+    @property
+    def count(self) -> int:
+        return len(self.codes) // self.config.codeStride
+
+    @property
+    def groupCount(self) -> int:
+        return self.config.groupCount(self.count)
+
+    def validate(self) -> None:
+        """PerChannel.swift:94-113."""
+        cs = self.config.codeStride
+        if len(self.codes) == 0 or len(self.codes) % cs != 0:
+            raise InvalidInput(f"codes is {len(self.codes)} bytes; expected a positive multiple of {cs}")
+        expected = self.groupCount * 2 * self.config.dim
+        if self.ranges.shape[0] != expected:
+            raise InvalidInput(f"ranges has {self.ranges.shape[0]} values; expected {expected} for {self.count} tokens")
+        r = self.ranges.view(np.float16).astype(np.float32).reshape(self.groupCount, 2, self.config.dim)
+        lo, hi = r[:, 0], r[:, 1]
+        bad = ~(np.isfinite(lo) & np.isfinite(hi) & (lo <= hi))
+        if bad.any():
+            g, ch = map(int, np.argwhere(bad)[0])
+            raise InvalidInput(f"group {g} channel {ch}: range [{lo[g, ch]}, {hi[g, ch]}] is invalid")
+
+    def range(self, group: int, channel: int) -> tuple[float, float]:
+        d = self.config.dim
+        return (half_to_float(self.ranges[group * 2 * d + channel]),
+                half_to_float(self.ranges[group * 2 * d + d + channel]))
+
+    def append(self, other: "ChannelCompressedBlock") -> None:
+        if other.config != self.config:
+            raise ConfigurationMismatch("cannot append a block with a different config")
+        if self.count % self.config.groupSize != 0:
+            raise InvalidInput(f"cannot append after a partial group ({self.count} tokens, group size "
+                               f"{self.config.groupSize})")
+        self.codes = self.codes + other.codes
+        self.ranges = np.concatenate([self.ranges, other.ranges])
+
+    @property
+    def payloadByteCount(self) -> int:
+        return len(self.codes)
+
+    @property
+    def sideInformationByteCount(self) -> int:
+        return self.ranges.shape[0] * 2 + self.headerByteCount
+
+    @property
+    def storedByteCount(self) -> int:
+        return self.payloadByteCount + self.sideInformationByteCount
+
+    @property
+    def originalByteCount(self) -> int:
+        return self.count * self.config.dim * 4
+
+    @property
+    def compressionRatio(self) -> float:
+        return self.originalByteCount / self.storedByteCount
+
+    @property
+    def compressionRatioVsFloat16(self) -> float:
+        return self.compressionRatio / 2
+
+    @property
+    def bitsPerCoordinate(self) -> float:
+        return self.storedByteCount * 8 / (self.count * self.config.dim)
+
+    def to_json(self) -> str:
+        return json.dumps({"formatVersion": self.formatVersion, "config": self.config.to_dict(),
+                           "codes": base64.b64encode(self.codes).decode(),
+                           "ranges": [int(r) for r in self.ranges]})
+
+    @classmethod
+    def from_json(cls, text: str) -> "ChannelCompressedBlock":
+        obj = json.loads(text)
+        if obj.get("formatVersion") != cls.formatVersion:
+            raise InvalidInput(f"Unsupported PITCH per-channel format version {obj.get('formatVersion')}; "
+                               f"expected {cls.formatVersion}")
+        c = obj["config"]
+        cfg = ChannelQuantConfig(c["dim"], c["bits"], c["groupSize"])
+        return cls(cfg, base64.b64decode(obj["codes"]), np.array(obj["ranges"], dtype=np.uint16))
+
+
+# ----------------------------------------------------------------------------------------- torch plumbing
+def _torch():
+    import torch
+    return torch
+
+
+def _buf(t, name: str):
+    """(pointer, byte length) of a contiguous device tensor used as a raw buffer."""
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise InvalidInput(f"{name} must be a torch tensor")
+    if not t.is_cuda:
+        raise InvalidInput(f"{name} buffer is not device memory")
+    if not t.is_contiguous():
+        raise InvalidInput(f"{name} buffer must be contiguous")
+    return t.data_ptr(), t.numel() * t.element_size()
+
+
+def _stream_handle(stream, device=None):
+    torch = _torch()
+    if stream is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _validate_values(x, limit: float, what: str) -> None:
+    """PITCH.validateValues (PITCH.swift:172-181) / validateChannelValues (PerChannel.swift:273-282)."""
+    torch = _torch()
+    if isinstance(x, torch.Tensor):
+        finite = bool(torch.isfinite(x).all())
+        largest = float(x.abs().max()) if finite and x.numel() else 0.0
+    else:
+        finite = bool(np.isfinite(x).all())
+        largest = float(np.abs(x).max()) if finite and x.size else 0.0
+    if not finite:
+        raise InvalidInput("input contains NaN or infinity")
+    if largest > limit:
+        raise InvalidInput(f"input magnitude {largest} exceeds {limit}; {what}")
+
+
+# ----------------------------------------------------------------------------------------- PITCH
+class PITCH:
+    """Public entry point (Sources/PITCH/PITCH.swift:15-189 and the PerChannel extension :182-290)."""
+
+    defaultSeed = DEFAULT_SEED
+    _shared: "PITCH | None" = None
+
+    def __init__(self, seed: int = DEFAULT_SEED, device=None):
+        if not (0 <= int(seed) <= 0xFFFFFFFF):
+            raise InvalidInput(f"seed {seed} must fit in 32 bits")
+        self.seed = int(seed)
+        self._lib = _lib_or_raise()
+        torch = _torch()
+        if device is None:
+            if not torch.cuda.is_available():
+                raise DeviceUnavailable("no HIP device is available")
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise DeviceUnavailable(f"{device} is not a HIP device")
+
+    @classmethod
+    def shared(cls) -> "PITCH":
+        if cls._shared is None:
+            cls._shared = cls()
+        return cls._shared
+
+    def config(self, method, dim: int, bits: int) -> QuantConfig:
+        return QuantConfig(method, dim, bits, self.seed)
+
+    def channelConfig(self, dim: int, bits: int, groupSize: int = 64) -> ChannelQuantConfig:
+        return ChannelQuantConfig(dim, bits, groupSize)
+
+    # ---- helpers
+    def _on_device(self, x, name="input"):
+        torch = _torch()
+        if isinstance(x, torch.Tensor):
+            t = x.detach()
+            if t.dtype != torch.float32:
+                raise InvalidInput(f"{name} must be float32")
+            return t.to(self.device).contiguous().reshape(-1)
+        a = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
+        return torch.from_numpy(a).to(self.device)
+
+    def _guard(self, fn, failure):
+        torch = _torch()
+        with torch.cuda.device(self.device):
+            try:
+                out = fn()
+                torch.cuda.current_stream(self.device).synchronize()
+                return out
+            except PITCHError:
+                raise
+            except RuntimeError as e:
+                raise failure(str(e)) from e
+
+    # ---- array API (PITCH.swift:68-132)
+    def encode(self, vectors, dim: int | None = None, bits: int | None = None, method=None,
+               seed: int | None = None, config: QuantConfig | None = None) -> CompressedBatch:
+        """Compresses len(vectors) / dim contiguous vectors; without dim, one vector (PITCH.swift:68-104)."""
+        torch = _torch()
+        n = int(vectors.numel()) if isinstance(vectors, torch.Tensor) else int(np.asarray(vectors).size)
+        if config is None:
+            if bits is None or method is None:
+                raise InvalidInput("encode needs a config or bits and method")
+            config = QuantConfig(method, n if dim is None else dim, bits, self.seed if seed is None else seed)
+        if n == 0 or n % config.dim != 0:
+            raise InvalidInput(f"{n} floats is not a whole number of {config.dim}-dim vectors")
+        _validate_values(vectors if isinstance(vectors, torch.Tensor) else np.asarray(vectors, dtype=np.float32),
+                         QuantConfig.maxInputMagnitude, "the kernels' float32 sum of squares would overflow")
+        count = n // config.dim
+
+        def run():
+            x = self._on_device(vectors)
+            codes = torch.empty(count * config.codeStride, dtype=torch.uint8, device=self.device)
+            scales = torch.empty(count, dtype=torch.float32, device=self.device)
+            self.enqueueEncode(x, codes, scales, count, config)
+            return codes, scales
+
+        codes, scales = self._guard(run, EncodingFailed)
+        return CompressedBatch(config, codes.cpu().numpy().tobytes(), scales.cpu().numpy(), _checked=False)
+
+    def decode(self, batch: CompressedBatch) -> np.ndarray:
+        """Reconstructs every vector of the batch, contiguously (PITCH.swift:107-115)."""
+        torch = _torch()
+        out = torch.empty(batch.count * batch.config.dim, dtype=torch.float32, device=self.device)
+        self.decode_into(batch, out, 0)
+        return out.cpu().numpy()
+
+    def decode_into(self, batch: CompressedBatch, buffer, offset: int = 0) -> None:
+        """Reconstructs the batch into a device buffer at byte offset, then waits (PITCH.swift:118-132)."""
+        torch = _torch()
+        batch.validate()
+
+        def run():
+            codes = torch.from_numpy(np.frombuffer(batch.codes, dtype=np.uint8).copy()).to(self.device)
+            scales = torch.from_numpy(batch.scales.copy()).to(self.device)
+            self.enqueueDecode(codes, scales, buffer, batch.count, batch.config, outputOffset=offset)
+
+        self._guard(run, DecodingFailed)
+
+    # ---- GPU-resident API (PITCH.swift:144-165)
+    def enqueueEncode(self, input, codes, scales, count: int, config: QuantConfig, inputOffset: int = 0,
+                      codesOffset: int = 0, scalesOffset: int = 0, stream=None) -> None:
+        """Launches encoding of count vectors; results are valid once the stream reaches this point."""
+        ip, ib = _buf(input, "input")
+        cp, cb = _buf(codes, "codes")
+        sp, sb = _buf(scales, "scales")
+        _check_offsets(inputOffset, codesOffset, scalesOffset)
+        rc = self._lib.pitch_enqueue_encode(ctypes.byref(config._c()), ip, ib, inputOffset, cp, cb, codesOffset,
+                                            sp, sb, scalesOffset, _count(count), _stream_handle(stream, self.device))
+        _raise_for(rc)
+
+    def enqueueDecode(self, codes, scales, output, count: int, config: QuantConfig, codesOffset: int = 0,
+                      scalesOffset: int = 0, outputOffset: int = 0, stream=None) -> None:
+        cp, cb = _buf(codes, "codes")
+        sp, sb = _buf(scales, "scales")
+        op, ob = _buf(output, "output")
+        _check_offsets(codesOffset, scalesOffset, outputOffset)
+        rc = self._lib.pitch_enqueue_decode(ctypes.byref(config._c()), cp, cb, codesOffset, sp, sb, scalesOffset,
+                                            op, ob, outputOffset, _count(count), _stream_handle(stream, self.device))
+        _raise_for(rc)
+
+    # ---- per-channel (PerChannel.swift:182-290)
+    def encodePerChannel(self, vectors, dim: int | None = None, bits: int | None = None, groupSize: int = 64,
+                         config: ChannelQuantConfig | None = None) -> ChannelCompressedBlock:
+        torch = _torch()
+        if config is None:
+            config = ChannelQuantConfig(dim, bits, groupSize)
+        n = int(vectors.numel()) if isinstance(vectors, torch.Tensor) else int(np.asarray(vectors).size)
+        if n == 0 or n % config.dim != 0:
+            raise InvalidInput(f"{n} floats is not a whole number of {config.dim}-dim tokens")
+        _validate_values(vectors if isinstance(vectors, torch.Tensor) else np.asarray(vectors, dtype=np.float32),
+                         ChannelQuantConfig.maxInputMagnitude, "per-channel ranges are stored in fp16")
+        count = n // config.dim
+        groups = config.groupCount(count)
+
+        def run():
+            x = self._on_device(vectors)
+            codes = torch.empty(count * config.codeStride, dtype=torch.uint8, device=self.device)
+            ranges = torch.empty(groups * config.rangeStride // 2, dtype=torch.int16, device=self.device)
+            self.enqueuePerChannelEncode(x, codes, ranges, count, config)
+            return codes, ranges
+
+        codes, ranges = self._guard(run, EncodingFailed)
+        return ChannelCompressedBlock(config, codes.cpu().numpy().tobytes(),
+                                      ranges.cpu().numpy().view(np.uint16), _checked=False)
+
+    def decodePerChannel(self, block: ChannelCompressedBlock) -> np.ndarray:
+        torch = _torch()
+        out = torch.empty(block.count * block.config.dim, dtype=torch.float32, device=self.device)
+        self.decodePerChannel_into(block, out, 0)
+        return out.cpu().numpy()
+
+    def decodePerChannel_into(self, block: ChannelCompressedBlock, buffer, offset: int = 0) -> None:
+        torch = _torch()
+        block.validate()
+
+        def run():
+            codes = torch.from_numpy(np.frombuffer(block.codes, dtype=np.uint8).copy()).to(self.device)
+            ranges = torch.from_numpy(block.ranges.view(np.int16).copy()).to(self.device)
+            self.enqueuePerChannelDecode(codes, ranges, buffer, block.count, block.config, outputOffset=offset)
+
+        self._guard(run, DecodingFailed)
+
+    def enqueuePerChannelEncode(self, input, codes, ranges, count: int, config: ChannelQuantConfig,
+                                inputOffset: int = 0, codesOffset: int = 0, rangesOffset: int = 0,
+                                stream=None) -> None:
+        ip, ib = _buf(input, "input")
+        cp, cb = _buf(codes, "codes")
+        rp, rb = _buf(ranges, "ranges")
+        _check_offsets(inputOffset, codesOffset, rangesOffset)
+        rc = self._lib.pitch_enqueue_channel_encode(ctypes.byref(config._c()), ip, ib, inputOffset, cp, cb,
+                                                    codesOffset, rp, rb, rangesOffset, _count(count),
+                                                    _stream_handle(stream, self.device))
+        _raise_for(rc)
+
+    def enqueuePerChannelDecode(self, codes, ranges, output, count: int, config: ChannelQuantConfig,
+                                codesOffset: int = 0, rangesOffset: int = 0, outputOffset: int = 0,
+                                stream=None) -> None:
+        cp, cb = _buf(codes, "codes")
+        rp, rb = _buf(ranges, "ranges")
+        op, ob = _buf(output, "output")
+        _check_offsets(codesOffset, rangesOffset, outputOffset)
+        rc = self._lib.pitch_enqueue_channel_decode(ctypes.byref(config._c()), cp, cb, codesOffset, rp, rb,
+                                                    rangesOffset, op, ob, outputOffset, _count(count),
+                                                    _stream_handle(stream, self.device))
+        _raise_for(rc)
+
+
+def _check_offsets(*offs) -> None:
+    for o in offs:
+        if not isinstance(o, (int, np.integer)) or o < 0:
+            raise InvalidInput(f"offset {o} must be a non-negative multiple of 4")
+
+
+def _count(c) -> int:
+    if not isinstance(c, (int, np.integer)) or c < 1:
+        raise InvalidInput("count must be at least 1")
+    return int(c)
+
+
+# ----------------------------------------------------------------------------------------- function mirrors
+# Function-level mirrors of reference/pitch_reference.py, on device tensors through the same kernels.
+SUPPORTED_BITS = range(2, 9)
+SUPPORTED_DIMS = [2 ** k for k in range(1, 11)]
+CHANNEL_DEFAULT_GROUP = 64
+FP16_MAX = 65504.0
+
+
+def code_stride_bytes(d: int, b: int) -> int:
+    """pitch_reference.py:65-66."""
+    return ((d * b + 7) // 8 + 3) & ~3
+
+
+def bits_per_coordinate(d: int, b: int) -> float:
+    """pitch_reference.py:134-135."""
+    return (code_stride_bytes(d, b) + 4) * 8 / d
+
+
+def channel_group_count(n: int, G: int) -> int:
+    return (n + G - 1) // G
+
+
+def channel_bits_per_coordinate(d: int, b: int, G: int = CHANNEL_DEFAULT_GROUP) -> float:
+    return code_stride_bytes(d, b) * 8 / d + 32 / G
+
+
+def pack_codes(codes, b: int, stream=None):
+    """(n, d) unpacked codes (integer tensor on the device) -> (n * codeStride,) uint8 packed codes."""
+    torch = _torch()
+    n, d = codes.shape
+    u8 = codes.to(torch.uint8).contiguous()
+    out = torch.empty(n * code_stride_bytes(d, b), dtype=torch.uint8, device=codes.device)
+    up, ub = _buf(u8, "unpacked")
+    pp, pb = _buf(out, "packed")
+    with torch.cuda.device(codes.device):
+        _raise_for(_lib_or_raise().pitch_enqueue_pack_codes(d, b, up, ub, 0, pp, pb, 0, n,
+                                                            _stream_handle(stream, codes.device)))
+    return out
+
+
+def unpack_codes(packed, n: int, d: int, b: int, stream=None):
+    """Packed codes (uint8 device tensor) -> (n, d) int64 codes."""
+    torch = _torch()
+    out = torch.empty(n * d, dtype=torch.uint8, device=packed.device)
+    pp, pb = _buf(packed.contiguous(), "packed")
+    up, ub = _buf(out, "unpacked")
+    with torch.cuda.device(packed.device):
+        _raise_for(_lib_or_raise().pitch_enqueue_unpack_codes(d, b, pp, pb, 0, up, ub, 0, n,
+                                                              _stream_handle(stream, packed.device)))
+    return out.view(n, d).to(torch.int64)
+
+
+def _pitch_for(t) -> PITCH:
+    return PITCH(device=t.device)
+
+
+def _encode_fn(method: str, X, b: int, seed: int):
+    torch = _torch()
+    n, d = X.shape
+    cfg = QuantConfig(method, d, b, seed)
+    x = X.to(torch.float32).contiguous()
+    codes = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=X.device)
+    scales = torch.empty(n, dtype=torch.float32, device=X.device)
+    with torch.cuda.device(X.device):
+        _pitch_for(X).enqueueEncode(x, codes, scales, n, cfg)
+    return unpack_codes(codes, n, d, b), scales
+
+
+def _decode_fn(method: str, codes, scales, b: int, seed: int):
+    torch = _torch()
+    n, d = codes.shape
+    cfg = QuantConfig(method, d, b, seed)
+    packed = pack_codes(codes, b)
+    out = torch.empty((n, d), dtype=torch.float32, device=codes.device)
+    with torch.cuda.device(codes.device):
+        _pitch_for(codes).enqueueDecode(packed, scales.to(torch.float32).contiguous(), out, n, cfg)
+    return out
+
+
+def turbo_encode(X, b: int, seed: int = DEFAULT_SEED):
+    """(codes (n, d) int64, norms (n,) float32) (pitch_reference.py:92-102)."""
+    return _encode_fn("turboQuant", X, b, seed)
+
+
+def turbo_decode(codes, norms, b: int, seed: int = DEFAULT_SEED):
+    """pitch_reference.py:104-107."""
+    return _decode_fn("turboQuant", codes, norms, b, seed)
+
+
+def polar_encode(X, b: int, seed: int = DEFAULT_SEED):
+    """(codes (n, d) int64, rmax (n,) float32) (pitch_reference.py:109-121)."""
+    return _encode_fn("polarQuant", X, b, seed)
+
+
+def polar_decode(codes, rmax, b: int, seed: int = DEFAULT_SEED):
+    """pitch_reference.py:123-129."""
+    return _decode_fn("polarQuant", codes, rmax, b, seed)
+
+
+ENCODERS = {"turboQuant": turbo_encode, "polarQuant": polar_encode}
+DECODERS = {"turboQuant": turbo_decode, "polarQuant": polar_decode}
+
+
+def channel_encode(X, b: int, G: int = CHANNEL_DEFAULT_GROUP):
+    """(codes (n, d) int64, ranges (groups, 2, d) float16) (pitch_reference.py:145-162)."""
+    torch = _torch()
+    n, d = X.shape
+    cfg = ChannelQuantConfig(d, b, G)
+    _validate_values(X, FP16_MAX, "per-channel ranges are stored in fp16")
+    x = X.to(torch.float32).contiguous()
+    codes = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=X.device)
+    ranges = torch.empty(cfg.groupCount(n) * 2 * d, dtype=torch.float16, device=X.device)
+    with torch.cuda.device(X.device):
+        _pitch_for(X).enqueuePerChannelEncode(x, codes, ranges, n, cfg)
+    return unpack_codes(codes, n, d, b), ranges.view(cfg.groupCount(n), 2, d)
+
+
+def channel_decode(codes, ranges, b: int, G: int = CHANNEL_DEFAULT_GROUP):
+    """pitch_reference.py:165-174."""
+    torch = _torch()
+    n, d = codes.shape
+    cfg = ChannelQuantConfig(d, b, G)
+    packed = pack_codes(codes, b)
+    out = torch.empty((n, d), dtype=torch.float32, device=codes.device)
+    with torch.cuda.device(codes.device):
+        _pitch_for(codes).enqueuePerChannelDecode(packed, ranges.to(torch.float16).contiguous(), out, n, cfg)
+    return out
+
+
+def rand_signs(seed: int, d: int):
+    """+1 / -1 rotation signs (pitch_reference.py:17-19), host-side integer arithmetic as in the kernels."""
+    i = (np.uint64(seed) + np.arange(d, dtype=np.uint64)) & np.uint64(0xFFFFFFFF)
+    state = (i * np.uint64(747796405) + np.uint64(2891336453)) & np.uint64(0xFFFFFFFF)
+    word = (((state >> ((state >> np.uint64(28)) + np.uint64(4))) ^ state) * np.uint64(277803737)) \
+        & np.uint64(0xFFFFFFFF)
+    h = ((word >> np.uint64(22)) ^ word) & np.uint64(0xFFFFFFFF)
+    return np.where(h & np.uint64(1), 1.0, -1.0)
+

@@ -1,0 +1,373 @@
+// C ABI of libpitch_amd.so: argument validation and kernel dispatch (declared in include/pitch_amd.h).
+//
+// Validation mirrors the reference's launch contract before any GPU work is issued:
+//   QuantConfig.init (Sources/PITCH/Models/QuantConfig.swift:24-35), ChannelQuantConfig.init
+//   (Sources/PITCH/PerChannel.swift:30-43), Codec.params/check (Sources/PITCH/Core/Codec.swift:28-47) and
+//   ChannelCodec.params/check (Sources/PITCH/PerChannel.swift:309-328).
+// The reference's 32-bit limit on count * dim is lifted (64-bit counts and offsets).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/pitch_amd.h"
+#include "pitch_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return PITCH_OK;
+}
+
+bool is_pow2(uint32_t x) { return x != 0 && (x & (x - 1)) == 0; }
+
+int validate_config(const pitch_config_t* c) {
+  if (!c) return fail(PITCH_ERR_INVALID_INPUT, "config is null");
+  if (c->method != PITCH_METHOD_TURBO && c->method != PITCH_METHOD_POLAR)
+    return fail(PITCH_ERR_INVALID_INPUT, "unknown method %u", c->method);
+  if (c->dim < 2 || c->dim > 1024 || !is_pow2(c->dim))
+    return fail(PITCH_ERR_INVALID_DIMENSION, "Invalid dimension %u. Must be a power of two in [2, 1024].", c->dim);
+  if (c->bits < 2 || c->bits > 8)
+    return fail(PITCH_ERR_INVALID_BIT_WIDTH, "Invalid bit width %u. Must be in 2...8.", c->bits);
+  return PITCH_OK;
+}
+
+int validate_channel_config(const pitch_channel_config_t* c) {
+  if (!c) return fail(PITCH_ERR_INVALID_INPUT, "config is null");
+  if (c->dim < 1 || c->dim > 1024)
+    return fail(PITCH_ERR_INVALID_INPUT, "per-channel dimension %u must be in 1...1024", c->dim);
+  if (c->bits < 2 || c->bits > 8)
+    return fail(PITCH_ERR_INVALID_BIT_WIDTH, "Invalid bit width %u. Must be in 2...8.", c->bits);
+  if (c->group_size < 1 || c->group_size > 65536)
+    return fail(PITCH_ERR_INVALID_INPUT, "group size %u must be in 1...65536", c->group_size);
+  return PITCH_OK;
+}
+
+uint32_t code_stride_of(uint32_t dim, uint32_t bits) { return (dim * bits + 31u) / 32u * 4u; }
+
+// Offset alignment and "needs N bytes after offset" (Codec.swift:37-47).
+int check_buffer(const void* ptr, uint64_t bytes, uint64_t off, uint64_t need, const char* name) {
+  if (!ptr) return fail(PITCH_ERR_INVALID_INPUT, "%s buffer is null", name);
+  if (off % 4 != 0)
+    return fail(PITCH_ERR_INVALID_INPUT, "%s offset %llu must be a non-negative multiple of 4", name,
+                (unsigned long long)off);
+  if (bytes < off || bytes - off < need)
+    return fail(PITCH_ERR_INVALID_INPUT, "%s buffer has %lld bytes after offset; needs %llu", name,
+                (long long)bytes - (long long)off, (unsigned long long)need);
+  return PITCH_OK;
+}
+
+// The buffer must be memory of the current device (Codec.swift:38-40 checks buffer.device).
+int check_device(const void* ptr, int dev, const char* name) {
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(PITCH_ERR_INVALID_INPUT, "%s buffer is not device memory", name);
+  }
+  if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged && !attr.isManaged)
+    return fail(PITCH_ERR_INVALID_INPUT, "%s buffer is not device memory", name);
+  if (attr.type == hipMemoryTypeDevice && attr.device != dev)
+    return fail(PITCH_ERR_INVALID_INPUT, "%s buffer belongs to device %d, not the current device %d", name,
+                attr.device, dev);
+  return PITCH_OK;
+}
+
+int current_device(int* dev) {
+  if (hipGetDevice(dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "no HIP device is available");
+  }
+  return PITCH_OK;
+}
+
+bool mul_overflows(uint64_t a, uint64_t b) { return b != 0 && a > UINT64_MAX / b; }
+
+#define PITCH_TRY(expr)       \
+  do {                        \
+    const int rc_ = (expr);   \
+    if (rc_ != PITCH_OK) return rc_; \
+  } while (0)
+
+template <typename T>
+T* at(const void* base, uint64_t off) {
+  return (T*)((const char*)base + off);
+}
+
+hipError_t launch_vec(uint32_t dim, bool encode, bool polar, int bits, const pitch::VecArgs& a, hipStream_t s) {
+  switch (dim) {
+    case 2: return pitch::launch_vec_d2(encode, polar, bits, a, s);
+    case 4: return pitch::launch_vec_d4(encode, polar, bits, a, s);
+    case 8: return pitch::launch_vec_d8(encode, polar, bits, a, s);
+    case 16: return pitch::launch_vec_d16(encode, polar, bits, a, s);
+    case 32: return pitch::launch_vec_d32(encode, polar, bits, a, s);
+    case 64: return pitch::launch_vec_d64(encode, polar, bits, a, s);
+    case 128: return pitch::launch_vec_d128(encode, polar, bits, a, s);
+    case 256: return pitch::launch_vec_d256(encode, polar, bits, a, s);
+    case 512: return pitch::launch_vec_d512(encode, polar, bits, a, s);
+    case 1024: return pitch::launch_vec_d1024(encode, polar, bits, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+namespace pitch {
+
+int device_cu_count() {
+  static std::mutex mu;
+  static std::unordered_map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 1;
+  cache[dev] = n;
+  return n;
+}
+
+uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, int> occ_cache;
+  // PITCH_BLOCKS_PER_CU overrides the resident-block count per CU (tuning aid); 0 or unset = occupancy.
+  static const int override_per_cu = [] {
+    const char* e = std::getenv("PITCH_BLOCKS_PER_CU");
+    return e ? std::atoi(e) : 0;
+  }();
+  int occ = 0;
+  if (override_per_cu > 0) {
+    occ = override_per_cu;
+  } else {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = occ_cache.find(kernel);
+    if (it != occ_cache.end()) {
+      occ = it->second;
+    } else {
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) != hipSuccess || occ < 1) occ = 1;
+      occ_cache[kernel] = occ;
+    }
+  }
+  const uint64_t cap = (uint64_t)device_cu_count() * (uint64_t)occ;
+  uint64_t g = blocks_needed < cap ? blocks_needed : cap;
+  return g < 1 ? 1 : g;
+}
+
+}  // namespace pitch
+
+extern "C" {
+
+uint32_t pitch_version(void) { return 0x000100u; }
+
+const char* pitch_last_error(void) { return g_last_error.c_str(); }
+
+int pitch_config(uint32_t method, uint32_t dim, uint32_t bits, uint32_t seed, pitch_config_t* out,
+                 uint32_t* code_stride) {
+  const pitch_config_t c{method, dim, bits, seed};
+  PITCH_TRY(validate_config(&c));
+  if (out) *out = c;
+  if (code_stride) *code_stride = code_stride_of(dim, bits);
+  return ok();
+}
+
+int pitch_channel_config(uint32_t dim, uint32_t bits, uint32_t group_size, pitch_channel_config_t* out,
+                         uint32_t* code_stride, uint32_t* range_stride) {
+  const pitch_channel_config_t c{dim, bits, group_size, 0u};
+  PITCH_TRY(validate_channel_config(&c));
+  if (out) *out = c;
+  if (code_stride) *code_stride = code_stride_of(dim, bits);
+  if (range_stride) *range_stride = 4u * dim;
+  return ok();
+}
+
+int pitch_enqueue_encode(const pitch_config_t* config, const void* input, uint64_t input_bytes,
+                         uint64_t input_offset, void* codes, uint64_t codes_bytes, uint64_t codes_offset,
+                         void* scales, uint64_t scales_bytes, uint64_t scales_offset, uint64_t count,
+                         void* stream) {
+  PITCH_TRY(validate_config(config));
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (mul_overflows(count, (uint64_t)dim * 4u)) return fail(PITCH_ERR_INVALID_INPUT, "count is too large");
+  PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * 4u, "input"));
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
+  PITCH_TRY(check_buffer(scales, scales_bytes, scales_offset, count * 4u, "scales"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(input, dev, "input"));
+  PITCH_TRY(check_device(codes, dev, "codes"));
+  PITCH_TRY(check_device(scales, dev, "scales"));
+  pitch::VecArgs a{};
+  a.in = at<const float>(input, input_offset);
+  a.codes_out = at<uint32_t>(codes, codes_offset);
+  a.scales_out = at<float>(scales, scales_offset);
+  a.count = count;
+  a.seed = config->seed;
+  const hipError_t e = launch_vec(dim, true, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
+                                  (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int pitch_enqueue_decode(const pitch_config_t* config, const void* codes, uint64_t codes_bytes,
+                         uint64_t codes_offset, const void* scales, uint64_t scales_bytes,
+                         uint64_t scales_offset, void* output, uint64_t output_bytes, uint64_t output_offset,
+                         uint64_t count, void* stream) {
+  PITCH_TRY(validate_config(config));
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (mul_overflows(count, (uint64_t)dim * 4u)) return fail(PITCH_ERR_INVALID_INPUT, "count is too large");
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
+  PITCH_TRY(check_buffer(scales, scales_bytes, scales_offset, count * 4u, "scales"));
+  PITCH_TRY(check_buffer(output, output_bytes, output_offset, count * dim * 4u, "output"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(codes, dev, "codes"));
+  PITCH_TRY(check_device(scales, dev, "scales"));
+  PITCH_TRY(check_device(output, dev, "output"));
+  pitch::VecArgs a{};
+  a.codes_in = at<const uint32_t>(codes, codes_offset);
+  a.scales_in = at<const float>(scales, scales_offset);
+  a.out = at<float>(output, output_offset);
+  a.count = count;
+  a.seed = config->seed;
+  const hipError_t e = launch_vec(dim, false, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
+                                  (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int pitch_enqueue_channel_encode(const pitch_channel_config_t* config, const void* input,
+                                 uint64_t input_bytes, uint64_t input_offset, void* codes,
+                                 uint64_t codes_bytes, uint64_t codes_offset, void* ranges,
+                                 uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count,
+                                 void* stream) {
+  PITCH_TRY(validate_channel_config(config));
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (count > 0xFFFFFFFFull) return fail(PITCH_ERR_INVALID_INPUT, "per-channel count must be below 2^32 tokens");
+  const uint64_t groups = (count + config->group_size - 1) / config->group_size;
+  PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * 4u, "input"));
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
+  PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(input, dev, "input"));
+  PITCH_TRY(check_device(codes, dev, "codes"));
+  PITCH_TRY(check_device(ranges, dev, "ranges"));
+  pitch::ChanArgs a{};
+  a.in = at<const float>(input, input_offset);
+  a.codes_out = at<uint32_t>(codes, codes_offset);
+  a.ranges_out = at<uint16_t>(ranges, ranges_offset);
+  a.count = (uint32_t)count;
+  a.dim = dim;
+  a.group = config->group_size;
+  a.nwords = cs / 4u;
+  const hipError_t e = pitch::launch_channel(true, (int)config->bits, a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int pitch_enqueue_channel_decode(const pitch_channel_config_t* config, const void* codes,
+                                 uint64_t codes_bytes, uint64_t codes_offset, const void* ranges,
+                                 uint64_t ranges_bytes, uint64_t ranges_offset, void* output,
+                                 uint64_t output_bytes, uint64_t output_offset, uint64_t count,
+                                 void* stream) {
+  PITCH_TRY(validate_channel_config(config));
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (count > 0xFFFFFFFFull) return fail(PITCH_ERR_INVALID_INPUT, "per-channel count must be below 2^32 tokens");
+  const uint64_t groups = (count + config->group_size - 1) / config->group_size;
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
+  PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
+  PITCH_TRY(check_buffer(output, output_bytes, output_offset, count * dim * 4u, "output"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(codes, dev, "codes"));
+  PITCH_TRY(check_device(ranges, dev, "ranges"));
+  PITCH_TRY(check_device(output, dev, "output"));
+  pitch::ChanArgs a{};
+  a.codes_in = at<const uint32_t>(codes, codes_offset);
+  a.ranges_in = at<const uint16_t>(ranges, ranges_offset);
+  a.out = at<float>(output, output_offset);
+  a.count = (uint32_t)count;
+  a.dim = dim;
+  a.group = config->group_size;
+  a.nwords = cs / 4u;
+  const hipError_t e = pitch::launch_channel(false, (int)config->bits, a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+static int pack_common(bool pack, uint32_t dim, uint32_t bits, const void* src, uint64_t src_bytes,
+                       uint64_t src_off, void* dst, uint64_t dst_bytes, uint64_t dst_off, uint64_t count,
+                       void* stream) {
+  if (dim < 1 || dim > 1024) return fail(PITCH_ERR_INVALID_DIMENSION, "dimension %u must be in 1...1024", dim);
+  if (bits < 2 || bits > 8) return fail(PITCH_ERR_INVALID_BIT_WIDTH, "Invalid bit width %u. Must be in 2...8.", bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (mul_overflows(count, 4096u)) return fail(PITCH_ERR_INVALID_INPUT, "count is too large");
+  const uint64_t packed = count * code_stride_of(dim, bits), unpacked = count * dim;
+  if (pack) {
+    PITCH_TRY(check_buffer(src, src_bytes, 0, 0, "unpacked"));
+    if (src_bytes < src_off || src_bytes - src_off < unpacked)
+      return fail(PITCH_ERR_INVALID_INPUT, "unpacked buffer needs %llu bytes after offset", (unsigned long long)unpacked);
+    PITCH_TRY(check_buffer(dst, dst_bytes, dst_off, packed, "packed"));
+  } else {
+    PITCH_TRY(check_buffer(src, src_bytes, src_off, packed, "packed"));
+    if (!dst) return fail(PITCH_ERR_INVALID_INPUT, "unpacked buffer is null");
+    if (dst_bytes < dst_off || dst_bytes - dst_off < unpacked)
+      return fail(PITCH_ERR_INVALID_INPUT, "unpacked buffer needs %llu bytes after offset", (unsigned long long)unpacked);
+  }
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(src, dev, pack ? "unpacked" : "packed"));
+  PITCH_TRY(check_device(dst, dev, pack ? "packed" : "unpacked"));
+  pitch::PackArgs a{};
+  a.count = count;
+  a.dim = dim;
+  a.bits = bits;
+  if (pack) {
+    a.unpacked_in = at<const uint8_t>(src, src_off);
+    a.packed_out = at<uint32_t>(dst, dst_off);
+  } else {
+    a.packed_in = at<const uint32_t>(src, src_off);
+    a.unpacked_out = at<uint8_t>(dst, dst_off);
+  }
+  const hipError_t e = pitch::launch_pack(pack, a, (hipStream_t)stream);
+  if (e != hipSuccess)
+    return fail(pack ? PITCH_ERR_ENCODING_FAILED : PITCH_ERR_DECODING_FAILED, "%s failed: %s",
+                pack ? "pack" : "unpack", hipGetErrorString(e));
+  return ok();
+}
+
+int pitch_enqueue_pack_codes(uint32_t dim, uint32_t bits, const void* unpacked, uint64_t unpacked_bytes,
+                             uint64_t unpacked_offset, void* packed, uint64_t packed_bytes,
+                             uint64_t packed_offset, uint64_t count, void* stream) {
+  return pack_common(true, dim, bits, unpacked, unpacked_bytes, unpacked_offset, packed, packed_bytes,
+                     packed_offset, count, stream);
+}
+
+int pitch_enqueue_unpack_codes(uint32_t dim, uint32_t bits, const void* packed, uint64_t packed_bytes,
+                               uint64_t packed_offset, void* unpacked, uint64_t unpacked_bytes,
+                               uint64_t unpacked_offset, uint64_t count, void* stream) {
+  return pack_common(false, dim, bits, packed, packed_bytes, packed_offset, unpacked, unpacked_bytes,
+                     unpacked_offset, count, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,359 @@
+// Per-channel (KIVI-style) key encode/decode.
+//
+// Semantics follow reference/pitch_reference.py:145-174 bit for bit: per group of G tokens and per channel,
+// float32 min and max rounded to fp16 (round to nearest even), step = (f32(hi16) - f32(lo16)) / (2^b - 1)
+// with 0 -> 1, code = clip(floor((x - lo) / step + 0.5), 0, 2^b - 1), all in float32 with correctly
+// rounded division; decode x = f32(code) * step + lo as two roundings (no fused multiply-add; the library
+// is built with -ffp-contract=off). The Metal kernels they replace (PITCHKernels.metal:262-325) read each
+// group twice and pack one token per barrier; here a workgroup loads a group once, keeps up to kMaxR
+// tokens per thread in registers between the range pass and the quantise pass, and packs codes from LDS.
+#include <hip/hip_fp16.h>
+
+#include "pitch_device.h"
+
+namespace pitch {
+namespace {
+
+constexpr int kMaxR = 8;           // tokens per thread held in registers between the two passes
+constexpr int kStageBytes = 8192;  // LDS staging for one tile of codes (one byte per code)
+constexpr int kDecR = 4;           // tokens per thread per decode iteration
+
+__device__ __forceinline__ uint16_t f2h_bits(float x) { return __half_as_ushort(__float2half_rn(x)); }
+__device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_as_half(b)); }
+
+__device__ __forceinline__ float kivi_step(float lo, float hi, float levels) {
+  const float s = (hi - lo) / levels;
+  return s == 0.0f ? 1.0f : s;
+}
+
+__device__ __forceinline__ uint32_t kivi_code(float x, float base, float step, float levels) {
+  const float q = floorf((x - base) / step + 0.5f);
+  return (uint32_t)fminf(fmaxf(q, 0.0f), levels);
+}
+
+// Packs token rows of `dim` one-byte codes (stage[tok * dim + i]) into words. Word wi of a row holds the
+// bits [32*wi, 32*wi + 32) of the row's code stream (reference/pitch_reference.py:68-78).
+template <int B>
+__device__ __forceinline__ void pack_rows(const uint8_t* stage, uint32_t ntok, uint32_t dim, uint32_t nwords,
+                                          uint32_t* dst) {
+  if ((dim & 31u) == 0u) {
+    // rows split into groups of 32 codes that pack into exactly B words each
+    const uint32_t gpr = dim >> 5;
+    const uint32_t ng = ntok * gpr;
+    for (uint32_t g = threadIdx.x; g < ng; g += kBlock) {
+      const uint32_t tok = g / gpr, gi = g - tok * gpr;
+      const uint4* q = (const uint4*)(stage + tok * dim + 32u * gi);
+      const uint4 q0 = q[0], q1 = q[1];
+      const uint32_t bytes[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      uint32_t w[B];
+      pack32<B>(bytes, w);
+      store_words<B>(dst + (uint64_t)tok * nwords + gi * B, w);
+    }
+  } else {
+    const uint32_t nw = ntok * nwords;
+    for (uint32_t w = threadIdx.x; w < nw; w += kBlock) {
+      const uint32_t tok = w / nwords, wi = w - tok * nwords;
+      const uint8_t* row = stage + tok * dim;
+      uint32_t word = 0u;
+      for (uint32_t i = (32u * wi) / B; i < dim; ++i) {
+        const int s = (int)(i * B) - (int)(32u * wi);
+        if (s >= 32) break;
+        const uint32_t c = row[i];
+        word |= s >= 0 ? (c << s) : (c >> (-s));
+      }
+      dst[(uint64_t)tok * nwords + wi] = word;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------- encode
+// dim % 4 == 0: thread (phase pp, column chunk col) owns channels [4col, 4col+4) of tokens pp, pp+P, ...
+template <int B>
+__global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
+  const float levels = (float)((1 << B) - 1);
+  __shared__ float4 s_lo[kBlock], s_hi[kBlock];
+  __shared__ float s_base[1024], s_step[1024];
+  __shared__ __attribute__((aligned(16))) uint8_t s_stage[kStageBytes];
+
+  const uint32_t dim = p.dim, C = dim >> 2, P = kBlock / C;
+  const uint32_t tid = threadIdx.x, pp = tid / C, col = tid - pp * C;
+  const bool active = pp < P;
+  const uint32_t TT = min(P * kMaxR, (uint32_t)kStageBytes / dim);  // tokens per packing tile
+  const uint32_t groups = (p.count + p.group - 1) / p.group;
+
+  for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
+    const uint32_t first = g * p.group;
+    const uint32_t n = min(p.group, p.count - first);
+    const float* src = p.in + (uint64_t)first * dim + 4u * col;
+
+    // pass 1: channel minima and maxima over the group
+    float4 lo = make_float4(__builtin_inff(), __builtin_inff(), __builtin_inff(), __builtin_inff());
+    float4 hi = make_float4(-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff());
+    float4 cache[kMaxR];
+#pragma unroll
+    for (int i = 0; i < kMaxR; ++i) {
+      const uint32_t tk = pp + i * P;
+      if (active && tk < n) {
+        const f32x4 x = *(const f32x4*)(src + (uint64_t)tk * dim);
+        cache[i] = make_float4(x.x, x.y, x.z, x.w);
+        lo = make_float4(fminf(lo.x, x.x), fminf(lo.y, x.y), fminf(lo.z, x.z), fminf(lo.w, x.w));
+        hi = make_float4(fmaxf(hi.x, x.x), fmaxf(hi.y, x.y), fmaxf(hi.z, x.z), fmaxf(hi.w, x.w));
+      }
+    }
+    for (uint32_t tk = pp + kMaxR * P; active && tk < n; tk += P) {
+      const f32x4 x = *(const f32x4*)(src + (uint64_t)tk * dim);
+      lo = make_float4(fminf(lo.x, x.x), fminf(lo.y, x.y), fminf(lo.z, x.z), fminf(lo.w, x.w));
+      hi = make_float4(fmaxf(hi.x, x.x), fmaxf(hi.y, x.y), fmaxf(hi.z, x.z), fmaxf(hi.w, x.w));
+    }
+    s_lo[tid] = lo;
+    s_hi[tid] = hi;
+    __syncthreads();
+    if (tid < C) {
+      float4 l = s_lo[tid], h = s_hi[tid];
+      for (uint32_t q = 1; q < P; ++q) {
+        const float4 a = s_lo[q * C + tid], b = s_hi[q * C + tid];
+        l = make_float4(fminf(l.x, a.x), fminf(l.y, a.y), fminf(l.z, a.z), fminf(l.w, a.w));
+        h = make_float4(fmaxf(h.x, b.x), fmaxf(h.y, b.y), fmaxf(h.z, b.z), fmaxf(h.w, b.w));
+      }
+      const float lv[4] = {l.x, l.y, l.z, l.w}, hv[4] = {h.x, h.y, h.z, h.w};
+      uint16_t l16[4], h16[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        l16[r] = f2h_bits(lv[r]);
+        h16[r] = f2h_bits(hv[r]);
+        const float b0 = h2f(l16[r]);
+        s_base[4 * tid + r] = b0;
+        s_step[4 * tid + r] = kivi_step(b0, h2f(h16[r]), levels);
+      }
+      uint16_t* rg = p.ranges_out + (uint64_t)g * 2u * dim + 4u * tid;
+      *(u32x2*)rg = u32x2{(uint32_t)l16[0] | ((uint32_t)l16[1] << 16), (uint32_t)l16[2] | ((uint32_t)l16[3] << 16)};
+      *(u32x2*)(rg + dim) =
+          u32x2{(uint32_t)h16[0] | ((uint32_t)h16[1] << 16), (uint32_t)h16[2] | ((uint32_t)h16[3] << 16)};
+    }
+    __syncthreads();
+
+    // pass 2: quantise tile by tile, stage one byte per code, pack rows
+    float bs[4] = {0.f, 0.f, 0.f, 0.f}, st[4] = {1.f, 1.f, 1.f, 1.f};
+    if (active) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { bs[r] = s_base[4 * col + r]; st[r] = s_step[4 * col + r]; }
+    }
+    for (uint32_t tb = 0; tb < n; tb += TT) {
+      const uint32_t nt = min(TT, n - tb);
+      for (uint32_t i = 0; i * P < nt; ++i) {
+        const uint32_t tk = tb + pp + i * P;
+        if (active && tk < tb + nt) {
+          float4 x;
+          bool cached = false;
+#pragma unroll
+          for (int j = 0; j < kMaxR; ++j) {
+            if (tb == 0 && (uint32_t)j == i) { x = cache[j]; cached = true; }
+          }
+          if (!cached) {
+            const f32x4 y = *(const f32x4*)(src + (uint64_t)tk * dim);
+            x = make_float4(y.x, y.y, y.z, y.w);
+          }
+          const uint32_t c = kivi_code(x.x, bs[0], st[0], levels) | (kivi_code(x.y, bs[1], st[1], levels) << 8) |
+                             (kivi_code(x.z, bs[2], st[2], levels) << 16) |
+                             (kivi_code(x.w, bs[3], st[3], levels) << 24);
+          *(uint32_t*)(s_stage + (tk - tb) * dim + 4u * col) = c;
+        }
+      }
+      __syncthreads();
+      pack_rows<B>(s_stage, nt, dim, p.nwords, p.codes_out + (uint64_t)(first + tb) * p.nwords);
+      __syncthreads();
+    }
+  }
+}
+
+// dim % 4 != 0: one channel per thread for the ranges, one code per thread for quantisation
+template <int B>
+__global__ __launch_bounds__(kBlock) void chan_encode1(ChanArgs p) {
+  const float levels = (float)((1 << B) - 1);
+  __shared__ float s_base[1024], s_step[1024];
+  __shared__ __attribute__((aligned(16))) uint8_t s_stage[kStageBytes];
+  const uint32_t dim = p.dim, tid = threadIdx.x;
+  const uint32_t TT = max(1u, (uint32_t)kStageBytes / dim);
+  const uint32_t groups = (p.count + p.group - 1) / p.group;
+  for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
+    const uint32_t first = g * p.group;
+    const uint32_t n = min(p.group, p.count - first);
+    const float* src = p.in + (uint64_t)first * dim;
+    for (uint32_t ch = tid; ch < dim; ch += kBlock) {
+      float lo = __builtin_inff(), hi = -__builtin_inff();
+      for (uint32_t tk = 0; tk < n; ++tk) {
+        const float x = src[(uint64_t)tk * dim + ch];
+        lo = fminf(lo, x);
+        hi = fmaxf(hi, x);
+      }
+      const uint16_t l16 = f2h_bits(lo), h16 = f2h_bits(hi);
+      p.ranges_out[(uint64_t)g * 2u * dim + ch] = l16;
+      p.ranges_out[(uint64_t)g * 2u * dim + dim + ch] = h16;
+      s_base[ch] = h2f(l16);
+      s_step[ch] = kivi_step(h2f(l16), h2f(h16), levels);
+    }
+    __syncthreads();
+    for (uint32_t tb = 0; tb < n; tb += TT) {
+      const uint32_t nt = min(TT, n - tb);
+      for (uint32_t it = tid; it < nt * dim; it += kBlock) {
+        const uint32_t tok = it / dim, ch = it - tok * dim;
+        s_stage[it] = (uint8_t)kivi_code(src[(uint64_t)(tb + tok) * dim + ch], s_base[ch], s_step[ch], levels);
+      }
+      __syncthreads();
+      pack_rows<B>(s_stage, nt, dim, p.nwords, p.codes_out + (uint64_t)(first + tb) * p.nwords);
+      __syncthreads();
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------- decode
+template <int B>
+__global__ __launch_bounds__(kBlock) void chan_decode4(ChanArgs p) {
+  const float levels = (float)((1 << B) - 1);
+  constexpr uint32_t kMask = (1u << B) - 1u;
+  const uint32_t dim = p.dim, C = dim >> 2, P = kBlock / C;
+  const uint32_t tid = threadIdx.x, pp = tid / C, col = tid - pp * C;
+  if (pp >= P) return;  // no barriers below
+  const uint32_t TT = P * kDecR;
+  const uint32_t pos = 4u * B * col, wi = pos >> 5, sh = pos & 31u;
+  const bool straddle = sh + 4u * B > 32u;
+
+  uint32_t gcur = 0xFFFFFFFFu;
+  uint64_t gend = 0;
+  float bs[4], st[4];
+  for (uint64_t tb = (uint64_t)blockIdx.x * TT; tb < p.count; tb += (uint64_t)gridDim.x * TT) {
+#pragma unroll
+    for (int i = 0; i < kDecR; ++i) {
+      const uint64_t tk = tb + pp + (uint64_t)i * P;
+      if (tk < p.count) {
+        if (gcur == 0xFFFFFFFFu || tk >= gend || tk + p.group < gend) {
+          gcur = (uint32_t)(tk / p.group);
+          gend = (uint64_t)(gcur + 1) * p.group;
+          const uint16_t* rg = p.ranges_in + (uint64_t)gcur * 2u * dim + 4u * col;
+          const u32x2 l = *(const u32x2*)rg, h = *(const u32x2*)(rg + dim);
+          const uint16_t l16[4] = {(uint16_t)l.x, (uint16_t)(l.x >> 16), (uint16_t)l.y, (uint16_t)(l.y >> 16)};
+          const uint16_t h16[4] = {(uint16_t)h.x, (uint16_t)(h.x >> 16), (uint16_t)h.y, (uint16_t)(h.y >> 16)};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            bs[r] = h2f(l16[r]);
+            st[r] = kivi_step(bs[r], h2f(h16[r]), levels);
+          }
+        }
+        const uint32_t* cw = p.codes_in + tk * p.nwords;
+        const uint32_t lo = cw[wi];
+        const uint32_t hi = straddle ? cw[wi + 1] : 0u;
+        const uint32_t bits = __builtin_amdgcn_alignbit(hi, lo, sh);
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (float)((bits >> (B * r)) & kMask) * st[r] + bs[r];
+        *(f32x4*)(p.out + tk * dim + 4u * col) = f32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+}
+
+template <int B>
+__global__ __launch_bounds__(kBlock) void chan_decode1(ChanArgs p) {
+  const float levels = (float)((1 << B) - 1);
+  constexpr uint32_t kMask = (1u << B) - 1u;
+  const uint64_t total = (uint64_t)p.count * p.dim;
+  for (uint64_t idx = (uint64_t)blockIdx.x * kBlock + threadIdx.x; idx < total;
+       idx += (uint64_t)gridDim.x * kBlock) {
+    const uint64_t tok = idx / p.dim;
+    const uint32_t ch = (uint32_t)(idx - tok * p.dim);
+    const uint64_t g = tok / p.group;
+    const float base = h2f(p.ranges_in[g * 2u * p.dim + ch]);
+    const float step = kivi_step(base, h2f(p.ranges_in[g * 2u * p.dim + p.dim + ch]), levels);
+    const uint32_t* cw = p.codes_in + tok * p.nwords;
+    const uint32_t pos = ch * B, wi = pos >> 5, sh = pos & 31u;
+    const uint32_t lo = cw[wi], hi = (sh + B > 32u) ? cw[wi + 1] : 0u;
+    const uint32_t code = __builtin_amdgcn_alignbit(hi, lo, sh) & kMask;
+    p.out[idx] = (float)code * step + base;
+  }
+}
+
+template <int B>
+hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
+  const bool vec4 = (a.dim & 3u) == 0u;
+  if (encode) {
+    const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;
+    const void* k = vec4 ? (const void*)&chan_encode4<B> : (const void*)&chan_encode1<B>;
+    const uint64_t grid = persistent_grid(k, groups);
+    if (vec4) hipLaunchKernelGGL((chan_encode4<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    else hipLaunchKernelGGL((chan_encode1<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+  } else if (vec4) {
+    const uint32_t P = kBlock / (a.dim >> 2);
+    const uint64_t need = ((uint64_t)a.count + P * kDecR - 1) / (P * kDecR);
+    const uint64_t grid = persistent_grid((const void*)&chan_decode4<B>, need);
+    hipLaunchKernelGGL((chan_decode4<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+  } else {
+    const uint64_t need = ((uint64_t)a.count * a.dim + kBlock - 1) / kBlock;
+    const uint64_t grid = persistent_grid((const void*)&chan_decode1<B>, need);
+    hipLaunchKernelGGL((chan_decode1<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------- pack
+__global__ __launch_bounds__(kBlock) void pack_generic(PackArgs p) {
+  const uint32_t nwords = (p.dim * p.bits + 31u) / 32u;
+  const uint64_t total = p.count * nwords;
+  for (uint64_t w = (uint64_t)blockIdx.x * kBlock + threadIdx.x; w < total; w += (uint64_t)gridDim.x * kBlock) {
+    const uint64_t row = w / nwords;
+    const uint32_t wi = (uint32_t)(w - row * nwords);
+    const uint8_t* src = p.unpacked_in + row * p.dim;
+    const uint32_t mask = (1u << p.bits) - 1u;
+    uint32_t word = 0u;
+    for (uint32_t i = (32u * wi) / p.bits; i < p.dim; ++i) {
+      const int s = (int)(i * p.bits) - (int)(32u * wi);
+      if (s >= 32) break;
+      const uint32_t c = src[i] & mask;
+      word |= s >= 0 ? (c << s) : (c >> (-s));
+    }
+    p.packed_out[w] = word;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void unpack_generic(PackArgs p) {
+  const uint32_t nwords = (p.dim * p.bits + 31u) / 32u;
+  const uint64_t total = p.count * p.dim;
+  const uint32_t mask = (1u << p.bits) - 1u;
+  for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (uint64_t)gridDim.x * kBlock) {
+    const uint64_t row = i / p.dim;
+    const uint32_t c = (uint32_t)(i - row * p.dim);
+    const uint32_t* w = p.packed_in + row * nwords;
+    const uint32_t pos = c * p.bits, wi = pos >> 5, sh = pos & 31u;
+    const uint32_t lo = w[wi], hi = (sh + p.bits > 32u) ? w[wi + 1] : 0u;
+    p.unpacked_out[i] = (uint8_t)(__builtin_amdgcn_alignbit(hi, lo, sh) & mask);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_channel(bool encode, int bits, const ChanArgs& a, hipStream_t s) {
+  switch (bits) {
+    case 2: return launch_b<2>(encode, a, s);
+    case 3: return launch_b<3>(encode, a, s);
+    case 4: return launch_b<4>(encode, a, s);
+    case 5: return launch_b<5>(encode, a, s);
+    case 6: return launch_b<6>(encode, a, s);
+    case 7: return launch_b<7>(encode, a, s);
+    case 8: return launch_b<8>(encode, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_pack(bool pack, const PackArgs& a, hipStream_t s) {
+  if (pack) {
+    const uint64_t nwords = (a.dim * a.bits + 31u) / 32u;
+    const uint64_t grid = persistent_grid((const void*)&pack_generic, (a.count * nwords + kBlock - 1) / kBlock);
+    hipLaunchKernelGGL(pack_generic, dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+  } else {
+    const uint64_t grid =
+        persistent_grid((const void*)&unpack_generic, (a.count * a.dim + kBlock - 1) / kBlock);
+    hipLaunchKernelGGL(unpack_generic, dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace pitch

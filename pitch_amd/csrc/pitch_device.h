@@ -1,0 +1,187 @@
+// Device-side building blocks shared by the codec kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "pitch_launch.h"
+#include "pitch_tables.inc"
+
+namespace pitch {
+
+constexpr int kBlock = 256;  // threads per workgroup: four wave64s
+
+// ---------------------------------------------------------------------------------------------------
+// compile-time loop
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
+
+// ---------------------------------------------------------------------------------------------------
+// Rotation signs. pcg_hash as reference/pitch_reference.py:11-15 (PITCHKernels.metal:26-31); the sign of
+// coordinate i is +1 when pcg_hash(seed + i) is odd and -1 when it is even (pitch_reference.py:17-19).
+__host__ __device__ __forceinline__ uint32_t pcg_hash(uint32_t v) {
+  const uint32_t state = v * 747796405u + 2891336453u;
+  const uint32_t word = ((state >> ((state >> 28u) + 4u)) ^ state) * 277803737u;
+  return (word >> 22u) ^ word;
+}
+__host__ __device__ __forceinline__ bool sign_is_negative(uint32_t seed, uint32_t i) {
+  return (pcg_hash(seed + i) & 1u) == 0u;
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Cross-lane exchange with the lane at (lane ^ MASK). Lanes 1 and 2 apart use DPP quad permutes, 4 apart a
+// half-row mirror followed by a quad reverse (i -> 7-i -> (7-i)^3 = i^4), 8 apart a row rotate by 8;
+// 16 and 32 apart go through ds_bpermute. Every lane of the wave must be active.
+template <int MASK>
+__device__ __forceinline__ uint32_t xchg_u32(uint32_t x) {
+  if constexpr (MASK == 1) {
+    return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);  // quad_perm:[1,0,3,2]
+  } else if constexpr (MASK == 2) {
+    return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);  // quad_perm:[2,3,0,1]
+  } else if constexpr (MASK == 4) {
+    const uint32_t y = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, true);  // row_half_mirror
+    return __builtin_amdgcn_mov_dpp(y, 0x1B, 0xF, 0xF, true);               // quad_perm:[3,2,1,0]
+  } else if constexpr (MASK == 8) {
+    return __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);  // row_ror:8
+  } else {
+    static_assert(MASK == 16 || MASK == 32, "lane distance");
+    const int src = (int)((__lane_id() ^ MASK) << 2);
+    return (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)x);
+  }
+}
+template <int MASK>
+__device__ __forceinline__ float xchg(float x) {
+  return __uint_as_float(xchg_u32<MASK>(__float_as_uint(x)));
+}
+template <int MASK>
+__device__ __forceinline__ double xchg(double x) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = xchg_u32<MASK>((uint32_t)u);
+  const uint32_t hi = xchg_u32<MASK>((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+__device__ __forceinline__ float fma_t(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double fma_t(double a, double b, double c) { return __builtin_fma(a, b, c); }
+
+// ---------------------------------------------------------------------------------------------------
+// Correctly rounded a / b given inv = RN(1 / b): q = RN(a * inv) is within one ulp of a / b, the
+// remainder a - b*q is exact under fma, and RN(q + r * inv) is the correctly rounded quotient
+// (Markstein's theorem). Used where the reference divides in float64 and the result is compared
+// against decision boundaries.
+__device__ __forceinline__ double div_rn(double a, double b, double inv) {
+  const double q = a * inv;
+  const double r = __builtin_fma(-q, b, a);
+  return __builtin_fma(r, inv, q);
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Register layout of one vector of D coordinates spread over a team of T consecutive lanes.
+// Coordinates are grouped into chunks of W (4, or 2 when D == 2); lane t of the team holds chunks
+// j = k*T + t for k = 0 .. CH-1, so consecutive lanes read consecutive 16-byte chunks and every global
+// access of a wave is contiguous per vector. Element e = k*W + r of a lane is coordinate
+// c = W*(k*T + t) + r: bits [0, lgW) of c select r (in registers), bits [lgW, lgW+lgT) select the team lane
+// (exchanged across lanes) and the remaining bits select k (in registers).
+#ifndef PITCH_E64
+#define PITCH_E64 16  // coordinates per lane at D = 64
+#endif
+#ifndef PITCH_E128
+#define PITCH_E128 32  // coordinates per lane at D = 128
+#endif
+
+template <int D>
+struct Geom {
+  static constexpr int W = D >= 4 ? 4 : D;
+  static constexpr int E = D <= 16 ? D : (D == 64 ? PITCH_E64 : (D == 128 ? PITCH_E128 : (D < 64 ? 16 : 32)));
+  static constexpr int T = D / E;
+  static constexpr int CH = E / W;
+  static constexpr int V = 64 / T;                  // vectors per wave
+  static constexpr int VPB = V * (kBlock / 64);     // vectors per workgroup iteration
+  static constexpr int LGD = ilog2(D), LGW = ilog2(W), LGT = ilog2(T);
+  static_assert(T * E == D && CH * W == E && T <= 64, "geometry");
+  __host__ __device__ static constexpr int coord(int t, int e) { return W * ((e / W) * T + t) + (e % W); }
+};
+
+// In-place unnormalised Walsh-Hadamard transform of one vector held by a team, with the stages in the
+// reference's order (bit 0 first; reference/pitch_reference.py:21-31) and each butterfly computing
+// exactly a + b and a - b, so a float64 transform reproduces the reference bit for bit.
+// Cross-lane butterfly: the low lane computes fma(mine, +1, partner) = a + b, the high lane
+// fma(mine, -1, partner) = a - b.
+template <int D, typename F>
+__device__ __forceinline__ void fwht(F (&v)[Geom<D>::E], int t) {
+  using G = Geom<D>;
+  static_for<0, G::LGD>([&](auto bit_c) {
+    constexpr int bit = decltype(bit_c)::value;
+    if constexpr (bit >= G::LGW && bit < G::LGW + G::LGT) {
+      constexpr int lm = 1 << (bit - G::LGW);
+      const F sg = (t & lm) ? F(-1) : F(1);
+#pragma unroll
+      for (int e = 0; e < G::E; ++e) v[e] = fma_t(v[e], sg, xchg<lm>(v[e]));
+    } else {
+      constexpr int m = bit < G::LGW ? (1 << bit) : (G::W << (bit - G::LGW - G::LGT));
+#pragma unroll
+      for (int e = 0; e < G::E; ++e) {
+        if (!(e & m)) {
+          const F a = v[e], b = v[e | m];
+          v[e] = a + b;
+          v[e | m] = a - b;
+        }
+      }
+    }
+  });
+}
+
+// Reduction over the team (all lanes end with the result).
+template <int T, typename F, typename Op>
+__device__ __forceinline__ F team_reduce(F x, Op op) {
+  static_for<0, ilog2(T)>([&](auto s_c) {
+    constexpr int lm = 1 << decltype(s_c)::value;
+    x = op(x, xchg<lm>(x));
+  });
+  return x;
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Unaligned (4-byte aligned) vector memory types: gfx950 global memory serves dword-aligned multi-dword
+// accesses, so offsets that are multiples of 4 bytes still use 8/12/16-byte instructions.
+typedef float f32x2 __attribute__((ext_vector_type(2), aligned(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+
+template <int N>
+__device__ __forceinline__ void store_words(uint32_t* dst, const uint32_t (&w)[N]) {
+  int i = 0;
+#pragma unroll
+  for (; i + 4 <= N; i += 4) *(u32x4*)(dst + i) = u32x4{w[i], w[i + 1], w[i + 2], w[i + 3]};
+  if constexpr (N % 4 == 3) *(u32x3*)(dst + i) = u32x3{w[i], w[i + 1], w[i + 2]};
+  if constexpr (N % 4 == 2) *(u32x2*)(dst + i) = u32x2{w[i], w[i + 1]};
+  if constexpr (N % 4 == 1) dst[i] = w[i];
+}
+
+// Packs 32 codes given as bytes (bytes[i] holds code i < 2^B) into B little-endian words: code i at bits
+// [i*B, i*B + B) (reference/pitch_reference.py:68-78).
+template <int B>
+__device__ __forceinline__ void pack32(const uint32_t (&bytes)[8], uint32_t (&w)[B]) {
+#pragma unroll
+  for (int k = 0; k < B; ++k) w[k] = 0u;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t c = (bytes[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+    const int pos = i * B, wi = pos >> 5, sh = pos & 31;
+    w[wi] |= c << sh;
+    if (sh + B > 32) w[wi + 1] |= c >> (32 - sh);
+  }
+}
+
+}  // namespace pitch

@@ -1,0 +1,74 @@
+// Internal launch interface between the C ABI (pitch_abi.cpp) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pitch {
+
+// Arguments of one per-vector encode or decode launch (pointers already advanced by the byte offsets).
+struct VecArgs {
+  const float* in;           // encode: count * dim fp32
+  const uint32_t* codes_in;  // decode: count * code_stride bytes
+  uint32_t* codes_out;       // encode
+  const float* scales_in;    // decode: count fp32
+  float* scales_out;         // encode
+  float* out;                // decode: count * dim fp32
+  uint64_t count;
+  uint32_t seed;
+  uint32_t reserved;
+  // Rotation signs per team lane: bit e of lane_flips[t] is 1 when the coordinate held as element e by
+  // team lane t has sign -1 (filled by the launcher from the seed).
+  uint32_t lane_flips[32];
+};
+
+// Arguments of one per-channel (KIVI) launch.
+struct ChanArgs {
+  const float* in;
+  const uint32_t* codes_in;
+  uint32_t* codes_out;
+  const uint16_t* ranges_in;  // fp16 bits, [group][min row][max row]
+  uint16_t* ranges_out;
+  float* out;
+  uint32_t count;   // tokens
+  uint32_t dim;     // channels
+  uint32_t group;   // tokens per group
+  uint32_t nwords;  // 32-bit words of codes per token
+};
+
+// Arguments of a generic pack / unpack launch (unpacked codes are one byte each).
+struct PackArgs {
+  const uint8_t* unpacked_in;
+  uint8_t* unpacked_out;
+  const uint32_t* packed_in;
+  uint32_t* packed_out;
+  uint64_t count;
+  uint32_t dim;
+  uint32_t bits;
+};
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// Grid size for a grid-stride kernel: enough workgroups to fill every CU at the kernel's occupancy,
+// but no more than the work needs.
+uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed);
+
+#define PITCH_DECLARE_VEC_LAUNCH(D) \
+  hipError_t launch_vec_d##D(bool encode, bool polar, int bits, const VecArgs& a, hipStream_t s);
+PITCH_DECLARE_VEC_LAUNCH(2)
+PITCH_DECLARE_VEC_LAUNCH(4)
+PITCH_DECLARE_VEC_LAUNCH(8)
+PITCH_DECLARE_VEC_LAUNCH(16)
+PITCH_DECLARE_VEC_LAUNCH(32)
+PITCH_DECLARE_VEC_LAUNCH(64)
+PITCH_DECLARE_VEC_LAUNCH(128)
+PITCH_DECLARE_VEC_LAUNCH(256)
+PITCH_DECLARE_VEC_LAUNCH(512)
+PITCH_DECLARE_VEC_LAUNCH(1024)
+#undef PITCH_DECLARE_VEC_LAUNCH
+
+hipError_t launch_channel(bool encode, int bits, const ChanArgs& a, hipStream_t s);
+hipError_t launch_pack(bool pack, const PackArgs& a, hipStream_t s);
+
+}  // namespace pitch
