@@ -144,24 +144,26 @@ int device_cu_count() {
   return n;
 }
 
-uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed) {
+uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size) {
   static std::mutex mu;
   static std::unordered_map<const void*, int> occ_cache;
-  // PITCH_BLOCKS_PER_CU overrides the resident-block count per CU (tuning aid); 0 or unset = occupancy.
+  // PITCH_BLOCKS_PER_CU overrides the resident 256-thread-block count per CU (tuning aid; smaller blocks
+  // scale it up); 0 or unset = occupancy.
   static const int override_per_cu = [] {
     const char* e = std::getenv("PITCH_BLOCKS_PER_CU");
     return e ? std::atoi(e) : 0;
   }();
   int occ = 0;
   if (override_per_cu > 0) {
-    occ = override_per_cu;
+    occ = override_per_cu * (256 / block_size);
   } else {
     std::lock_guard<std::mutex> lock(mu);
     auto it = occ_cache.find(kernel);
     if (it != occ_cache.end()) {
       occ = it->second;
     } else {
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) != hipSuccess || occ < 1) occ = 1;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, block_size, 0) != hipSuccess || occ < 1)
+        occ = 1;
       occ_cache[kernel] = occ;
     }
   }

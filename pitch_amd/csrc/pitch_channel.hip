@@ -246,7 +246,8 @@ __global__ __launch_bounds__(kBlock) void chan_decode4(ChanArgs p) {
         float o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = (float)((bits >> (B * r)) & kMask) * st[r] + bs[r];
-        *(f32x4*)(p.out + tk * dim + 4u * col) = f32x4{o[0], o[1], o[2], o[3]};
+        // a token row is written by consecutive lanes as whole cache lines: stream it past the caches
+        __builtin_nontemporal_store(f32x4{o[0], o[1], o[2], o[3]}, (f32x4*)(p.out + tk * dim + 4u * col));
       }
     }
   }

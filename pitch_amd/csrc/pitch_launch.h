@@ -52,7 +52,7 @@ int device_cu_count();
 
 // Grid size for a grid-stride kernel: enough workgroups to fill every CU at the kernel's occupancy,
 // but no more than the work needs.
-uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed);
+uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256);
 
 #define PITCH_DECLARE_VEC_LAUNCH(D) \
   hipError_t launch_vec_d##D(bool encode, bool polar, int bits, const VecArgs& a, hipStream_t s);

@@ -40,6 +40,109 @@ __device__ __forceinline__ double div_sqrt_d(double y) {
   else return div_rn(y, C::kSqrt, C::kInvSqrt);
 }
 
+// TurboQuant quantiser: code = #{edges < u}, searchsorted(edges, u, 'left') (pitch_reference.py:99-101).
+// With a bucket table (gen_tables.py lut_for): j = clamp(floor(u * 2^m + off)), code = c_j + [u > e_j], one
+// 8-byte LDS read per coordinate. Lookups are issued in batches of up to 15 (what the LDS wait counter
+// tracks) before any result is used, so a wave pays one LDS round trip per batch, not per coordinate.
+// Tables too large for LDS use a binary search over the float64 edges.
+template <int D, int B>
+struct TqQuant {
+  static constexpr int L = 1 << B;
+  static constexpr PitchLutInfo LI = pitch_lut_info(ilog2(D), B);
+  static constexpr bool kLut = LI.offset >= 0;
+  static constexpr int kBatch = 15;
+
+  struct Smem {
+    uint2 lut[kLut ? LI.entries : 1];
+    double edge64[kLut ? 1 : L];
+  };
+
+  __device__ static void load(Smem& sm, int tid, int nthreads) {
+    if constexpr (kLut) {
+      for (int i = tid; i < LI.entries; i += nthreads)
+        sm.lut[i] = make_uint2(pitch_lut_tab[2 * (LI.offset + i)], pitch_lut_tab[2 * (LI.offset + i) + 1]);
+    } else {
+      constexpr int off = pitch_codebook_offset(ilog2(D), B);
+      for (int i = tid; i < L; i += nthreads) sm.edge64[i] = (double)pitch_edge_tab[off + i];
+    }
+  }
+
+  // Codes of x[0..N) packed into words as they are produced: code e at bits [e*B, e*B + B) of w.
+  template <int N, int NWORDS>
+  __device__ static void codes_packed(const Smem& sm, const double (&x)[N], double us, uint32_t (&w)[NWORDS]) {
+#pragma unroll
+    for (int i = 0; i < NWORDS; ++i) w[i] = 0u;
+    auto put = [&](int e, uint32_t cd) {
+      const int pos = e * B, wi = pos >> 5, sh = pos & 31;
+      w[wi] |= cd << sh;
+      if (sh + B > 32) w[wi + 1] |= cd >> (32 - sh);
+    };
+    if constexpr (kLut) {
+      const double us_m = us * LI.scale;
+#pragma unroll
+      for (int b0 = 0; b0 < N; b0 += kBatch) {
+        uint2 ent[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          if (b0 + i < N) {
+            const double tt = __builtin_fmax(__builtin_fma(x[b0 + i], us_m, LI.off), 0.0);
+            uint32_t j = (uint32_t)tt;
+            j = j < (uint32_t)(LI.entries - 1) ? j : (uint32_t)(LI.entries - 1);
+            ent[i] = sm.lut[j];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i)
+          if (b0 + i < N) put(b0 + i, ent[i].y + (x[b0 + i] * us > (double)__uint_as_float(ent[i].x) ? 1u : 0u));
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const double u = x[e] * us;
+        uint32_t cd = 0;
+#pragma unroll
+        for (int s = L / 2; s >= 1; s >>= 1) cd = (u > sm.edge64[cd + s - 1]) ? cd + s : cd;
+        put(e, cd);
+      }
+    }
+  }
+
+  // codes of x[0..N) with u = x * us; us_m = us * 2^m (exact scaling)
+  template <int N>
+  __device__ static void codes(const Smem& sm, const double (&x)[N], double us, uint32_t (&out)[N]) {
+    if constexpr (kLut) {
+      const double us_m = us * LI.scale;
+#pragma unroll
+      for (int b0 = 0; b0 < N; b0 += kBatch) {
+        uint2 ent[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          if (b0 + i < N) {
+            const double tt = __builtin_fmax(__builtin_fma(x[b0 + i], us_m, LI.off), 0.0);
+            uint32_t j = (uint32_t)tt;
+            j = j < (uint32_t)(LI.entries - 1) ? j : (uint32_t)(LI.entries - 1);
+            ent[i] = sm.lut[j];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          if (b0 + i < N)
+            out[b0 + i] = ent[i].y + (x[b0 + i] * us > (double)__uint_as_float(ent[i].x) ? 1u : 0u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const double u = x[e] * us;
+        uint32_t cd = 0;
+#pragma unroll
+        for (int s = L / 2; s >= 1; s >>= 1) cd = (u > sm.edge64[cd + s - 1]) ? cd + s : cd;
+        out[e] = cd;
+      }
+    }
+  }
+};
+
 template <int W>
 __device__ __forceinline__ void load_chunk(const float* src, float (&f)[W]) {
   if constexpr (W == 4) {
@@ -73,7 +176,8 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
   constexpr int L = 1 << B;
   constexpr int NW = (D * B + 31) / 32;  // 32-bit words of codes per vector
   constexpr bool kStage = D >= 32;       // codes are packed from LDS in groups of 32
-  __shared__ double s_edge[POLAR ? 1 : L];
+  using Q = TqQuant<D, B>;
+  __shared__ typename Q::Smem s_q;
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[kStage ? G::VPB * D / 4 : 4];
 
   const int tid = threadIdx.x;
@@ -81,10 +185,7 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
   const int t = lane & (G::T - 1);
   const int slot = (tid >> 6) * G::V + lane / G::T;
 
-  if constexpr (!POLAR) {
-    constexpr int off = pitch_codebook_offset(ilog2(D), B);
-    for (int i = tid; i < L; i += kBlock) s_edge[i] = (double)pitch_edge_tab[off + i];
-  }
+  if constexpr (!POLAR) Q::load(s_q, tid, kBlock);
   const uint32_t fbits = p.lane_flips[t];
   uint32_t flip[G::E];
 #pragma unroll
@@ -122,15 +223,7 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
       const double us = (1.0 / safe) * DimConst<D>::kInvSqrt;
       scale = (float)nrm;
       fwht<D, double>(x, t);
-      // code = number of edges strictly below u: searchsorted(edges, u, 'left') (pitch_reference.py:101)
-#pragma unroll
-      for (int e = 0; e < G::E; ++e) {
-        const double u = x[e] * us;
-        uint32_t cd = 0;
-#pragma unroll
-        for (int s = L / 2; s >= 1; s >>= 1) cd = (u > s_edge[cd + s - 1]) ? cd + s : cd;
-        code[e] = cd;
-      }
+      Q::codes(s_q, x, us, code);
     } else {
       fwht<D, double>(x, t);
 #pragma unroll
@@ -296,6 +389,10 @@ __device__ __forceinline__ void decode_chunk(uint32_t bits, const float* s_tab, 
   }
 }
 
+#ifndef PITCH_DEC_LDS_STORE
+#define PITCH_DEC_LDS_STORE 1  // decoded vectors are staged in LDS and stored as contiguous wave blocks
+#endif
+
 #ifndef PITCH_DEC_WAVES
 #define PITCH_DEC_WAVES 1  // minimum waves per SIMD requested for the decoders (caps their VGPRs)
 #endif
@@ -307,6 +404,11 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   constexpr int NW = (D * B + 31) / 32;
   constexpr int CB = G::W * B;  // bits of codes per chunk (<= 32)
   __shared__ __attribute__((aligned(16))) float s_tab[TB::FLOATS];
+  // optional LDS staging of the output (D >= 64): each wave writes its vectors back contiguously
+  constexpr bool kLdsStore = PITCH_DEC_LDS_STORE && D >= 64 && G::W == 4;
+  constexpr int kVecStride = D + 4;  // floats; padding spreads consecutive vectors over the LDS banks
+  constexpr int kWaveOutFloats = G::V * kVecStride;
+  __shared__ __attribute__((aligned(16))) float s_out[kLdsStore ? 4 * kWaveOutFloats : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -362,7 +464,35 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
     fwht<D, float>(y, t);
 
     const float f = b.scale * DimConst<D>::kInvSqrtF;
-    if (valid) {
+    if constexpr (kLdsStore) {
+      // stage the wave's vectors in LDS, then write them back as contiguous 1 KB wave stores
+      float* ws = s_out + (tid >> 6) * kWaveOutFloats;
+      const int vw = lane / G::T;  // vector within the wave
+#pragma unroll
+      for (int k = 0; k < G::CH; ++k) {
+        float o[G::W];
+#pragma unroll
+        for (int r = 0; r < G::W; ++r)
+          o[r] = __uint_as_float(__float_as_uint(y[k * G::W + r] * f) ^ flip[k * G::W + r]);
+        *(float4*)(ws + vw * kVecStride + G::W * (k * G::T + t)) = float4{o[0], o[1], o[2], o[3]};
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint64_t wbase = base + (uint64_t)(tid >> 6) * G::V;  // first vector of this wave
+      float* dstw = p.out + wbase * D;
+#pragma unroll
+      for (int m = 0; m < G::V * D / 4 / 64; ++m) {
+        const int q = lane + 64 * m;          // 16-byte chunk of the wave's output block
+        const int vq = q / (D / 4), cq = q % (D / 4);
+        const float4 val = *(const float4*)(ws + vq * kVecStride + 4 * cq);
+        if (!TAIL || wbase + vq < p.count) {
+          float o[4] = {val.x, val.y, val.z, val.w};
+          store_chunk<4>(dstw + 4 * q, o);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    } else if (valid) {
       float* dst = p.out + v * D;
 #pragma unroll
       for (int k = 0; k < G::CH; ++k) {
@@ -410,10 +540,167 @@ void fill_lane_flips(uint32_t seed, uint32_t* out) {
   for (int t = 0; t < 32; ++t) out[t] = cached[t];
 }
 
+// ----------------------------------------------------------------------------------------------------
+// Lane-per-vector TurboQuant encoder, D in 8..128. A workgroup is one wave; it stages V = 64 / T vectors per
+// iteration through LDS with coalesced 1 KB loads, after which each team of T lanes (T = 1 up to D = 64, 2 at
+// D = 128) holds its vector as E = D / T contiguous float64 coordinates: coordinate c = t * E + e. The
+// transform runs in registers (plus one DPP exchange at D = 128), the rotation signs are wave-uniform
+// scalars, codes are packed in registers and written back through LDS as contiguous wave stores.
+template <int D>
+struct Lpv {
+  static constexpr int T = D <= 64 ? 1 : 2;
+  static constexpr int E = D / T;
+  static constexpr int V = 64 / T;        // vectors per wave iteration
+  static constexpr int HALF = E + 4;      // staged floats per team lane (padding spreads lanes over the banks)
+  static constexpr int STRIDE = T * HALF; // staged floats per vector
+  static constexpr int QPV = D / 4;       // 16-byte chunks per vector
+  static constexpr int QPL = V * QPV / 64;  // 16-byte chunks each lane loads per iteration
+};
+
+// Transform of E contiguous coordinates per lane across a team of T lanes (bits >= log2 E cross lanes).
+template <int E, int T, typename F>
+__device__ __forceinline__ void fwht_contig(F (&v)[E], int t) {
+  static_for<0, ilog2(E) + ilog2(T)>([&](auto bit_c) {
+    constexpr int bit = decltype(bit_c)::value;
+    if constexpr (bit < ilog2(E)) {
+      constexpr int m = 1 << bit;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if (!(e & m)) {
+          const F a = v[e], b = v[e | m];
+          v[e] = a + b;
+          v[e | m] = a - b;
+        }
+      }
+    } else {
+      constexpr int lm = 1 << (bit - ilog2(E));
+      const F sg = (t & lm) ? F(-1) : F(1);
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[e] = fma_t(v[e], sg, xchg<lm>(v[e]));
+    }
+  });
+}
+
+// Coalesced load of the wave's block of V vectors (vectors past the end re-read the last one).
+template <int D>
+__device__ __forceinline__ void lpv_fetch(const float* in, uint64_t base, uint64_t count, int lane,
+                                         f32x4 (&pf)[Lpv<D>::QPL]) {
+  using Lp = Lpv<D>;
+#pragma unroll
+  for (int i = 0; i < Lp::QPL; ++i) {
+    const int q = lane + 64 * i;
+    const int vq = q / Lp::QPV, pq = q % Lp::QPV;
+    const uint64_t vg = base + vq < count ? base + vq : count - 1;
+    pf[i] = *(const f32x4*)(in + vg * D + 4 * pq);
+  }
+}
+
+template <int D, int B>
+__global__ __launch_bounds__(64) void tq_encode_lpv(VecArgs p) {
+  using Lp = Lpv<D>;
+  constexpr int E = Lp::E, T = Lp::T, V = Lp::V;
+  constexpr int L = 1 << B;
+  constexpr int NW = (D * B + 31) / 32;   // code words per vector
+  constexpr int NWL = (E * B + 31) / 32;  // code words per lane (E * B is a multiple of 32 when T > 1)
+  using Q = TqQuant<D, B>;
+  static_assert(T == 1 || (E * B) % 32 == 0, "lanes of a team own whole code words");
+  __shared__ __attribute__((aligned(16))) float s_in[V * Lp::STRIDE];
+  __shared__ __attribute__((aligned(16))) uint32_t s_codes[V * NW];
+  __shared__ typename Q::Smem s_q;
+
+  const int lane = threadIdx.x;
+  const int t = lane & (T - 1);
+  const int vw = lane / T;
+  Q::load(s_q, lane, 64);
+  __syncthreads();
+
+  for (uint64_t base = (uint64_t)blockIdx.x * V; base < p.count; base += (uint64_t)gridDim.x * V) {
+    // stage the wave's block of V vectors in LDS with coalesced loads
+    {
+      f32x4 pf[Lp::QPL];
+      lpv_fetch<D>(p.in, base, p.count, lane, pf);
+#pragma unroll
+      for (int i = 0; i < Lp::QPL; ++i) {
+        const int q = lane + 64 * i;
+        const int vq = q / Lp::QPV, pq = q % Lp::QPV;
+        const int h = (4 * pq) / E, pe = 4 * pq - h * E;
+        *(float4*)(s_in + vq * Lp::STRIDE + h * Lp::HALF + pe) = float4{pf[i].x, pf[i].y, pf[i].z, pf[i].w};
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // this lane's E coordinates c = t * E + e with the rotation signs applied (exact); the sign bits of
+    // coordinates 0..D-1 are wave-uniform kernel arguments (bit c % 32 of word c / 32)
+    double x[E];
+#pragma unroll
+    for (int k = 0; k < E / 4; ++k) {
+      const float4 f = *(const float4*)(s_in + vw * Lp::STRIDE + t * Lp::HALF + 4 * k);
+      const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = 4 * k + r;
+        uint32_t m = (p.lane_flips[e >> 5] >> (e & 31)) << 31;
+        if constexpr (T > 1) m = t ? (p.lane_flips[(E + e) >> 5] >> ((E + e) & 31)) << 31 : m;
+        x[e] = (double)__uint_as_float(__float_as_uint(fv[r]) ^ m);
+      }
+    }
+
+    // u = H(s * x) / (||x|| sqrt(d)) as in vec_encode (pitch_reference.py:96-98)
+    double ss = 0.0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) ss = __builtin_fma(x[e], x[e], ss);
+    ss = team_reduce<T>(ss, [](double a, double b) { return a + b; });
+    const double nrm = __builtin_sqrt(ss);
+    const double us = (1.0 / (nrm > 0.0 ? nrm : 1.0)) * DimConst<D>::kInvSqrt;
+    fwht_contig<E, T, double>(x, t);
+
+    // code = #{edges < u} (pitch_reference.py:101), packed in registers (code of coordinate e at bit e * B)
+    uint32_t w[NWL];
+    Q::codes_packed(s_q, x, us, w);
+#pragma unroll
+    for (int i = 0; i < NWL; ++i) s_codes[vw * NW + t * NWL + i] = w[i];
+    if (t == 0 && base + vw < p.count) p.scales_out[base + vw] = (float)nrm;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // write the wave's V * NW code words contiguously, in the widest chunks that stay inside one vector
+    constexpr int CW = NW % 4 == 0 ? 4 : (NW % 2 == 0 ? 2 : 1);
+    uint32_t* dst = p.codes_out + base * NW;
+#pragma unroll
+    for (int i = 0; i < (V * NW / CW + 63) / 64; ++i) {
+      const int q = lane + 64 * i;
+      if (q < V * NW / CW && base + (q * CW) / NW < p.count) {
+        if constexpr (CW == 4) *(u32x4*)(dst + 4 * q) = *(const u32x4*)(s_codes + 4 * q);
+        else if constexpr (CW == 2) *(u32x2*)(dst + 2 * q) = *(const u32x2*)(s_codes + 2 * q);
+        else dst[q] = s_codes[q];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+template <int D>
+constexpr bool use_lpv_encoder() { return D >= 8 && D <= 128; }
+
 template <int D, int B, bool POLAR>
 hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   using G = Geom<D>;
   VecArgs a = args;
+  if constexpr (!POLAR && use_lpv_encoder<D>()) {
+    if (encode) {
+      // sign bits of coordinates 0..D-1, wave-uniform in this kernel
+      for (int i = 0; i < 32; ++i) a.lane_flips[i] = 0u;
+      for (int c = 0; c < D; ++c)
+        if (sign_is_negative(a.seed, (uint32_t)c)) a.lane_flips[c >> 5] |= 1u << (c & 31);
+      const uint64_t need = (a.count + Lpv<D>::V - 1) / Lpv<D>::V;
+      const void* k = (const void*)&tq_encode_lpv<D, B>;
+      const uint64_t grid = persistent_grid(k, need, 64);
+      hipLaunchKernelGGL((tq_encode_lpv<D, B>), dim3((uint32_t)grid), dim3(64), 0, s, a);
+      return hipGetLastError();
+    }
+  }
   fill_lane_flips<D>(a.seed, a.lane_flips);
   const uint64_t need = (a.count + G::VPB - 1) / G::VPB;
   if (encode) {
