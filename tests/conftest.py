@@ -14,6 +14,16 @@ def pytest_configure(config):
 
 
 @pytest.fixture(scope="session")
+def built_library():
+    """libpitch_amd.so, built in-tree first if no build is present (hipcc cross-compiles without a GPU)."""
+    from pitch_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        from pitch_amd.build import build
+        build()
+    return _lib.LIB_PATH
+
+
+@pytest.fixture(scope="session")
 def device():
     import torch
     if not torch.cuda.is_available():

@@ -1,0 +1,226 @@
+"""The C ABI of libpitch_amd.so without a GPU (CPU only): exports, configs and argument validation.
+
+Every symbol declared in include/pitch_amd.h must be exported and bound by pitch_amd/_lib.py. The config
+entry points and the enqueue entry points' argument checks need no device: they mirror QuantConfig.init
+(Sources/PITCH/Models/QuantConfig.swift:24-40), ChannelQuantConfig.init (Sources/PITCH/PerChannel.swift:36-52)
+and the buffer checks of Sources/PITCH/Core/Codec.swift:30-47 and PerChannel.swift:318-374, and they all run
+before the library looks for a device. The buffers passed here are host memory and never reach a kernel:
+every call either fails validation or stops at the device-memory check.
+"""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from pitch_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "pitch_amd.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(pitch_[a-z0-9_]+)\s*\(", text)))
+
+
+def header_defines():
+    return {m.group(1): int(m.group(2)) for m in
+            re.finditer(r"#define\s+(PITCH_(?:OK|ERR_[A-Z_]+))\s+\(?(-?\d+)\)?", HEADER.read_text())}
+
+
+@pytest.fixture(scope="module")
+def lib(built_library):
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = header_functions()
+    assert len(names) >= 10
+    assert set(names) == set(_lib.SIGNATURES), "header and ctypes binding disagree"
+    for n in names:
+        assert hasattr(lib, n), f"{n} not exported"
+    dyn = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True)
+    if dyn.returncode == 0:
+        exported = {line.split()[-1] for line in dyn.stdout.splitlines() if line.strip()}
+        assert set(names) <= exported
+
+
+def test_error_codes_match_header():
+    d = header_defines()
+    assert d["PITCH_OK"] == _lib.PITCH_OK == 0
+    assert d["PITCH_ERR_INVALID_INPUT"] == _lib.ERR_INVALID_INPUT
+    assert d["PITCH_ERR_INVALID_BIT_WIDTH"] == _lib.ERR_INVALID_BIT_WIDTH
+    assert d["PITCH_ERR_INVALID_DIMENSION"] == _lib.ERR_INVALID_DIMENSION
+    assert d["PITCH_ERR_CONFIGURATION_MISMATCH"] == _lib.ERR_CONFIGURATION_MISMATCH
+    assert d["PITCH_ERR_ENCODING_FAILED"] == _lib.ERR_ENCODING_FAILED
+    assert d["PITCH_ERR_DECODING_FAILED"] == _lib.ERR_DECODING_FAILED
+    assert d["PITCH_ERR_DEVICE_UNAVAILABLE"] == _lib.ERR_DEVICE_UNAVAILABLE
+
+
+def test_version(lib):
+    assert lib.pitch_version() == 0x000100
+
+
+def _config(lib, method, dim, bits, seed=0x50495443):
+    c = _lib.PitchConfigC()
+    cs = ctypes.c_uint32(0)
+    rc = lib.pitch_config(method, dim, bits, seed, ctypes.byref(c), ctypes.byref(cs))
+    return rc, c, cs.value
+
+
+def test_config_all_valid(lib):
+    for method in (0, 1):
+        for dim in [2 ** k for k in range(1, 11)]:
+            for bits in range(2, 9):
+                rc, c, cs = _config(lib, method, dim, bits, 7)
+                assert rc == 0
+                assert (c.method, c.dim, c.bits, c.seed) == (method, dim, bits, 7)
+                assert cs == ((dim * bits + 7) // 8 + 3) & ~3        # reference/pitch_reference.py:65-66
+
+
+@pytest.mark.parametrize("dim", [0, 1, 3, 100, 2048, 4096])
+def test_config_invalid_dimension(lib, dim):
+    """CodecTests.invalidDimensionThrows (Tests/PITCHTests/CodecTests.swift:121-126)."""
+    rc, _, _ = _config(lib, 0, dim, 4)
+    assert rc == _lib.ERR_INVALID_DIMENSION
+    assert "dimension" in _lib.last_error().lower()
+
+
+@pytest.mark.parametrize("bits", [0, 1, 9, 16])
+def test_config_invalid_bits(lib, bits):
+    """CodecTests.invalidBitWidthThrows (CodecTests.swift:128-133)."""
+    rc, _, _ = _config(lib, 1, 64, bits)
+    assert rc == _lib.ERR_INVALID_BIT_WIDTH
+    assert "bit width" in _lib.last_error().lower()
+
+
+def test_config_invalid_method_and_null_outputs(lib):
+    assert _config(lib, 2, 64, 4)[0] == _lib.ERR_INVALID_INPUT
+    assert lib.pitch_config(0, 64, 4, 0, None, None) == 0
+
+
+def _channel_config(lib, dim, bits, G):
+    c = _lib.PitchChannelConfigC()
+    cs, rs = ctypes.c_uint32(0), ctypes.c_uint32(0)
+    rc = lib.pitch_channel_config(dim, bits, G, ctypes.byref(c), ctypes.byref(cs), ctypes.byref(rs))
+    return rc, c, cs.value, rs.value
+
+
+def test_channel_config(lib):
+    rc, c, cs, rs = _channel_config(lib, 96, 4, 64)
+    assert rc == 0 and (c.dim, c.bits, c.group_size, c.reserved) == (96, 4, 64, 0)
+    assert cs == 48 and rs == 384
+    assert _channel_config(lib, 1, 2, 1)[0] == 0
+    assert _channel_config(lib, 1024, 8, 65536)[0] == 0
+    # PerChannelTests.rejectsInvalidArguments (Tests/PITCHTests/PerChannelTests.swift:186-191)
+    assert _channel_config(lib, 0, 4, 64)[0] == _lib.ERR_INVALID_INPUT
+    assert _channel_config(lib, 2048, 4, 64)[0] == _lib.ERR_INVALID_INPUT
+    assert _channel_config(lib, 64, 1, 64)[0] == _lib.ERR_INVALID_BIT_WIDTH
+    assert _channel_config(lib, 64, 4, 0)[0] == _lib.ERR_INVALID_INPUT
+    assert _channel_config(lib, 64, 4, 65537)[0] == _lib.ERR_INVALID_INPUT
+
+
+# ----------------------------------------------------------------------------- enqueue validation
+class Host:
+    """A host buffer used only as a pointer for argument checks; it never reaches a kernel."""
+
+    def __init__(self, nbytes):
+        self.buf = ctypes.create_string_buffer(max(nbytes, 1))
+        self.nbytes = nbytes
+
+    @property
+    def p(self):
+        return ctypes.cast(self.buf, ctypes.c_void_p)
+
+
+def _enc(lib, cfg, count, inp, codes, scales, offs=(0, 0, 0)):
+    return lib.pitch_enqueue_encode(ctypes.byref(cfg) if cfg is not None else None, inp.p, inp.nbytes, offs[0],
+                                    codes.p, codes.nbytes, offs[1], scales.p, scales.nbytes, offs[2], count, None)
+
+
+def _dec(lib, cfg, count, codes, scales, out, offs=(0, 0, 0)):
+    return lib.pitch_enqueue_decode(ctypes.byref(cfg) if cfg is not None else None, codes.p, codes.nbytes, offs[0],
+                                    scales.p, scales.nbytes, offs[1], out.p, out.nbytes, offs[2], count, None)
+
+
+def test_enqueue_rejects_undersized_buffers(lib):
+    """BatchAPITests.enqueueRejectsUndersizedBuffers (Tests/PITCHTests/BatchAPITests.swift:93-103)."""
+    cfg = _lib.PitchConfigC(0, 64, 4, 0)
+    rc = _enc(lib, cfg, 4, Host(64 * 4 * 4), Host(32 * 3), Host(16))      # codes need 4 * 32 bytes
+    assert rc == _lib.ERR_INVALID_INPUT
+    assert "codes" in _lib.last_error()
+    assert _enc(lib, cfg, 4, Host(64 * 4 * 4 - 4), Host(128), Host(16)) == _lib.ERR_INVALID_INPUT
+    assert _enc(lib, cfg, 4, Host(1024), Host(128), Host(12)) == _lib.ERR_INVALID_INPUT
+    assert _dec(lib, cfg, 4, Host(128), Host(16), Host(1020)) == _lib.ERR_INVALID_INPUT
+    # the size check counts the bytes after the offset
+    assert _enc(lib, cfg, 4, Host(1024), Host(128 + 4), Host(16), offs=(0, 8, 0)) == _lib.ERR_INVALID_INPUT
+    assert _enc(lib, cfg, 1, Host(1024), Host(128), Host(16), offs=(0, 256, 0)) == _lib.ERR_INVALID_INPUT
+
+
+def test_enqueue_rejects_misaligned_offsets(lib):
+    """BatchAPITests.enqueueRejectsMisalignedOffset (BatchAPITests.swift:105-116)."""
+    cfg = _lib.PitchConfigC(1, 64, 4, 0)
+    rc = _dec(lib, cfg, 1, Host(1024), Host(64), Host(4096), offs=(2, 0, 0))
+    assert rc == _lib.ERR_INVALID_INPUT and "multiple of 4" in _lib.last_error()
+    assert _dec(lib, cfg, 1, Host(1024), Host(64), Host(4096), offs=(0, 1, 0)) == _lib.ERR_INVALID_INPUT
+    assert _enc(lib, cfg, 1, Host(1024), Host(64), Host(64), offs=(6, 0, 0)) == _lib.ERR_INVALID_INPUT
+
+
+def test_enqueue_rejects_bad_config_and_count(lib):
+    big = Host(1 << 16)
+    assert _enc(lib, None, 1, big, big, big) == _lib.ERR_INVALID_INPUT
+    assert _enc(lib, _lib.PitchConfigC(0, 100, 4, 0), 1, big, big, big) == _lib.ERR_INVALID_DIMENSION
+    assert _dec(lib, _lib.PitchConfigC(0, 64, 9, 0), 1, big, big, big) == _lib.ERR_INVALID_BIT_WIDTH
+    assert _dec(lib, _lib.PitchConfigC(5, 64, 4, 0), 1, big, big, big) == _lib.ERR_INVALID_INPUT
+    assert _enc(lib, _lib.PitchConfigC(0, 64, 4, 0), 0, big, big, big) == _lib.ERR_INVALID_INPUT
+    assert _enc(lib, _lib.PitchConfigC(0, 1024, 4, 0), 2 ** 62, big, big, big) == _lib.ERR_INVALID_INPUT
+    null = Host(0)
+    null.buf = None
+    assert lib.pitch_enqueue_encode(ctypes.byref(_lib.PitchConfigC(0, 64, 4, 0)), None, 1 << 20, 0, big.p,
+                                    big.nbytes, 0, big.p, big.nbytes, 0, 1, None) == _lib.ERR_INVALID_INPUT
+
+
+def test_channel_enqueue_validation(lib):
+    """PerChannel.swift:318-374: ranges need groups * 4 * dim bytes after the offset."""
+    cfg = _lib.PitchChannelConfigC(64, 4, 64, 0)
+    n = 150                                           # 3 groups, the last one partial
+    inp, codes, ranges, out = Host(n * 256), Host(n * 32), Host(3 * 256), Host(n * 256)
+
+    def enc(r, offs=(0, 0, 0), count=n, c=cfg):
+        return lib.pitch_enqueue_channel_encode(ctypes.byref(c), inp.p, inp.nbytes, offs[0], codes.p,
+                                                codes.nbytes, offs[1], r.p, r.nbytes, offs[2], count, None)
+
+    def dec(r, offs=(0, 0, 0), count=n, c=cfg):
+        return lib.pitch_enqueue_channel_decode(ctypes.byref(c), codes.p, codes.nbytes, offs[0], r.p, r.nbytes,
+                                                offs[1], out.p, out.nbytes, offs[2], count, None)
+
+    assert enc(Host(2 * 256)) == _lib.ERR_INVALID_INPUT and "ranges" in _lib.last_error()
+    assert dec(Host(3 * 256 - 4)) == _lib.ERR_INVALID_INPUT
+    assert enc(ranges, offs=(0, 0, 2)) == _lib.ERR_INVALID_INPUT
+    assert enc(ranges, count=0) == _lib.ERR_INVALID_INPUT
+    assert enc(ranges, count=2 ** 32) == _lib.ERR_INVALID_INPUT
+    assert enc(ranges, c=_lib.PitchChannelConfigC(64, 4, 0, 0)) == _lib.ERR_INVALID_INPUT
+    assert dec(ranges, c=_lib.PitchChannelConfigC(64, 1, 64, 0)) == _lib.ERR_INVALID_BIT_WIDTH
+
+
+def test_valid_arguments_on_host_memory_stop_before_any_kernel(lib):
+    """With correct sizes, host pointers are refused by the device-memory check (or, with no GPU at all,
+    by the device lookup): either way an error, never a launch."""
+    cfg = _lib.PitchConfigC(0, 64, 4, 0)
+    rc = _enc(lib, cfg, 4, Host(1024), Host(128), Host(16))
+    assert rc in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+    assert _lib.last_error()
+
+
+def test_pack_entry_validation(lib):
+    big = Host(1 << 12)
+    assert lib.pitch_enqueue_pack_codes(0, 4, big.p, big.nbytes, 0, big.p, big.nbytes, 0, 1, None) \
+        == _lib.ERR_INVALID_DIMENSION
+    assert lib.pitch_enqueue_unpack_codes(64, 1, big.p, big.nbytes, 0, big.p, big.nbytes, 0, 1, None) \
+        == _lib.ERR_INVALID_BIT_WIDTH
+    assert lib.pitch_enqueue_pack_codes(64, 4, big.p, big.nbytes, 0, big.p, big.nbytes, 0, 0, None) \
+        == _lib.ERR_INVALID_INPUT
+    assert lib.pitch_enqueue_pack_codes(64, 4, big.p, 63, 0, big.p, big.nbytes, 0, 1, None) \
+        == _lib.ERR_INVALID_INPUT
