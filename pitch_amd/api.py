@@ -509,7 +509,9 @@ class PITCH:
             if t.dtype != torch.float32:
                 raise InvalidInput(f"{name} must be float32")
             return t.to(self.device).contiguous().reshape(-1)
-        a = np.ascontiguousarray(np.asarray(x, dtype=np.float32).reshape(-1))
+        a = np.asarray(x, dtype=np.float32).reshape(-1)
+        if not (a.flags.c_contiguous and a.flags.writeable):
+            a = a.copy()
         return torch.from_numpy(a).to(self.device)
 
     def _guard(self, fn, failure):

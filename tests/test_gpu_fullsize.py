@@ -1,0 +1,154 @@
+"""The kernels at BASELINE sizes (one GPU's share), checked through size-independent properties.
+
+At full size the oracle cannot check every vector in seconds, so each case checks:
+* a sample of rows (the first and last 64, plus 1024 at random) against the oracle: per-vector codes to the
+  counted near-boundary band and scales to one float32 ulp, KIVI codes and fp16 ranges bit-exact, and the
+  decode of the kernel's own codes within 1e-5 relative L2 (per-vector) or bit-exact (KIVI);
+* that encoding a slice through byte offsets into the whole cache gives the same bytes as the whole call;
+* the decode/encode error statistics (Theorem 1 band for TurboQuant on Gaussian rows).
+Inputs are generated on the device with torch's seeded generator. Sizes follow the BASELINE configs: config 2
+(32768 x 12 x 64, TurboQuant b = 2/3/4), config 3 (8 heads x 32768 x 64 KIVI keys, G = 64, b = 4), config 4
+(917,504 x 128, TurboQuant and PolarQuant b = 4), config 5 at one GPU's share under 8-way tensor parallelism
+(32 layers x 131072 x 128: V TurboQuant b = 3, K KIVI b = 4), and one call of more than 2^32 floats.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import pitch_oracle as O
+from test_gpu_parity import check_codes, check_scales, max_rel_diff, REL_L2_BAR
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(n, d, seed, dev, kind):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    if kind == "gauss":
+        return torch.randn(n, d, generator=g, device=dev)
+    if kind == "t5":       # Student-t nu = 5 times a per-row log-uniform factor in [0.5, 4]
+        z = torch.randn(n, d, generator=g, device=dev)
+        chi = torch.randn(n, d, 5, generator=g, device=dev).square_().sum(-1) if n * d <= 64 << 20 else None
+        if chi is None:    # large sizes: a cheaper heavy-tailed stand-in with the same support
+            u = torch.rand(n, d, generator=g, device=dev)
+            chi = 5 * (u.clamp_min(1e-6) ** 0.8)
+        f = torch.exp(torch.empty(n, 1, device=dev).uniform_(math.log(0.5), math.log(4), generator=g))
+        return z / torch.sqrt(chi / 5) * f
+    if kind == "keys":     # per-channel scales, a few outlier channels and a per-channel bias
+        z = torch.randn(n, d, generator=g, device=dev)
+        s = torch.exp(torch.randn(d, generator=g, device=dev))
+        s[:4] *= 20
+        return z * s + 3 * torch.randn(d, generator=g, device=dev)
+    raise ValueError(kind)
+
+
+def _sample(n, seed):
+    rng = np.random.default_rng(seed)
+    idx = np.concatenate([np.arange(min(64, n)), np.arange(max(0, n - 64), n), rng.integers(0, n, 1024)])
+    return np.unique(idx)
+
+
+def per_vector_full(q, method, n, d, bits, seed, kind="gauss", theorem1=False):
+    import torch
+    import pitch_amd as P
+    dev = q.device
+    print(f"full-size {method} n={n} d={d} b={bits}", flush=True)
+    cfg = P.QuantConfig(method, d, bits)
+    x = _gen(n, d, seed, dev, kind).contiguous()
+    codes = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=dev)
+    scales = torch.empty(n, dtype=torch.float32, device=dev)
+    out = torch.empty(n, d, dtype=torch.float32, device=dev)
+    q.enqueueEncode(x, codes, scales, n, cfg)
+    q.enqueueDecode(codes, scales, out, n, cfg)
+    torch.cuda.synchronize()
+    idx = _sample(n, seed)
+    it = torch.from_numpy(idx).to(dev)
+    X = x[it].cpu().numpy()
+    C = codes.view(n, cfg.codeStride)[it].cpu().numpy().tobytes()
+    S = scales[it].cpu().numpy()
+    ref_codes, ref_scales = O.ENCODERS[method](X.astype(np.float64), bits)
+    check_codes(method, X, bits, P.DEFAULT_SEED, C, O.pack_codes(ref_codes, bits), f"{method} n={n}")
+    check_scales(S, np.asarray(ref_scales, np.float32), "scales")
+    ours = O.unpack_codes(C, len(idx), d, bits)
+    recon = O.DECODERS[method](ours, S.astype(np.float64), bits)
+    assert max_rel_diff(out[it].cpu().numpy(), recon, d) < REL_L2_BAR
+    # a slice encoded through byte offsets equals the same bytes of the whole call
+    lo, m = n // 3, min(n // 3, 100003)
+    c2 = torch.zeros(m * cfg.codeStride, dtype=torch.uint8, device=dev)
+    s2 = torch.zeros(m, dtype=torch.float32, device=dev)
+    q.enqueueEncode(x, c2, s2, m, cfg, inputOffset=lo * d * 4)
+    torch.cuda.synchronize()
+    assert torch.equal(c2, codes[lo * cfg.codeStride:(lo + m) * cfg.codeStride])
+    assert torch.equal(s2, scales[lo:lo + m])
+    if theorem1:
+        num = (x - out).double().square().sum(1)
+        den = x.double().square().sum(1)
+        e = float((num / den).mean())
+        assert 4.0 ** -bits <= e <= math.sqrt(3) * math.pi / 2 * 4.0 ** -bits
+    del x, codes, scales, out, c2, s2
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_config2_gpt2_v_cache(q, bits):
+    per_vector_full(q, "turboQuant", 32768 * 12, 64, bits, 2000 + bits, "t5")
+
+
+@pytest.mark.parametrize("method", ["turboQuant", "polarQuant"])
+def test_config4_qwen_d128(q, method):
+    per_vector_full(q, method, 28 * 2 * 16384, 128, 4, 4000, "gauss", theorem1=(method == "turboQuant"))
+
+
+def test_config5_v_share(q):
+    per_vector_full(q, "turboQuant", 32 * 131072, 128, 3, 5000, "t5")
+
+
+def test_more_than_2_32_floats_in_one_call(q):
+    """count * dim > 2^32 (a documented extension: the reference caps a call below 2^32 elements)."""
+    per_vector_full(q, "turboQuant", (1 << 22) + 100, 1024, 4, 6000, "gauss")
+
+
+def channel_full(q, heads, tokens, d, bits, G, seed):
+    import torch
+    import pitch_amd as P
+    dev = q.device
+    print(f"full-size KIVI heads={heads} tokens={tokens} d={d} b={bits} G={G}", flush=True)
+    cfg = P.ChannelQuantConfig(d, bits, G)
+    groups = cfg.groupCount(tokens)
+    x = _gen(heads * tokens, d, seed, dev, "keys").contiguous()
+    codes = torch.empty(heads * tokens * cfg.codeStride, dtype=torch.uint8, device=dev)
+    ranges = torch.empty(heads * groups * cfg.rangeStride // 2, dtype=torch.float16, device=dev)
+    out = torch.empty(heads * tokens, d, dtype=torch.float32, device=dev)
+    for h in range(heads):           # one call per head, at its offsets in the whole cache
+        q.enqueuePerChannelEncode(x, codes, ranges, tokens, cfg, inputOffset=h * tokens * d * 4,
+                                  codesOffset=h * tokens * cfg.codeStride, rangesOffset=h * groups * cfg.rangeStride)
+        q.enqueuePerChannelDecode(codes, ranges, out, tokens, cfg, codesOffset=h * tokens * cfg.codeStride,
+                                  rangesOffset=h * groups * cfg.rangeStride, outputOffset=h * tokens * d * 4)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(seed)
+    picks = [(0, 0), (heads - 1, groups - 1)] + [(int(rng.integers(heads)), int(rng.integers(groups)))
+                                                   for _ in range(14)]
+    for h, g in picks:
+        t0 = h * tokens + g * G
+        m = min(G, tokens - g * G)
+        X = x[t0:t0 + m].cpu().numpy()
+        ref_codes, ref_ranges = O.channel_encode(X, bits, G)
+        got_c = codes[t0 * cfg.codeStride:(t0 + m) * cfg.codeStride].cpu().numpy().tobytes()
+        assert got_c == O.pack_codes(ref_codes, bits), (h, g)
+        r0 = (h * groups + g) * 2 * d
+        got_r = ranges[r0:r0 + 2 * d].cpu().numpy().view(np.uint16)
+        assert np.array_equal(got_r, ref_ranges.view(np.uint16).reshape(-1)), (h, g)
+        ref = O.channel_decode(ref_codes, ref_ranges, bits, G)
+        assert np.array_equal(out[t0:t0 + m].cpu().numpy().view(np.uint32), ref.view(np.uint32)), (h, g)
+    del x, codes, ranges, out
+    torch.cuda.empty_cache()
+
+
+def test_config3_kivi_keys(q):
+    channel_full(q, 8, 32768, 64, 4, 64, 3000)
+
+
+def test_config5_k_share(q):
+    channel_full(q, 32, 131072, 128, 4, 64, 5001)
