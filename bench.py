@@ -64,6 +64,17 @@ class Timer:
         return start.elapsed_time(end) / steps
 
 
+def profiled_traffic(bits: int):
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3 PMC summary, if present."""
+    f = ROOT / "profiles" / "vec_decode_d64_b4_config2_hbm_traffic.md"
+    if bits != 4 or not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def student_t(torch, shape, nu, gen, device):
     """Student-t(nu) = N(0,1) / sqrt(chi2(nu) / nu), generated on the device."""
     z = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
@@ -189,6 +200,7 @@ def main() -> int:
     ms = timer.time(dec_step, args.steps, args.warmup)
     nbytes = n * per_vector_bytes(d, b)
     gbps = nbytes / (ms * 1e-3) / 1e9
+    traffic = profiled_traffic(b)
     # decode of set 0 vs the oracle on a sample (the timed output is the product)
     c0, s0, o0 = sets[0]
     samp = np.random.default_rng(0).choice(n, 4096, replace=False)
@@ -211,9 +223,12 @@ def main() -> int:
         "vectors_per_s": round(n / (ms * 1e-3), 1),
         "pct_of_hbm_peak": round(100 * gbps / PEAK_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / PEAK_GBPS, 4), "traffic": None,
-                     "kernel": f"pitch::vec_decode<64,{b},false>",
-                     "algorithmic_bytes_per_launch": nbytes},
+                     "frac": round(gbps / PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": f"pitch::vec_decode<64, {b}, false>",
+                     "kernel_us_per_launch": round(ms * 1e3, 3),
+                     "algorithmic_bytes_per_launch": nbytes,
+                     "traffic_source": ("profiles/vec_decode_d64_b4_config2_hbm_traffic.md (rocprofv3 FETCH_SIZE x2 "
+                                        "+ WRITE_SIZE x1, scaled by a 1 GiB copy)") if traffic else None},
         "parity": {"encode_code_diffs_near_boundary": gate_diffs, "decode_max_rel_l2": rel},
     }
 

@@ -390,3 +390,38 @@ def test_channel_against_oracle(q, d, G, bits):
     dec = q.decodePerChannel(ours)
     ref = O.channel_decode(codes, ranges, bits, G)
     assert np.array_equal(dec.view(np.uint32), ref.reshape(-1).view(np.uint32))
+
+
+# ----------------------------------------------------------------------------- function-level mirrors
+@pytest.mark.parametrize("method", METHODS)
+@pytest.mark.parametrize("d,bits", [(16, 3), (64, 4), (128, 2), (512, 8)])
+def test_function_mirrors(q, method, d, bits):
+    """pitch_amd.turbo_encode / polar_* / pack_codes / unpack_codes on device tensors (pitch_reference.py:68-132)."""
+    import torch
+    import pitch_amd as P
+    X = gaussian(200, d, d + bits)
+    x = torch.from_numpy(X).to(q.device)
+    codes, scales = P.ENCODERS[method](x, bits, 0x00C0FFEE)
+    ref_codes, ref_scales = O.ENCODERS[method](X.astype(np.float64), bits, 0x00C0FFEE)
+    got = codes.cpu().numpy()
+    check_codes(method, X, bits, 0x00C0FFEE, O.pack_codes(got, bits), O.pack_codes(ref_codes, bits), "mirror")
+    check_scales(scales.cpu().numpy(), np.asarray(ref_scales, np.float32), "mirror")
+    rec = P.DECODERS[method](codes, scales, bits, 0x00C0FFEE).cpu().numpy()
+    ref = O.DECODERS[method](got, scales.cpu().numpy().astype(np.float64), bits, 0x00C0FFEE)
+    assert max_rel_diff(rec, ref, d) < REL_L2_BAR
+    packed = P.pack_codes(codes, bits)
+    assert packed.cpu().numpy().tobytes() == O.pack_codes(got, bits)
+    assert torch.equal(P.unpack_codes(packed, 200, d, bits), codes)
+
+
+@pytest.mark.parametrize("d,bits,G", [(7, 3, 16), (64, 4, 64), (128, 8, 100)])
+def test_channel_function_mirrors(q, d, bits, G):
+    import torch
+    import pitch_amd as P
+    X = offset_keys(150, d, d) if d >= 4 else gaussian(150, d, d)
+    codes, ranges = P.channel_encode(torch.from_numpy(X).to(q.device), bits, G)
+    ref_codes, ref_ranges = O.channel_encode(X, bits, G)
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+    assert np.array_equal(ranges.cpu().numpy().view(np.uint16), ref_ranges.view(np.uint16))
+    dec = P.channel_decode(codes, ranges, bits, G).cpu().numpy()
+    assert np.array_equal(dec.view(np.uint32), O.channel_decode(ref_codes, ref_ranges, bits, G).view(np.uint32))

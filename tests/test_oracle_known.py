@@ -268,3 +268,25 @@ def test_accounting():
     assert O.channel_bits_per_coordinate(128, 4) == 4.5
     assert O.channel_bits_per_coordinate(128, 4, 128) == 4.25
     assert O.channel_group_count(150, 64) == 3
+
+
+# ----------------------------------------------------------------------------- parity band classifiers
+def test_near_boundary_classifiers():
+    """The tolerance band of the parity bar: within 1e-6 (relative) of a decision edge or rounding point."""
+    e = O.turbo_edges(64, 4)
+    k = 11
+    U = np.zeros((1, 64))
+    U[0, :6] = [e[k], e[k] * (1 + 5e-7), e[k] * (1 + 2e-6), 0.0, 0.5 * (e[k] + e[k + 1]), 1e-9]
+    m = O.turbo_near_boundary(U, 4)[0]
+    assert list(m[:6]) == [True, True, False, True, False, True]     # 0 and 1e-9 sit on the zero middle edge
+    t = np.array([3.0, 3.0 + 2e-6, 3.0 + 1e-5, 2.5, 1e7 + 1.0, 0.5])
+    assert list(O._near_integer(t, 1e-6)) == [True, True, False, False, True, False]
+    # a polar pair at the origin counts as on a boundary (its angle is decided by signed zeros)
+    m = O.polar_near_boundary(np.zeros((1, 4)), 3, 0)
+    assert list(m[0]) == [False, True, False, True]           # radius code 0 is clear; the angle of r = 0 is not
+    X = O.unrotate(np.array([[0.6, 0.8, 0.3, 0.1]]), 0)
+    assert not O.polar_near_boundary(X, 3, 0)[0, 1]           # angle 0.927 rad: 1.68 bins + 0.5, far from a tie
+    # KIVI: exact rounding ties are flagged, a value mid-way between ties is not
+    Xk = np.array([[0.0], [1.0], [0.5], [0.25]], np.float32)
+    mk = O.channel_near_boundary(Xk, 2, 4)[:, 0]
+    assert list(mk) == [False, False, True, False]
