@@ -15,6 +15,15 @@
 #ifndef PITCH_DIM
 #error "compile with -DPITCH_DIM=<dim>"
 #endif
+#ifndef PITCH_LPV_EMAX
+#define PITCH_LPV_EMAX 32  // most coordinates one lane of the TurboQuant encoder holds
+#endif
+#ifndef PITCH_ENC_PREFETCH
+#define PITCH_ENC_PREFETCH 1  // 1: the TurboQuant encoder loads block i+1 while it computes block i
+#endif
+#ifndef PITCH_ENC_WAVES
+#define PITCH_ENC_WAVES 2  // waves per SIMD the TurboQuant encoder's register budget must allow
+#endif
 
 namespace pitch {
 namespace {
@@ -42,9 +51,9 @@ __device__ __forceinline__ double div_sqrt_d(double y) {
 
 // TurboQuant quantiser: code = #{edges < u}, searchsorted(edges, u, 'left') (pitch_reference.py:99-101).
 // With a bucket table (gen_tables.py lut_for): j = clamp(floor(u * 2^m + off)), code = c_j + [u > e_j], one
-// 8-byte LDS read per coordinate. Lookups are issued in batches of up to 15 (what the LDS wait counter
-// tracks) before any result is used, so a wave pays one LDS round trip per batch, not per coordinate.
-// Tables too large for LDS use a binary search over the float64 edges.
+// 8-byte LDS read per coordinate (e_j as float32 bits, c_j). Lookups are issued in batches of up to 15 (what
+// the LDS wait counter tracks) before any result is used, so a wave pays one LDS round trip per batch, not per
+// coordinate. Tables too large for LDS use a binary search over the float64 edges.
 template <int D, int B>
 struct TqQuant {
   static constexpr int L = 1 << B;
@@ -53,7 +62,7 @@ struct TqQuant {
   static constexpr int kBatch = 15;
 
   struct Smem {
-    uint2 lut[kLut ? LI.entries : 1];
+    uint2 lut[kLut ? LI.entries : 1];  // (float32 bits of e_j, c_j)
     double edge64[kLut ? 1 : L];
   };
 
@@ -67,79 +76,62 @@ struct TqQuant {
     }
   }
 
+  // Bucket of u = x * us: |u| <= 1 for the coordinates of a rotated unit vector, so the index fits an int.
+  __device__ static int bucket(double x, double us_m) {
+    const int j = (int)__builtin_fma(x, us_m, LI.off);
+    return min(max(j, 0), LI.entries - 1);
+  }
+
+  // Applies f(e, code) to the codes of x[0..N) in order, with u = x * us.
+  template <int N, typename F>
+  __device__ static void for_codes(const Smem& sm, const double (&x)[N], double us, F&& f) {
+    if constexpr (kLut) {
+      const double us_m = us * LI.scale;
+#pragma unroll
+      for (int b0 = 0; b0 < N; b0 += kBatch) {
+        // one 8-byte read per entry through a 32-bit LDS address
+        struct W2 { uint32_t e, c; };
+        typedef __attribute__((address_space(3))) const W2 lds_w2;
+        lds_w2* tab = (lds_w2*)(sm.lut);
+        W2 ent[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          if (b0 + i < N) {
+            const int j = bucket(x[b0 + i], us_m);
+            ent[i] = W2{tab[j].e, tab[j].c};
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i)
+          if (b0 + i < N) f(b0 + i, ent[i].c + (x[b0 + i] * us > (double)__uint_as_float(ent[i].e) ? 1u : 0u));
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const double u = x[e] * us;
+        uint32_t cd = 0;
+#pragma unroll
+        for (int s = L / 2; s >= 1; s >>= 1) cd = (u > sm.edge64[cd + s - 1]) ? cd + s : cd;
+        f(e, cd);
+      }
+    }
+  }
+
   // Codes of x[0..N) packed into words as they are produced: code e at bits [e*B, e*B + B) of w.
   template <int N, int NWORDS>
   __device__ static void codes_packed(const Smem& sm, const double (&x)[N], double us, uint32_t (&w)[NWORDS]) {
 #pragma unroll
     for (int i = 0; i < NWORDS; ++i) w[i] = 0u;
-    auto put = [&](int e, uint32_t cd) {
+    for_codes(sm, x, us, [&](int e, uint32_t cd) {
       const int pos = e * B, wi = pos >> 5, sh = pos & 31;
       w[wi] |= cd << sh;
       if (sh + B > 32) w[wi + 1] |= cd >> (32 - sh);
-    };
-    if constexpr (kLut) {
-      const double us_m = us * LI.scale;
-#pragma unroll
-      for (int b0 = 0; b0 < N; b0 += kBatch) {
-        uint2 ent[kBatch];
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          if (b0 + i < N) {
-            const double tt = __builtin_fmax(__builtin_fma(x[b0 + i], us_m, LI.off), 0.0);
-            uint32_t j = (uint32_t)tt;
-            j = j < (uint32_t)(LI.entries - 1) ? j : (uint32_t)(LI.entries - 1);
-            ent[i] = sm.lut[j];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i)
-          if (b0 + i < N) put(b0 + i, ent[i].y + (x[b0 + i] * us > (double)__uint_as_float(ent[i].x) ? 1u : 0u));
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < N; ++e) {
-        const double u = x[e] * us;
-        uint32_t cd = 0;
-#pragma unroll
-        for (int s = L / 2; s >= 1; s >>= 1) cd = (u > sm.edge64[cd + s - 1]) ? cd + s : cd;
-        put(e, cd);
-      }
-    }
+    });
   }
 
-  // codes of x[0..N) with u = x * us; us_m = us * 2^m (exact scaling)
   template <int N>
   __device__ static void codes(const Smem& sm, const double (&x)[N], double us, uint32_t (&out)[N]) {
-    if constexpr (kLut) {
-      const double us_m = us * LI.scale;
-#pragma unroll
-      for (int b0 = 0; b0 < N; b0 += kBatch) {
-        uint2 ent[kBatch];
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          if (b0 + i < N) {
-            const double tt = __builtin_fmax(__builtin_fma(x[b0 + i], us_m, LI.off), 0.0);
-            uint32_t j = (uint32_t)tt;
-            j = j < (uint32_t)(LI.entries - 1) ? j : (uint32_t)(LI.entries - 1);
-            ent[i] = sm.lut[j];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          if (b0 + i < N)
-            out[b0 + i] = ent[i].y + (x[b0 + i] * us > (double)__uint_as_float(ent[i].x) ? 1u : 0u);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < N; ++e) {
-        const double u = x[e] * us;
-        uint32_t cd = 0;
-#pragma unroll
-        for (int s = L / 2; s >= 1; s >>= 1) cd = (u > sm.edge64[cd + s - 1]) ? cd + s : cd;
-        out[e] = cd;
-      }
-    }
+    for_codes(sm, x, us, [&](int e, uint32_t cd) { out[e] = cd; });
   }
 };
 
@@ -548,7 +540,7 @@ void fill_lane_flips(uint32_t seed, uint32_t* out) {
 // scalars, codes are packed in registers and written back through LDS as contiguous wave stores.
 template <int D>
 struct Lpv {
-  static constexpr int T = D <= 64 ? 1 : 2;
+  static constexpr int T = D <= PITCH_LPV_EMAX ? 1 : D / PITCH_LPV_EMAX;  // lanes per vector
   static constexpr int E = D / T;
   static constexpr int V = 64 / T;        // vectors per wave iteration
   static constexpr int HALF = E + 4;      // staged floats per team lane (padding spreads lanes over the banks)
@@ -586,17 +578,25 @@ template <int D>
 __device__ __forceinline__ void lpv_fetch(const float* in, uint64_t base, uint64_t count, int lane,
                                          f32x4 (&pf)[Lpv<D>::QPL]) {
   using Lp = Lpv<D>;
+  if (base + Lp::V <= count) {
+    // whole block: the wave reads V * D contiguous floats, 1 KB per instruction
+    const float* blk = in + base * D + 4 * lane;
 #pragma unroll
-  for (int i = 0; i < Lp::QPL; ++i) {
-    const int q = lane + 64 * i;
-    const int vq = q / Lp::QPV, pq = q % Lp::QPV;
-    const uint64_t vg = base + vq < count ? base + vq : count - 1;
-    pf[i] = *(const f32x4*)(in + vg * D + 4 * pq);
+    for (int i = 0; i < Lp::QPL; ++i) pf[i] = *(const f32x4*)(blk + 256 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < Lp::QPL; ++i) {
+      const int q = lane + 64 * i;
+      const int vq = q / Lp::QPV, pq = q % Lp::QPV;
+      const uint64_t vg = base + vq < count ? base + vq : count - 1;
+      pf[i] = *(const f32x4*)(in + vg * D + 4 * pq);
+    }
   }
 }
 
 template <int D, int B>
-__global__ __launch_bounds__(64) void tq_encode_lpv(VecArgs p) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(PITCH_ENC_WAVES)))
+void tq_encode_lpv(VecArgs p) {
   using Lp = Lpv<D>;
   constexpr int E = Lp::E, T = Lp::T, V = Lp::V;
   constexpr int L = 1 << B;
@@ -611,40 +611,55 @@ __global__ __launch_bounds__(64) void tq_encode_lpv(VecArgs p) {
   const int lane = threadIdx.x;
   const int t = lane & (T - 1);
   const int vw = lane / T;
+#if PITCH_ENC_PREFETCH
+  // software pipeline: the next block's loads are in flight while this block is computed; the first block's
+  // loads are issued before the table set-up so the two latencies overlap
+  f32x4 pf[Lp::QPL];
+  if ((uint64_t)blockIdx.x * V < p.count) lpv_fetch<D>(p.in, (uint64_t)blockIdx.x * V, p.count, lane, pf);
+#endif
   Q::load(s_q, lane, 64);
+  // Every 16-byte chunk this lane stages holds coordinates 4 * pq .. 4 * pq + 3 with pq = lane % QPV (64 is a
+  // multiple of QPV), so the rotation signs are applied at staging with four fixed sign-bit masks.
+  static_assert(64 % Lp::QPV == 0, "staged chunk positions are fixed per lane");
+  uint32_t smask[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    smask[r] = sign_is_negative(p.seed, (uint32_t)(4 * (lane % Lp::QPV) + r)) ? 0x80000000u : 0u;
   __syncthreads();
-
   for (uint64_t base = (uint64_t)blockIdx.x * V; base < p.count; base += (uint64_t)gridDim.x * V) {
     // stage the wave's block of V vectors in LDS with coalesced loads
     {
+#if !PITCH_ENC_PREFETCH
       f32x4 pf[Lp::QPL];
       lpv_fetch<D>(p.in, base, p.count, lane, pf);
+#endif
 #pragma unroll
       for (int i = 0; i < Lp::QPL; ++i) {
         const int q = lane + 64 * i;
         const int vq = q / Lp::QPV, pq = q % Lp::QPV;
         const int h = (4 * pq) / E, pe = 4 * pq - h * E;
-        *(float4*)(s_in + vq * Lp::STRIDE + h * Lp::HALF + pe) = float4{pf[i].x, pf[i].y, pf[i].z, pf[i].w};
+        *(float4*)(s_in + vq * Lp::STRIDE + h * Lp::HALF + pe) =
+            float4{__uint_as_float(__float_as_uint(pf[i].x) ^ smask[0]), __uint_as_float(__float_as_uint(pf[i].y) ^ smask[1]),
+                   __uint_as_float(__float_as_uint(pf[i].z) ^ smask[2]), __uint_as_float(__float_as_uint(pf[i].w) ^ smask[3])};
       }
+#if PITCH_ENC_PREFETCH
+      const uint64_t nb = base + (uint64_t)gridDim.x * V;
+      if (nb < p.count) lpv_fetch<D>(p.in, nb, p.count, lane, pf);
+#endif
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // this lane's E coordinates c = t * E + e with the rotation signs applied (exact); the sign bits of
-    // coordinates 0..D-1 are wave-uniform kernel arguments (bit c % 32 of word c / 32)
+    // this lane's E coordinates c = t * E + e, signs already applied (exact)
     double x[E];
 #pragma unroll
     for (int k = 0; k < E / 4; ++k) {
       const float4 f = *(const float4*)(s_in + vw * Lp::STRIDE + t * Lp::HALF + 4 * k);
-      const float fv[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int e = 4 * k + r;
-        uint32_t m = (p.lane_flips[e >> 5] >> (e & 31)) << 31;
-        if constexpr (T > 1) m = t ? (p.lane_flips[(E + e) >> 5] >> ((E + e) & 31)) << 31 : m;
-        x[e] = (double)__uint_as_float(__float_as_uint(fv[r]) ^ m);
-      }
+      x[4 * k] = (double)f.x;
+      x[4 * k + 1] = (double)f.y;
+      x[4 * k + 2] = (double)f.z;
+      x[4 * k + 3] = (double)f.w;
     }
 
     // u = H(s * x) / (||x|| sqrt(d)) as in vec_encode (pitch_reference.py:96-98)
@@ -690,10 +705,6 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   VecArgs a = args;
   if constexpr (!POLAR && use_lpv_encoder<D>()) {
     if (encode) {
-      // sign bits of coordinates 0..D-1, wave-uniform in this kernel
-      for (int i = 0; i < 32; ++i) a.lane_flips[i] = 0u;
-      for (int c = 0; c < D; ++c)
-        if (sign_is_negative(a.seed, (uint32_t)c)) a.lane_flips[c >> 5] |= 1u << (c & 31);
       const uint64_t need = (a.count + Lpv<D>::V - 1) / Lpv<D>::V;
       const void* k = (const void*)&tq_encode_lpv<D, B>;
       const uint64_t grid = persistent_grid(k, need, 64);
