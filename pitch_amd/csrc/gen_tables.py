@@ -8,6 +8,8 @@
 * For PolarQuant decode (reference/pitch_reference.py:123-129): per bit width, the radius fractions
   k / (2^b - 1) and the unit vectors (cos, sin)(k / 2^b * 2 * pi), evaluated in float64 with the
   reference's operation order and rounded once to float32.
+* The bucket tables of the TurboQuant encoder (lut_for) and the float32 atan polynomials of the PolarQuant
+  encoder's fast angle path (atan_poly), each checked here against the exact answer.
 
 Usage: python gen_tables.py <codebooks.json> <out.inc>
 """
@@ -78,6 +80,38 @@ def lut_for(edges: np.ndarray, b: int, full: bool = True):
     return scale, off, ent
 
 
+# atan(z) = z * P(z^2) on [0, 1]: polynomial degree per bit width b, and the float32 error bound (rad) each
+# degree must meet. The angle code's t = theta / (2 pi) * 2^b + 0.5 may be off by at most 1e-4 (a third of the
+# encoder's guard band); 1e-4 * 2 pi / 2^b less 6e-7 rad for the other float32 roundings is the budget.
+ATAN_DEG = {2: 4, 3: 4, 4: 5, 5: 5, 6: 6, 7: 6, 8: 7}
+ATAN_MAX_ERR = {4: 4e-5, 5: 6e-6, 6: 1e-6, 7: 2e-7}
+
+
+def atan_eval32(c32, zt):
+    """z * P(z^2) in float32 with fused multiply-adds, as the encoder evaluates it."""
+    zt = np.asarray(zt, np.float32)
+    st = (zt * zt).astype(np.float32)
+    p = np.full_like(st, c32[-1])
+    for c in c32[-2::-1]:
+        p = (p.astype(np.float64) * st + np.float64(c)).astype(np.float32)
+    return (p.astype(np.float64) * zt).astype(np.float32)
+
+
+def atan_poly(deg: int = 7):
+    """Least-squares fit of atan(z) / z as a polynomial of degree deg in s = z^2 over [0, 1] (Chebyshev-spaced
+    and uniform nodes), rounded to float32. The PolarQuant encoder evaluates z * P(z^2) in float32 for its fast
+    angle path; the float32 evaluation error is checked here on a dense grid against ATAN_MAX_ERR[deg]."""
+    z = np.concatenate([np.cos(np.linspace(0, np.pi / 2, 20001)), np.linspace(0, 1, 20001)])
+    s = z * z
+    f = np.where(z > 0, np.arctan(z) / np.where(z > 0, z, 1), 1.0)
+    coef, *_ = np.linalg.lstsq(np.vander(s, deg + 1, increasing=True), f, rcond=None)
+    c32 = coef.astype(np.float32)
+    zt = np.linspace(0, 1, 1000001).astype(np.float32)
+    err = np.abs(atan_eval32(c32, zt).astype(np.float64) - np.arctan(zt.astype(np.float64))).max()
+    assert err < ATAN_MAX_ERR[deg], (deg, err)
+    return c32
+
+
 def main(src: str, dst: str) -> None:
     books = json.loads(open(src).read())
     cb_all, edge_all = [], []
@@ -135,6 +169,14 @@ def main(src: str, dst: str) -> None:
     lines.append(f"static __device__ const float pitch_polar_cos_tab[{len(cos_)}] = {{{_floats(cos_)}}};")
     lines.append(f"static __device__ const float pitch_polar_sin_tab[{len(sin_)}] = {{{_floats(sin_)}}};")
     lines.append("static constexpr int pitch_polar_offset(int bits) { return (1 << bits) - 4; }")
+    # fitted atan polynomials: row deg holds the deg + 1 coefficients of degree deg (zero-padded)
+    rows = []
+    for deg in range(9):
+        c = atan_poly(deg) if deg in ATAN_MAX_ERR else np.zeros(0, np.float32)
+        rows.append("{" + _floats(list(c) + [0.0] * (9 - len(c))) + "}")
+    lines.append(f"static constexpr float pitch_atan_coef[9][9] = {{{','.join(rows)}}};")
+    lines.append("static constexpr int pitch_atan_degree(int bits) { return "
+                 + " : ".join(f"bits == {b} ? {d}" for b, d in ATAN_DEG.items()) + " : 7; }")
     for b in BITS:
         assert poffs[b] == (1 << b) - 4
     open(dst, "w").write("\n".join(lines) + "\n")

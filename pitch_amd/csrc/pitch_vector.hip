@@ -41,6 +41,58 @@ struct DimConst {
 constexpr double kTwoPi = 0x1.921fb54442d18p+2;  // 2 * np.pi
 constexpr double kInvTwoPi = 1.0 / kTwoPi;
 
+// Fast PolarQuant quantisation. A radius or angle code is floor(t) with t = value * levels + 0.5
+// (pitch_reference.py:116-117). The encoder first evaluates t in float32; when t is at least kPolarGuard
+// from an integer, floor(t) is certain and used. Otherwise (and for a pair at the origin) the float64 path
+// that follows the reference's operation order decides. kPolarGuard is about four times the worst float32
+// error of t at b = 8 (radius: under 7e-5; angle: under 1e-4), so only pairs within 3e-4 of a rounding
+// point take the float64 path.
+constexpr float kPolarGuard = 3e-4f;
+
+// theta / (2 pi) in [0, 1] of the direction (a, c) = atan2(c, a) mod 2 pi, in float32: octant reduction and
+// atan(z) = z * P(z^2) on [0, 1] with the least-squares polynomial gen_tables.py fits for bit width B, whose
+// error keeps t = turns * 2^B + 0.5 within 1e-4 of its exact value.
+template <int B>
+__device__ __forceinline__ float angle_turns(float c, float a) {
+  constexpr int DEG = pitch_atan_degree(B);
+  const float ax = __builtin_fabsf(a), ay = __builtin_fabsf(c);
+  const float mx = __builtin_fmaxf(ax, ay), mn = __builtin_fminf(ax, ay);
+  const float z = mn * __builtin_amdgcn_rcpf(mx);
+  const float s = z * z;
+  float poly = pitch_atan_coef[DEG][DEG];
+#pragma unroll
+  for (int i = DEG - 1; i >= 0; --i) poly = __builtin_fmaf(poly, s, pitch_atan_coef[DEG][i]);
+  float at = poly * z;                                   // atan(mn / mx) in [0, pi / 4]
+  if (ay > ax) at = 0x1.921fb6p+0f - at;                 // pi / 2 - at
+  if (a < 0.f) at = 0x1.921fb6p+1f - at;                 // pi - at
+  const float turns = at * 0x1.45f306p-3f;               // / (2 pi), in [0, 0.5]
+  return c < 0.f ? 1.f - turns : turns;
+}
+
+// Radius and angle codes of the pair (a, c) with r2 = a^2 + c^2 in float64, in the reference's order
+// (pitch_reference.py:111-117): floor(r / rmax * (2^B - 1) + 0.5) clipped, floor(theta / 2 pi * 2^B + 0.5)
+// mod 2^B with theta = atan2(c, a) mod 2 pi. Out of line: only pairs near a rounding point come here.
+template <int B>
+__device__ __attribute__((noinline)) uint2 polar_codes_exact(double a, double c, double r2, double safe,
+                                                             double inv) {
+  constexpr int L = 1 << B;
+  constexpr double RL = double(L - 1), N = double(L);
+  double rq = __builtin_floor(div_rn(__builtin_sqrt(r2), safe, inv) * RL + 0.5);
+  rq = rq < 0.0 ? 0.0 : (rq > RL ? RL : rq);
+  double th = atan2(c, a);
+  if (th < 0.0) th += kTwoPi;  // np.mod(theta, 2 pi) for theta in [-pi, 0)
+  const double tq = __builtin_floor(div_rn(th, kTwoPi, kInvTwoPi) * N + 0.5);
+  return make_uint2((uint32_t)rq, (uint32_t)tq & (uint32_t)(L - 1));
+}
+
+// floor(t) when t is at least kPolarGuard from an integer (then ok is left alone), else ok = false.
+__device__ __forceinline__ float guarded_floor(float t, bool& ok) {
+  const float k = __builtin_floorf(t);
+  const float f = t - k;
+  ok = ok && f > kPolarGuard && f < 1.f - kPolarGuard;
+  return k;
+}
+
 // y / sqrt(D) rounded as the reference's division (pitch_reference.py:33).
 template <int D>
 __device__ __forceinline__ double div_sqrt_d(double y) {
@@ -217,34 +269,47 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
       fwht<D, double>(x, t);
       Q::codes(s_q, x, us, code);
     } else {
+      // The codes depend only on the directions and the radii relative to rmax, which the division by sqrt(d)
+      // of rotate() leaves unchanged (up to float64 rounding, far inside the near-boundary band): the pairs are
+      // taken from the unnormalised transform and only rmax is scaled (exactly when d is a power of 4).
       fwht<D, double>(x, t);
-#pragma unroll
-      for (int e = 0; e < G::E; ++e) x[e] = div_sqrt_d<D>(x[e]);
       // pairs (y_2p, y_2p+1) -> radius and angle (pitch_reference.py:111-121)
       constexpr int NP = G::E / 2;
-      double rad[NP];
-      double rmax = 0.0;
+      double r2[NP];
+      double rmax2 = 0.0;
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
         const double a = x[2 * q], c = x[2 * q + 1];
-        rad[q] = __builtin_sqrt(__builtin_fma(a, a, c * c));
-        rmax = rad[q] > rmax ? rad[q] : rmax;
+        r2[q] = __builtin_fma(a, a, c * c);
+        rmax2 = r2[q] > rmax2 ? r2[q] : rmax2;
       }
-      rmax = team_reduce<G::T>(rmax, [](double a, double b) { return a > b ? a : b; });
+      rmax2 = team_reduce<G::T>(rmax2, [](double a, double b) { return a > b ? a : b; });
+      const double rmax = __builtin_sqrt(rmax2);  // = max of the pairs' radii: sqrt is monotone
       const double safe = rmax > 0.0 ? rmax : 1.0;
       const double inv = 1.0 / safe;
-      constexpr double RL = double(L - 1), N = double(L);
+      uint32_t need = 0u;  // bit q: pair q is decided by the float64 path
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
-        double rq = __builtin_floor(div_rn(rad[q], safe, inv) * RL + 0.5);
-        rq = rq < 0.0 ? 0.0 : (rq > RL ? RL : rq);
-        code[2 * q] = (uint32_t)rq;
-        double th = atan2(x[2 * q + 1], x[2 * q]);
-        if (th < 0.0) th += kTwoPi;  // np.mod(theta, 2 pi) for theta in [-pi, 0)
-        const double tq = __builtin_floor(div_rn(th, kTwoPi, kInvTwoPi) * N + 0.5);
-        code[2 * q + 1] = (uint32_t)tq & (uint32_t)(L - 1);
+        // float32 fast path on the pair scaled by 1 / rmax (no overflow or underflow of its square)
+        const float af = (float)(x[2 * q] * inv), cf = (float)(x[2 * q + 1] * inv);
+        const float rf = __builtin_amdgcn_sqrtf(__builtin_fmaf(af, af, cf * cf));
+        bool ok = r2[q] > 0.0;
+        const float kr = guarded_floor(__builtin_fmaf(rf, float(L - 1), 0.5f), ok);
+        const float ka = guarded_floor(__builtin_fmaf(angle_turns<B>(cf, af), float(L), 0.5f), ok);
+        code[2 * q] = (uint32_t)__builtin_fminf(kr, float(L - 1));
+        code[2 * q + 1] = (uint32_t)ka & (uint32_t)(L - 1);
+        need |= ok ? 0u : 1u << q;
       }
-      scale = (float)rmax;
+      // float64 path for the pairs the guard rejected (rare): one shared out-of-line copy
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        if (need & (1u << q)) {
+          const uint2 cc = polar_codes_exact<B>(x[2 * q], x[2 * q + 1], r2[q], safe, inv);
+          code[2 * q] = cc.x;
+          code[2 * q + 1] = cc.y;
+        }
+      }
+      scale = (float)div_sqrt_d<D>(rmax);
     }
 
     if constexpr (kStage) {

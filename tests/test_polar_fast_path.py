@@ -1,0 +1,93 @@
+"""The PolarQuant encoder's float32 fast path, emulated on the CPU (CPU only).
+
+pitch_vector.hip decides each radius and angle code from t = value * levels + 0.5 evaluated in float32
+(angle_turns: octant reduction and the fitted atan polynomial) and keeps floor(t) only when t lies at least
+kPolarGuard = 3e-4 from an integer; otherwise the float64 path decides. This test evaluates the same float32
+steps in numpy (fused multiply-adds as one rounding, the reciprocal correctly rounded, which the hardware's
+1-ulp reciprocal can differ from by one ulp) on rotated K/V-like vectors and checks that
+* the float32 t stays within a third of the guard of the float64 t of the oracle at every bit width,
+* every code the guard accepts equals the oracle's code (pitch_reference.py:109-121),
+* the guard sends only a small fraction of pairs to the float64 path.
+"""
+import importlib.util
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import pitch_oracle as O
+
+ROOT = Path(__file__).resolve().parent.parent
+_spec = importlib.util.spec_from_file_location("gen_tables", ROOT / "pitch_amd" / "csrc" / "gen_tables.py")
+G = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(G)
+GUARD = 3e-4
+f32 = np.float32
+
+
+def _fma32(a, b, c):
+    return (a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)).astype(f32)
+
+
+def angle_turns(c, a, coef):
+    ax, ay = np.abs(a), np.abs(c)
+    mx, mn = np.maximum(ax, ay), np.minimum(ax, ay)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        z = (mn * (f32(1) / mx)).astype(f32)
+    s = (z * z).astype(f32)
+    p = np.full_like(s, coef[-1])
+    for k in coef[-2::-1]:
+        p = _fma32(p, s, np.full_like(s, k))
+    at = (p * z).astype(f32)
+    at = np.where(ay > ax, (f32(np.pi / 2) - at).astype(f32), at)
+    at = np.where(a < 0, (f32(np.pi) - at).astype(f32), at)
+    turns = (at * f32(1 / (2 * np.pi))).astype(f32)
+    return np.where(c < 0, (f32(1) - turns).astype(f32), turns)
+
+
+@pytest.mark.parametrize("d", [16, 64, 128])
+def test_fast_path_matches_oracle(d):
+    rng = np.random.default_rng(d)
+    X = rng.standard_t(5, size=(6000, d)) * np.exp(rng.uniform(-2, 3, size=(6000, 1))) + rng.normal(0, 2, (1, d))
+    X = X.astype(np.float32).astype(np.float64)
+    Y = O.rotate(X, O.DEFAULT_SEED)
+    a, c = Y[:, 0::2], Y[:, 1::2]
+    r, theta = O.polar_parts(X)
+    rmax = r.max(1, keepdims=True)
+    inv = 1.0 / np.where(rmax > 0, rmax, 1.0)
+    af, cf = (a * inv).astype(f32), (c * inv).astype(f32)
+    rf = np.sqrt(_fma32(af, af, (cf * cf).astype(f32))).astype(f32)
+    for b in range(2, 9):
+        L = 2 ** b
+        turns = angle_turns(cf, af, G.atan_poly(G.ATAN_DEG[b]))
+        tr = _fma32(rf, np.full_like(rf, f32(L - 1)), np.full_like(rf, f32(0.5)))
+        ta = _fma32(turns, np.full_like(turns, f32(L)), np.full_like(turns, f32(0.5)))
+        tr_exact = r * inv * (L - 1) + 0.5
+        ta_exact = theta / (2 * np.pi) * L + 0.5
+        # the angle's t is compared modulo L (a direction just below 2 pi wraps to code 0)
+        da = np.abs(ta - ta_exact)
+        da = np.minimum(da, np.abs(da - L))
+        assert np.abs(tr - tr_exact).max() < GUARD / 3, b
+        assert da.max() < GUARD / 3, b
+        fr, fa = tr - np.floor(tr), ta - np.floor(ta)
+        ok = (r > 0) & (fr > GUARD) & (fr < 1 - GUARD) & (fa > GUARD) & (fa < 1 - GUARD)
+        codes, _ = O.polar_encode(X, b)
+        rc = np.minimum(np.floor(tr), L - 1).astype(np.int64)
+        ac = np.floor(ta).astype(np.int64) & (L - 1)
+        assert np.array_equal(rc[ok], codes[:, 0::2][ok]), b
+        assert np.array_equal(ac[ok], codes[:, 1::2][ok]), b
+        assert ok.mean() > 0.99, (b, ok.mean())
+
+
+@pytest.mark.parametrize("b", range(2, 9))
+def test_angle_error_budget(b):
+    """Full circle: the emulated float32 angle keeps t = turns * 2^b + 0.5 within 1e-4 of the exact t."""
+    coef = G.atan_poly(G.ATAN_DEG[b])
+    th = np.linspace(-math.pi, math.pi, 400001)
+    a, c = np.cos(th).astype(f32), np.sin(th).astype(f32)
+    turns = angle_turns(c, a, coef).astype(np.float64)
+    ref = np.mod(np.arctan2(c.astype(np.float64), a.astype(np.float64)), 2 * np.pi) / (2 * np.pi)
+    err = np.abs(turns - ref)
+    err = np.minimum(err, 1 - err)
+    assert err.max() * 2 ** b < 1e-4
