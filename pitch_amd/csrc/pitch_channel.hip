@@ -166,6 +166,137 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
   }
 }
 
+// ------------------------------------------------------------------------------------------- encode, G <= 64
+// One wave per (group, slab of 64 channels), four independent waves per workgroup, no workgroup barriers.
+// Lane (r, c) = (lane / 16, lane % 16) holds channels 4c .. 4c+3 of the slab for tokens r, r + 4, ..., r + 60
+// of the group, so each load instruction reads four token rows of 256 bytes. The channel minima and maxima
+// are reduced across the four token phases with two lane exchanges; every lane then knows the fp16 range of
+// its channels. Codes are staged as bytes in the wave's LDS slice and packed 32 at a time.
+//
+// Quantiser: the reference's t = RN(RN((x - lo) / step) + 0.5) (pitch_reference.py:157, float32) is first
+// taken as RN(RN((x - lo) * RN(1 / step)) + 0.5), which is within 3 float32 ulps of t (under 5e-5 for
+// t < 256). floor(t) is kept when t is at least kKiviGuard from an integer; otherwise the correctly rounded
+// division decides (the library is built with -fhip-fp32-correctly-rounded-divide-sqrt).
+constexpr float kKiviGuard = 1e-4f;
+#ifndef PITCH_KIVI_WAVES
+#define PITCH_KIVI_WAVES 3  // waves per SIMD the per-channel encoder's register budget allows
+#endif
+constexpr int kSlab = 64;        // channels per wave
+constexpr int kGroupMaxW = 64;   // largest group this kernel takes (16 tokens per lane)
+
+template <int B>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KIVI_WAVES))) void chan_encode_w(ChanArgs p) {
+  constexpr int TPL = kGroupMaxW / 4;  // tokens per lane
+  const float levels = (float)((1 << B) - 1);
+  __shared__ __attribute__((aligned(16))) uint8_t s_stage_all[kBlock / 64][kGroupMaxW * kSlab];
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint8_t* s_stage = s_stage_all[wid];
+  const int r = lane >> 4, c = lane & 15;
+  const uint32_t dim = p.dim, G = p.group;
+  const uint32_t slabs = (dim + kSlab - 1) / kSlab;
+  const uint32_t groups = (p.count + G - 1) / G;
+  const uint64_t items = (uint64_t)groups * slabs;
+  const uint64_t waves = (uint64_t)gridDim.x * (kBlock / 64);
+
+  for (uint64_t it = (uint64_t)blockIdx.x * (kBlock / 64) + wid; it < items; it += waves) {
+    const uint32_t g = (uint32_t)(it / slabs), sl = (uint32_t)(it - (uint64_t)g * slabs);
+    const uint32_t first = g * G, n = min(G, p.count - first);
+    const uint32_t ch0 = sl * kSlab, cw = min((uint32_t)kSlab, dim - ch0);  // cw is a multiple of 4
+    const bool cact = 4u * c < cw;
+    const float* src = p.in + (uint64_t)first * dim + ch0 + (cact ? 4u * c : 0u);
+
+    // loads: rows past the group's end re-read its last row (no effect on the range)
+    float4 x[TPL];
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      const uint32_t tk = r + 4u * i;
+      const f32x4 v = *(const f32x4*)(src + (uint64_t)(tk < n ? tk : n - 1) * dim);
+      x[i] = make_float4(v.x, v.y, v.z, v.w);
+    }
+    float4 lo = x[0], hi = x[0];
+#pragma unroll
+    for (int i = 1; i < TPL; ++i) {
+      lo = make_float4(fminf(lo.x, x[i].x), fminf(lo.y, x[i].y), fminf(lo.z, x[i].z), fminf(lo.w, x[i].w));
+      hi = make_float4(fmaxf(hi.x, x[i].x), fmaxf(hi.y, x[i].y), fmaxf(hi.z, x[i].z), fmaxf(hi.w, x[i].w));
+    }
+    float l[4] = {lo.x, lo.y, lo.z, lo.w}, h[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      l[k] = fminf(l[k], __shfl_xor(l[k], 16));
+      h[k] = fmaxf(h[k], __shfl_xor(h[k], 16));
+      l[k] = fminf(l[k], __shfl_xor(l[k], 32));
+      h[k] = fmaxf(h[k], __shfl_xor(h[k], 32));
+    }
+    uint16_t l16[4], h16[4];
+    float bs[4], st[4], inv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      l16[k] = f2h_bits(l[k]);
+      h16[k] = f2h_bits(h[k]);
+      bs[k] = h2f(l16[k]);
+      st[k] = kivi_step(bs[k], h2f(h16[k]), levels);
+      inv[k] = 1.0f / st[k];
+    }
+    if (r == 0 && cact) {
+      uint16_t* rg = p.ranges_out + (uint64_t)g * 2u * dim + ch0 + 4u * c;
+      *(u32x2*)rg = u32x2{(uint32_t)l16[0] | ((uint32_t)l16[1] << 16), (uint32_t)l16[2] | ((uint32_t)l16[3] << 16)};
+      *(u32x2*)(rg + dim) =
+          u32x2{(uint32_t)h16[0] | ((uint32_t)h16[1] << 16), (uint32_t)h16[2] | ((uint32_t)h16[3] << 16)};
+    }
+    // codes clip(floor((x - lo) / step + 0.5), 0, 2^B - 1) (pitch_reference.py:157-158), one byte each in LDS
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      const uint32_t tk = r + 4u * i;
+      if (tk < n && cact) {
+        const float xv[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+        uint32_t word = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float a = xv[k] - bs[k];
+          float q = floorf(a * inv[k] + 0.5f);
+          const float f = (a * inv[k] + 0.5f) - q;
+          if (!(f > kKiviGuard && f < 1.0f - kKiviGuard)) q = floorf(a / st[k] + 0.5f);  // exact division
+          word |= (uint32_t)fminf(fmaxf(q, 0.0f), levels) << (8 * k);
+        }
+        *(uint32_t*)(s_stage + tk * kSlab + 4u * c) = word;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // pack: the slab's codes of a token start at word ch0 * B / 32 of its row (ch0 is a multiple of 64)
+    uint32_t* dst = p.codes_out + (uint64_t)first * p.nwords + ch0 * B / 32u;
+    if ((cw & 31u) == 0u) {
+      const uint32_t gpr = cw >> 5, ng = n * gpr;  // 32-code groups per row, then in all
+      for (uint32_t q = lane; q < ng; q += 64) {
+        const uint32_t tok = q / gpr, gi = q - tok * gpr;
+        const uint4* s4 = (const uint4*)(s_stage + tok * kSlab + 32u * gi);
+        const uint4 q0 = s4[0], q1 = s4[1];
+        const uint32_t bytes[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        uint32_t w[B];
+        pack32<B>(bytes, w);
+        store_words<B>(dst + (uint64_t)tok * p.nwords + gi * B, w);
+      }
+    } else {
+      // last, partial slab of a row whose width is not a multiple of 32: it ends the row
+      const uint32_t wpr = p.nwords - ch0 * B / 32u, nw = n * wpr;
+      for (uint32_t q = lane; q < nw; q += 64) {
+        const uint32_t tok = q / wpr, wi = q - tok * wpr;
+        const uint8_t* row = s_stage + tok * kSlab;
+        uint32_t word = 0u;
+        for (uint32_t i = (32u * wi) / B; i < cw; ++i) {
+          const int sh = (int)(i * B) - (int)(32u * wi);
+          if (sh >= 32) break;
+          const uint32_t cd = row[i];
+          word |= sh >= 0 ? (cd << sh) : (cd >> (-sh));
+        }
+        dst[(uint64_t)tok * p.nwords + wi] = word;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // dim % 4 != 0: one channel per thread for the ranges, one code per thread for quantisation
 template <int B>
 __global__ __launch_bounds__(kBlock) void chan_encode1(ChanArgs p) {
@@ -276,7 +407,11 @@ __global__ __launch_bounds__(kBlock) void chan_decode1(ChanArgs p) {
 template <int B>
 hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
   const bool vec4 = (a.dim & 3u) == 0u;
-  if (encode) {
+  if (encode && vec4 && a.group <= (uint32_t)kGroupMaxW) {
+    const uint64_t items = (((uint64_t)a.count + a.group - 1) / a.group) * ((a.dim + kSlab - 1) / kSlab);
+    const uint64_t grid = persistent_grid((const void*)&chan_encode_w<B>, (items + 3) / 4);
+    hipLaunchKernelGGL((chan_encode_w<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+  } else if (encode) {
     const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;
     const void* k = vec4 ? (const void*)&chan_encode4<B> : (const void*)&chan_encode1<B>;
     const uint64_t grid = persistent_grid(k, groups);

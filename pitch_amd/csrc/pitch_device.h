@@ -74,17 +74,6 @@ __device__ __forceinline__ float fma_t(float a, float b, float c) { return __bui
 __device__ __forceinline__ double fma_t(double a, double b, double c) { return __builtin_fma(a, b, c); }
 
 // ---------------------------------------------------------------------------------------------------
-// Correctly rounded a / b given inv = RN(1 / b): q = RN(a * inv) is within one ulp of a / b, the
-// remainder a - b*q is exact under fma, and RN(q + r * inv) is the correctly rounded quotient
-// (Markstein's theorem). Used where the reference divides in float64 and the result is compared
-// against decision boundaries.
-__device__ __forceinline__ double div_rn(double a, double b, double inv) {
-  const double q = a * inv;
-  const double r = __builtin_fma(-q, b, a);
-  return __builtin_fma(r, inv, q);
-}
-
-// ---------------------------------------------------------------------------------------------------
 // Register layout of one vector of D coordinates spread over a team of T consecutive lanes.
 // Coordinates are grouped into chunks of W (4, or 2 when D == 2); lane t of the team holds chunks
 // j = k*T + t for k = 0 .. CH-1, so consecutive lanes read consecutive 16-byte chunks and every global

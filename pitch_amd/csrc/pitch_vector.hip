@@ -39,7 +39,6 @@ struct DimConst {
 };
 
 constexpr double kTwoPi = 0x1.921fb54442d18p+2;  // 2 * np.pi
-constexpr double kInvTwoPi = 1.0 / kTwoPi;
 
 // Fast PolarQuant quantisation. A radius or angle code is floor(t) with t = value * levels + 0.5
 // (pitch_reference.py:116-117). The encoder first evaluates t in float32; when t is at least kPolarGuard
@@ -73,15 +72,14 @@ __device__ __forceinline__ float angle_turns(float c, float a) {
 // (pitch_reference.py:111-117): floor(r / rmax * (2^B - 1) + 0.5) clipped, floor(theta / 2 pi * 2^B + 0.5)
 // mod 2^B with theta = atan2(c, a) mod 2 pi. Out of line: only pairs near a rounding point come here.
 template <int B>
-__device__ __attribute__((noinline)) uint2 polar_codes_exact(double a, double c, double r2, double safe,
-                                                             double inv) {
+__device__ __attribute__((noinline)) uint2 polar_codes_exact(double a, double c, double r2, double safe) {
   constexpr int L = 1 << B;
   constexpr double RL = double(L - 1), N = double(L);
-  double rq = __builtin_floor(div_rn(__builtin_sqrt(r2), safe, inv) * RL + 0.5);
+  double rq = __builtin_floor(__builtin_sqrt(r2) / safe * RL + 0.5);
   rq = rq < 0.0 ? 0.0 : (rq > RL ? RL : rq);
   double th = atan2(c, a);
   if (th < 0.0) th += kTwoPi;  // np.mod(theta, 2 pi) for theta in [-pi, 0)
-  const double tq = __builtin_floor(div_rn(th, kTwoPi, kInvTwoPi) * N + 0.5);
+  const double tq = __builtin_floor(th / kTwoPi * N + 0.5);
   return make_uint2((uint32_t)rq, (uint32_t)tq & (uint32_t)(L - 1));
 }
 
@@ -98,7 +96,7 @@ template <int D>
 __device__ __forceinline__ double div_sqrt_d(double y) {
   using C = DimConst<D>;
   if constexpr (C::kPow4) return y * C::kInvSqrt;
-  else return div_rn(y, C::kSqrt, C::kInvSqrt);
+  else return y / C::kSqrt;
 }
 
 // TurboQuant quantiser: code = #{edges < u}, searchsorted(edges, u, 'left') (pitch_reference.py:99-101).
@@ -304,7 +302,7 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
         if (need & (1u << q)) {
-          const uint2 cc = polar_codes_exact<B>(x[2 * q], x[2 * q + 1], r2[q], safe, inv);
+          const uint2 cc = polar_codes_exact<B>(x[2 * q], x[2 * q + 1], r2[q], safe);
           code[2 * q] = cc.x;
           code[2 * q + 1] = cc.y;
         }
