@@ -384,6 +384,69 @@ __global__ __launch_bounds__(kBlock) void chan_decode4(ChanArgs p) {
   }
 }
 
+// Group size a multiple of 64: one wave per (group, slab of SW channels), four independent waves per
+// workgroup. A lane loads the fp16 ranges of its four channels once, then for each 64-token chunk of the
+// group issues all its code-word loads before decoding; lane (r, c) holds channels 4c .. 4c+3 of tokens
+// r, r + 64 / TPL, ..., so one store instruction writes 256 / SW whole slab rows of SW * 4 bytes.
+template <int B, int SW>
+__global__ __launch_bounds__(kBlock) void chan_decode_w(ChanArgs p) {
+  constexpr int QW = SW / 4;        // lanes per slab row
+  constexpr int RPI = 64 / QW;      // rows per store instruction
+  constexpr int TPL = 64 / RPI;     // tokens per lane per 64-token chunk
+  constexpr uint32_t kMask = (1u << B) - 1u;
+  const float levels = (float)((1 << B) - 1);
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = lane / QW, c = lane % QW;
+  const uint32_t dim = p.dim, G = p.group;
+  const uint32_t slabs = (dim + SW - 1) / SW;
+  const uint32_t groups = (p.count + G - 1) / G;
+  const uint64_t items = (uint64_t)groups * slabs;
+  const uint64_t waves = (uint64_t)gridDim.x * (kBlock / 64);
+
+  for (uint64_t it = (uint64_t)blockIdx.x * (kBlock / 64) + wid; it < items; it += waves) {
+    const uint32_t g = (uint32_t)(it / slabs), sl = (uint32_t)(it - (uint64_t)g * slabs);
+    const uint32_t first = g * G, n = min(G, p.count - first);
+    const uint32_t ch0 = sl * SW, cw = min((uint32_t)SW, dim - ch0);
+    const bool cact = 4u * c < cw;
+    const uint32_t ch = ch0 + (cact ? 4u * c : 0u);
+    const uint16_t* rg = p.ranges_in + (uint64_t)g * 2u * dim + ch;
+    const u32x2 lw = *(const u32x2*)rg, hw = *(const u32x2*)(rg + dim);
+    const uint16_t l16[4] = {(uint16_t)lw.x, (uint16_t)(lw.x >> 16), (uint16_t)lw.y, (uint16_t)(lw.y >> 16)};
+    const uint16_t h16[4] = {(uint16_t)hw.x, (uint16_t)(hw.x >> 16), (uint16_t)hw.y, (uint16_t)(hw.y >> 16)};
+    float bs[4], st[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      bs[k] = h2f(l16[k]);
+      st[k] = kivi_step(bs[k], h2f(h16[k]), levels);
+    }
+    const uint32_t pos = ch * B, wi = pos >> 5, sh = pos & 31u;
+    const bool straddle = sh + 4u * B > 32u;
+    for (uint32_t t0 = 0; t0 < n; t0 += 64) {
+      const uint32_t* cwp = p.codes_in + (uint64_t)(first + t0) * p.nwords + wi;
+      uint32_t lo[TPL], hi[TPL];
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        const uint32_t tk = t0 + r + RPI * i;
+        const uint32_t tc = (tk < n ? tk : n - 1) - t0;  // rows past the group's end re-read its last row
+        lo[i] = cwp[(uint64_t)tc * p.nwords];
+        hi[i] = straddle ? cwp[(uint64_t)tc * p.nwords + 1] : 0u;
+      }
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        const uint32_t tk = t0 + r + RPI * i;
+        if (tk < n && cact) {
+          const uint32_t bits = __builtin_amdgcn_alignbit(hi[i], lo[i], sh);
+          float o[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) o[k] = (float)((bits >> (B * k)) & kMask) * st[k] + bs[k];
+          __builtin_nontemporal_store(f32x4{o[0], o[1], o[2], o[3]},
+                                      (f32x4*)(p.out + (uint64_t)(first + tk) * dim + ch));
+        }
+      }
+    }
+  }
+}
+
 template <int B>
 __global__ __launch_bounds__(kBlock) void chan_decode1(ChanArgs p) {
   const float levels = (float)((1 << B) - 1);
@@ -417,6 +480,10 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
     const uint64_t grid = persistent_grid(k, groups);
     if (vec4) hipLaunchKernelGGL((chan_encode4<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
     else hipLaunchKernelGGL((chan_encode1<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+  } else if (vec4 && a.group % 64u == 0u) {
+    const uint64_t items = (((uint64_t)a.count + a.group - 1) / a.group) * ((a.dim + kSlab - 1) / kSlab);
+    const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, kSlab>, (items + 3) / 4);
+    hipLaunchKernelGGL((chan_decode_w<B, kSlab>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else if (vec4) {
     const uint32_t P = kBlock / (a.dim >> 2);
     const uint64_t need = ((uint64_t)a.count + P * kDecR - 1) / (P * kDecR);
