@@ -18,6 +18,9 @@
 #ifndef PITCH_LPV_EMAX
 #define PITCH_LPV_EMAX 32  // most coordinates one lane of the TurboQuant encoder holds
 #endif
+#ifndef PITCH_QBATCH
+#define PITCH_QBATCH 15  // bucket-table lookups issued before the first is used (the LDS counter tracks 15)
+#endif
 #ifndef PITCH_ENC_PREFETCH
 #define PITCH_ENC_PREFETCH 1  // 1: the TurboQuant encoder loads block i+1 while it computes block i
 #endif
@@ -109,7 +112,7 @@ struct TqQuant {
   static constexpr int L = 1 << B;
   static constexpr PitchLutInfo LI = pitch_lut_info(ilog2(D), B);
   static constexpr bool kLut = LI.offset >= 0;
-  static constexpr int kBatch = 15;
+  static constexpr int kBatch = PITCH_QBATCH;
 
   struct Smem {
     uint2 lut[kLut ? LI.entries : 1];  // (float32 bits of e_j, c_j)
@@ -220,7 +223,10 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
   constexpr bool kStage = D >= 32;       // codes are packed from LDS in groups of 32
   using Q = TqQuant<D, B>;
   __shared__ typename Q::Smem s_q;
-  __shared__ __attribute__((aligned(16))) uint32_t s_stage[kStage ? G::VPB * D / 4 : 4];
+  // staged code bytes: one row of D / 4 + 4 words per vector, so the team lanes of consecutive vectors write
+  // to different LDS banks and every 32-code group stays 16-byte aligned
+  constexpr int kStageRow = D / 4 + 4;
+  __shared__ __attribute__((aligned(16))) uint32_t s_stage[kStage ? G::VPB * kStageRow : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -314,7 +320,7 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
 #pragma unroll
       for (int k = 0; k < G::CH; ++k) {
         const int c0 = G::W * (k * G::T + t);
-        s_stage[(slot * D + c0) >> 2] = code[4 * k] | (code[4 * k + 1] << 8) | (code[4 * k + 2] << 16) |
+        s_stage[slot * kStageRow + (c0 >> 2)] = code[4 * k] | (code[4 * k + 1] << 8) | (code[4 * k + 2] << 16) |
                                         (code[4 * k + 3] << 24);
       }
     } else {
@@ -343,7 +349,7 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
           const int vs = g / GPV, gi = g % GPV;
           const uint64_t vv = base + vs;
           if (!TAIL || vv < p.count) {
-            const uint4* q = (const uint4*)(s_stage + ((vs * D + 32 * gi) >> 2));
+            const uint4* q = (const uint4*)(s_stage + vs * kStageRow + 8 * gi);
             const uint4 q0 = q[0], q1 = q[1];
             const uint32_t bytes[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
             uint32_t w[B];
@@ -448,6 +454,9 @@ __device__ __forceinline__ void decode_chunk(uint32_t bits, const float* s_tab, 
 #define PITCH_DEC_LDS_STORE 1  // decoded vectors are staged in LDS and stored as contiguous wave blocks
 #endif
 
+#ifndef PITCH_DEC_PAD
+#define PITCH_DEC_PAD 16  // floats of padding per vector in the decoders' LDS output staging
+#endif
 #ifndef PITCH_DEC_WAVES
 #define PITCH_DEC_WAVES 1  // minimum waves per SIMD requested for the decoders (caps their VGPRs)
 #endif
@@ -461,7 +470,9 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   __shared__ __attribute__((aligned(16))) float s_tab[TB::FLOATS];
   // optional LDS staging of the output (D >= 64): each wave writes its vectors back contiguously
   constexpr bool kLdsStore = PITCH_DEC_LDS_STORE && D >= 64 && G::W == 4;
-  constexpr int kVecStride = D + 4;  // floats; padding spreads consecutive vectors over the LDS banks
+  // floats per staged vector: the 16-float padding puts the team lanes of neighbouring vectors, which write
+  // in the same LDS cycle, on disjoint banks
+  constexpr int kVecStride = D + PITCH_DEC_PAD;
   constexpr int kWaveOutFloats = G::V * kVecStride;
   __shared__ __attribute__((aligned(16))) float s_out[kLdsStore ? 4 * kWaveOutFloats : 4];
 
