@@ -36,6 +36,15 @@ extern "C" {
 #define PITCH_METHOD_TURBO 0u
 #define PITCH_METHOD_POLAR 1u
 
+/* Element type of the uncompressed vectors of the *_io entry points: what encode reads and decode writes.
+ * The reference's codec is float32 only ("Inputs and outputs are float32; models that keep caches in fp16 or
+ * bf16 need a conversion", README.md:97). 16-bit inputs are widened to float32 exactly and encoded as the
+ * float32 entry point encodes them; decoded values are the float32 entry point's results rounded to nearest
+ * even (overflow to infinity). Codes, scales and ranges are the same bytes for every element type. */
+#define PITCH_IO_F32 0u
+#define PITCH_IO_F16 1u
+#define PITCH_IO_BF16 2u
+
 /* Default rotation seed, PITCH.defaultSeed = 0x50495443 (Sources/PITCH/PITCH.swift:18). */
 #define PITCH_DEFAULT_SEED 0x50495443u
 
@@ -84,6 +93,14 @@ int pitch_enqueue_encode(const pitch_config_t* config, const void* input, uint64
                          void* scales, uint64_t scales_bytes, uint64_t scales_offset, uint64_t count,
                          void* stream /* hipStream_t; NULL = default stream */);
 
+/* pitch_enqueue_encode with input elements of type io_type (PITCH_IO_*): the input buffer needs
+ * count * dim * element-size bytes after its offset. Extends PITCH.enqueueEncode (Sources/PITCH/PITCH.swift:
+ * 144-153) past its float32-only input (README.md:97). */
+int pitch_enqueue_encode_io(const pitch_config_t* config, uint32_t io_type, const void* input,
+                            uint64_t input_bytes, uint64_t input_offset, void* codes, uint64_t codes_bytes,
+                            uint64_t codes_offset, void* scales, uint64_t scales_bytes, uint64_t scales_offset,
+                            uint64_t count, void* stream);
+
 /* Decodes count vectors into count * dim fp32 values.
  * Replaces PITCH.enqueueDecode(codes:codesOffset:scales:scalesOffset:output:outputOffset:count:config:
  * commandBuffer:) (Sources/PITCH/PITCH.swift:156-165 -> Sources/PITCH/Core/Codec.swift:107-140). */
@@ -91,6 +108,13 @@ int pitch_enqueue_decode(const pitch_config_t* config, const void* codes, uint64
                          uint64_t codes_offset, const void* scales, uint64_t scales_bytes,
                          uint64_t scales_offset, void* output, uint64_t output_bytes, uint64_t output_offset,
                          uint64_t count, void* stream);
+
+/* pitch_enqueue_decode writing elements of type io_type (PITCH_IO_*). Extends PITCH.enqueueDecode
+ * (Sources/PITCH/PITCH.swift:156-165) past its float32-only output (README.md:97). */
+int pitch_enqueue_decode_io(const pitch_config_t* config, uint32_t io_type, const void* codes,
+                            uint64_t codes_bytes, uint64_t codes_offset, const void* scales, uint64_t scales_bytes,
+                            uint64_t scales_offset, void* output, uint64_t output_bytes, uint64_t output_offset,
+                            uint64_t count, void* stream);
 
 /* Encodes count tokens of one head's keys (token-major, dim channels) per channel over groups of
  * group_size tokens: writes count * code_stride bytes of codes and ceil(count / group_size) * range_stride
@@ -103,6 +127,15 @@ int pitch_enqueue_channel_encode(const pitch_channel_config_t* config, const voi
                                  uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count,
                                  void* stream);
 
+/* pitch_enqueue_channel_encode with key elements of type io_type (PITCH_IO_*). Extends
+ * PITCH.enqueuePerChannelEncode (Sources/PITCH/PerChannel.swift:251-260) past float32-only input
+ * (README.md:97). */
+int pitch_enqueue_channel_encode_io(const pitch_channel_config_t* config, uint32_t io_type, const void* input,
+                                    uint64_t input_bytes, uint64_t input_offset, void* codes,
+                                    uint64_t codes_bytes, uint64_t codes_offset, void* ranges,
+                                    uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count,
+                                    void* stream);
+
 /* Decodes count per-channel tokens into count * dim fp32 values.
  * Replaces PITCH.enqueuePerChannelDecode(codes:codesOffset:ranges:rangesOffset:output:outputOffset:count:
  * config:commandBuffer:) (Sources/PITCH/PerChannel.swift:261-270 -> :365-389). */
@@ -111,6 +144,15 @@ int pitch_enqueue_channel_decode(const pitch_channel_config_t* config, const voi
                                  uint64_t ranges_bytes, uint64_t ranges_offset, void* output,
                                  uint64_t output_bytes, uint64_t output_offset, uint64_t count,
                                  void* stream);
+
+/* pitch_enqueue_channel_decode writing elements of type io_type (PITCH_IO_*). Extends
+ * PITCH.enqueuePerChannelDecode (Sources/PITCH/PerChannel.swift:261-270) past float32-only output
+ * (README.md:97). */
+int pitch_enqueue_channel_decode_io(const pitch_channel_config_t* config, uint32_t io_type, const void* codes,
+                                    uint64_t codes_bytes, uint64_t codes_offset, const void* ranges,
+                                    uint64_t ranges_bytes, uint64_t ranges_offset, void* output,
+                                    uint64_t output_bytes, uint64_t output_offset, uint64_t count,
+                                    void* stream);
 
 /* Packs count rows of dim unpacked codes (one uint8 per code, each < 2^bits) into count * code_stride
  * bytes, code i at bits [i * bits, i * bits + bits) of the row's little-endian 32-bit words.

@@ -257,6 +257,60 @@ def channel_bits_per_coordinate(d: int, b: int, G: int = CHANNEL_DEFAULT_GROUP) 
     return code_stride_bytes(d, b) * 8 / d + 32 / G
 
 
+# ----------------------------------------------------------------------------- 16-bit element types
+# The reference reads and writes float32 only and leaves float16 / bfloat16 caches to a conversion by the
+# caller ("Inputs and outputs are float32; models that keep caches in fp16 or bf16 need a conversion",
+# README.md:97). The 16-bit entry points are specified as exactly that conversion: a 16-bit input is widened
+# to float32 (exact for both types) and encoded as float32; a 16-bit output is the float32 decode rounded to
+# nearest even. These helpers state the two roundings; tests/test_io_rounding.py pins them against torch's
+# and numpy's own conversions.
+IO_TYPES = ("float32", "float16", "bfloat16")
+
+
+def bf16_bits(x) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, round to nearest even; NaN -> quiet NaN of the same sign, and a
+    finite value beyond the largest bfloat16 rounds to infinity."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = ((u + np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16))
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    quiet = (u >> np.uint64(16)) | np.uint64(0x40)
+    return np.where(nan, quiet, rounded).astype(np.uint16)
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    """bfloat16 bit patterns -> float32 (exact)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def to_io_bits(x, io: str) -> np.ndarray:
+    """float32 values -> the element type's bit patterns (float32 bits unchanged; 16-bit types RNE)."""
+    x = np.asarray(x, dtype=np.float32)
+    if io == "float32":
+        return x.view(np.uint32)
+    if io == "float16":
+        with np.errstate(over="ignore"):                      # beyond 65504 rounds to infinity
+            return x.astype(np.float16).view(np.uint16)
+    if io == "bfloat16":
+        return bf16_bits(x)
+    raise ValueError(io)
+
+
+def from_io_bits(bits, io: str) -> np.ndarray:
+    """The element type's bit patterns -> float32 (exact)."""
+    if io == "float32":
+        return np.asarray(bits, dtype=np.uint32).view(np.float32)
+    if io == "float16":
+        return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+    if io == "bfloat16":
+        return bf16_to_f32(bits)
+    raise ValueError(io)
+
+
+def round_io(x, io: str) -> np.ndarray:
+    """float32 values rounded to the element type and widened back (what a 16-bit decode holds)."""
+    return from_io_bits(to_io_bits(x, io), io)
+
+
 # ----------------------------------------------------------------------------- boundary classification
 # The parity bar for per-vector codes: a code may differ from the oracle's only at a coordinate whose
 # rotated value lies within REL_BAND of a decision boundary, relative to max(|boundary|, floor). The floor

@@ -20,6 +20,10 @@ ERR_ENCODING_FAILED = -5
 ERR_DECODING_FAILED = -6
 ERR_DEVICE_UNAVAILABLE = -7
 
+IO_F32 = 0    # element types of uncompressed vectors (PITCH_IO_*)
+IO_F16 = 1
+IO_BF16 = 2
+
 
 class PitchConfigC(ctypes.Structure):
     _fields_ = [("method", ctypes.c_uint32), ("dim", ctypes.c_uint32), ("bits", ctypes.c_uint32),
@@ -48,6 +52,14 @@ SIGNATURES = {
                                             _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_channel_decode": (_int, [ctypes.POINTER(PitchChannelConfigC), _vp, _u64, _u64, _vp,
                                             _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_encode_io": (_int, [ctypes.POINTER(PitchConfigC), _u32, _vp, _u64, _u64, _vp, _u64, _u64,
+                                       _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_decode_io": (_int, [ctypes.POINTER(PitchConfigC), _u32, _vp, _u64, _u64, _vp, _u64, _u64,
+                                       _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_channel_encode_io": (_int, [ctypes.POINTER(PitchChannelConfigC), _u32, _vp, _u64, _u64, _vp,
+                                               _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_channel_decode_io": (_int, [ctypes.POINTER(PitchChannelConfigC), _u32, _vp, _u64, _u64, _vp,
+                                               _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_pack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_unpack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
 }

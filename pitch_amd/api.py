@@ -444,6 +444,22 @@ def _buf(t, name: str):
     return t.data_ptr(), t.numel() * t.element_size()
 
 
+_IO_NAMES = {"float32": _lib.IO_F32, "float16": _lib.IO_F16, "bfloat16": _lib.IO_BF16}
+
+
+def _io_type(t, element_type=None) -> int:
+    """Element type code (PITCH_IO_*) of an uncompressed buffer: element_type when given (a torch dtype or
+    "float32" / "float16" / "bfloat16"), else the tensor's own dtype when it is float16 or bfloat16, else
+    float32 (a raw byte buffer holds float32 values, as in the reference's untyped buffers)."""
+    torch = _torch()
+    if element_type is None:
+        return {torch.float16: _lib.IO_F16, torch.bfloat16: _lib.IO_BF16}.get(t.dtype, _lib.IO_F32)
+    name = str(element_type).replace("torch.", "")
+    if name not in _IO_NAMES:
+        raise InvalidInput(f"element type {element_type} is not float32, float16 or bfloat16")
+    return _IO_NAMES[name]
+
+
 def _stream_handle(stream, device=None):
     torch = _torch()
     if stream is None:
@@ -503,13 +519,15 @@ class PITCH:
 
     # ---- helpers
     def _on_device(self, x, name="input"):
+        """Flat device copy of the vectors, keeping a float16 or bfloat16 tensor's (or float16 array's) type."""
         torch = _torch()
         if isinstance(x, torch.Tensor):
             t = x.detach()
-            if t.dtype != torch.float32:
-                raise InvalidInput(f"{name} must be float32")
+            if t.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+                raise InvalidInput(f"{name} must be float32, float16 or bfloat16")
             return t.to(self.device).contiguous().reshape(-1)
-        a = np.asarray(x, dtype=np.float32).reshape(-1)
+        a = np.asarray(x)
+        a = a.reshape(-1) if a.dtype == np.float16 else np.asarray(a, dtype=np.float32).reshape(-1)
         if not (a.flags.c_contiguous and a.flags.writeable):
             a = a.copy()
         return torch.from_numpy(a).to(self.device)
@@ -573,24 +591,36 @@ class PITCH:
 
     # ---- GPU-resident API (PITCH.swift:144-165)
     def enqueueEncode(self, input, codes, scales, count: int, config: QuantConfig, inputOffset: int = 0,
-                      codesOffset: int = 0, scalesOffset: int = 0, stream=None) -> None:
-        """Launches encoding of count vectors; results are valid once the stream reaches this point."""
+                      codesOffset: int = 0, scalesOffset: int = 0, stream=None, elementType=None) -> None:
+        """Launches encoding of count vectors; results are valid once the stream reaches this point. The input's
+        element type is elementType, else the tensor's dtype when float16/bfloat16, else float32."""
         ip, ib = _buf(input, "input")
         cp, cb = _buf(codes, "codes")
         sp, sb = _buf(scales, "scales")
         _check_offsets(inputOffset, codesOffset, scalesOffset)
-        rc = self._lib.pitch_enqueue_encode(ctypes.byref(config._c()), ip, ib, inputOffset, cp, cb, codesOffset,
-                                            sp, sb, scalesOffset, _count(count), _stream_handle(stream, self.device))
+        io = _io_type(input, elementType)
+        args = (ip, ib, inputOffset, cp, cb, codesOffset, sp, sb, scalesOffset, _count(count),
+                _stream_handle(stream, self.device))
+        if io == _lib.IO_F32:
+            rc = self._lib.pitch_enqueue_encode(ctypes.byref(config._c()), *args)
+        else:
+            rc = self._lib.pitch_enqueue_encode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
 
     def enqueueDecode(self, codes, scales, output, count: int, config: QuantConfig, codesOffset: int = 0,
-                      scalesOffset: int = 0, outputOffset: int = 0, stream=None) -> None:
+                      scalesOffset: int = 0, outputOffset: int = 0, stream=None, elementType=None) -> None:
+        """Launches decoding of count vectors into output, whose element type is chosen as for enqueueEncode."""
         cp, cb = _buf(codes, "codes")
         sp, sb = _buf(scales, "scales")
         op, ob = _buf(output, "output")
         _check_offsets(codesOffset, scalesOffset, outputOffset)
-        rc = self._lib.pitch_enqueue_decode(ctypes.byref(config._c()), cp, cb, codesOffset, sp, sb, scalesOffset,
-                                            op, ob, outputOffset, _count(count), _stream_handle(stream, self.device))
+        io = _io_type(output, elementType)
+        args = (cp, cb, codesOffset, sp, sb, scalesOffset, op, ob, outputOffset, _count(count),
+                _stream_handle(stream, self.device))
+        if io == _lib.IO_F32:
+            rc = self._lib.pitch_enqueue_decode(ctypes.byref(config._c()), *args)
+        else:
+            rc = self._lib.pitch_enqueue_decode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
 
     # ---- per-channel (PerChannel.swift:182-290)
@@ -637,26 +667,34 @@ class PITCH:
 
     def enqueuePerChannelEncode(self, input, codes, ranges, count: int, config: ChannelQuantConfig,
                                 inputOffset: int = 0, codesOffset: int = 0, rangesOffset: int = 0,
-                                stream=None) -> None:
+                                stream=None, elementType=None) -> None:
         ip, ib = _buf(input, "input")
         cp, cb = _buf(codes, "codes")
         rp, rb = _buf(ranges, "ranges")
         _check_offsets(inputOffset, codesOffset, rangesOffset)
-        rc = self._lib.pitch_enqueue_channel_encode(ctypes.byref(config._c()), ip, ib, inputOffset, cp, cb,
-                                                    codesOffset, rp, rb, rangesOffset, _count(count),
-                                                    _stream_handle(stream, self.device))
+        io = _io_type(input, elementType)
+        args = (ip, ib, inputOffset, cp, cb, codesOffset, rp, rb, rangesOffset, _count(count),
+                _stream_handle(stream, self.device))
+        if io == _lib.IO_F32:
+            rc = self._lib.pitch_enqueue_channel_encode(ctypes.byref(config._c()), *args)
+        else:
+            rc = self._lib.pitch_enqueue_channel_encode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
 
     def enqueuePerChannelDecode(self, codes, ranges, output, count: int, config: ChannelQuantConfig,
                                 codesOffset: int = 0, rangesOffset: int = 0, outputOffset: int = 0,
-                                stream=None) -> None:
+                                stream=None, elementType=None) -> None:
         cp, cb = _buf(codes, "codes")
         rp, rb = _buf(ranges, "ranges")
         op, ob = _buf(output, "output")
         _check_offsets(codesOffset, rangesOffset, outputOffset)
-        rc = self._lib.pitch_enqueue_channel_decode(ctypes.byref(config._c()), cp, cb, codesOffset, rp, rb,
-                                                    rangesOffset, op, ob, outputOffset, _count(count),
-                                                    _stream_handle(stream, self.device))
+        io = _io_type(output, elementType)
+        args = (cp, cb, codesOffset, rp, rb, rangesOffset, op, ob, outputOffset, _count(count),
+                _stream_handle(stream, self.device))
+        if io == _lib.IO_F32:
+            rc = self._lib.pitch_enqueue_channel_decode(ctypes.byref(config._c()), *args)
+        else:
+            rc = self._lib.pitch_enqueue_channel_decode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
 
 
@@ -728,11 +766,17 @@ def _pitch_for(t) -> PITCH:
     return PITCH(device=t.device)
 
 
+def _io_input(X):
+    """X as a contiguous tensor the kernels read directly: float16 and bfloat16 stay 16-bit."""
+    torch = _torch()
+    return (X if X.dtype in (torch.float16, torch.bfloat16) else X.to(torch.float32)).contiguous()
+
+
 def _encode_fn(method: str, X, b: int, seed: int):
     torch = _torch()
     n, d = X.shape
     cfg = QuantConfig(method, d, b, seed)
-    x = X.to(torch.float32).contiguous()
+    x = _io_input(X)
     codes = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=X.device)
     scales = torch.empty(n, dtype=torch.float32, device=X.device)
     with torch.cuda.device(X.device):
@@ -740,35 +784,36 @@ def _encode_fn(method: str, X, b: int, seed: int):
     return unpack_codes(codes, n, d, b), scales
 
 
-def _decode_fn(method: str, codes, scales, b: int, seed: int):
+def _decode_fn(method: str, codes, scales, b: int, seed: int, dtype=None):
     torch = _torch()
     n, d = codes.shape
     cfg = QuantConfig(method, d, b, seed)
     packed = pack_codes(codes, b)
-    out = torch.empty((n, d), dtype=torch.float32, device=codes.device)
+    out = torch.empty((n, d), dtype=dtype or torch.float32, device=codes.device)
     with torch.cuda.device(codes.device):
         _pitch_for(codes).enqueueDecode(packed, scales.to(torch.float32).contiguous(), out, n, cfg)
     return out
 
 
 def turbo_encode(X, b: int, seed: int = DEFAULT_SEED):
-    """(codes (n, d) int64, norms (n,) float32) (pitch_reference.py:92-102)."""
+    """(codes (n, d) int64, norms (n,) float32) (pitch_reference.py:92-102). X may be float16 or bfloat16: the
+    kernels widen it to float32 exactly."""
     return _encode_fn("turboQuant", X, b, seed)
 
 
-def turbo_decode(codes, norms, b: int, seed: int = DEFAULT_SEED):
-    """pitch_reference.py:104-107."""
-    return _decode_fn("turboQuant", codes, norms, b, seed)
+def turbo_decode(codes, norms, b: int, seed: int = DEFAULT_SEED, dtype=None):
+    """pitch_reference.py:104-107; dtype float16 or bfloat16 rounds the float32 result to nearest even."""
+    return _decode_fn("turboQuant", codes, norms, b, seed, dtype)
 
 
 def polar_encode(X, b: int, seed: int = DEFAULT_SEED):
-    """(codes (n, d) int64, rmax (n,) float32) (pitch_reference.py:109-121)."""
+    """(codes (n, d) int64, rmax (n,) float32) (pitch_reference.py:109-121); X as for turbo_encode."""
     return _encode_fn("polarQuant", X, b, seed)
 
 
-def polar_decode(codes, rmax, b: int, seed: int = DEFAULT_SEED):
-    """pitch_reference.py:123-129."""
-    return _decode_fn("polarQuant", codes, rmax, b, seed)
+def polar_decode(codes, rmax, b: int, seed: int = DEFAULT_SEED, dtype=None):
+    """pitch_reference.py:123-129; dtype as for turbo_decode."""
+    return _decode_fn("polarQuant", codes, rmax, b, seed, dtype)
 
 
 ENCODERS = {"turboQuant": turbo_encode, "polarQuant": polar_encode}
@@ -776,12 +821,13 @@ DECODERS = {"turboQuant": turbo_decode, "polarQuant": polar_decode}
 
 
 def channel_encode(X, b: int, G: int = CHANNEL_DEFAULT_GROUP):
-    """(codes (n, d) int64, ranges (groups, 2, d) float16) (pitch_reference.py:145-162)."""
+    """(codes (n, d) int64, ranges (groups, 2, d) float16) (pitch_reference.py:145-162); X may be float16 or
+    bfloat16."""
     torch = _torch()
     n, d = X.shape
     cfg = ChannelQuantConfig(d, b, G)
     _validate_values(X, FP16_MAX, "per-channel ranges are stored in fp16")
-    x = X.to(torch.float32).contiguous()
+    x = _io_input(X)
     codes = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=X.device)
     ranges = torch.empty(cfg.groupCount(n) * 2 * d, dtype=torch.float16, device=X.device)
     with torch.cuda.device(X.device):
@@ -789,13 +835,13 @@ def channel_encode(X, b: int, G: int = CHANNEL_DEFAULT_GROUP):
     return unpack_codes(codes, n, d, b), ranges.view(cfg.groupCount(n), 2, d)
 
 
-def channel_decode(codes, ranges, b: int, G: int = CHANNEL_DEFAULT_GROUP):
-    """pitch_reference.py:165-174."""
+def channel_decode(codes, ranges, b: int, G: int = CHANNEL_DEFAULT_GROUP, dtype=None):
+    """pitch_reference.py:165-174; dtype float16 or bfloat16 rounds the float32 result to nearest even."""
     torch = _torch()
     n, d = codes.shape
     cfg = ChannelQuantConfig(d, b, G)
     packed = pack_codes(codes, b)
-    out = torch.empty((n, d), dtype=torch.float32, device=codes.device)
+    out = torch.empty((n, d), dtype=dtype or torch.float32, device=codes.device)
     with torch.cuda.device(codes.device):
         _pitch_for(codes).enqueuePerChannelDecode(packed, ranges.to(torch.float16).contiguous(), out, n, cfg)
     return out

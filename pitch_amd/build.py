@@ -3,8 +3,9 @@
     python -m pitch_amd.build        # or pitch_amd.build.build()
 
 Steps: generate csrc/pitch_tables.inc from data/codebooks.json, compile csrc/pitch_vector.hip once per
-dimension (-DPITCH_DIM=2..1024), csrc/pitch_channel.hip and csrc/pitch_abi.cpp, and link the shared library
-next to this file. Object files go to <repo>/_build/.
+dimension and element type of the uncompressed vectors (-DPITCH_DIM=2..1024, -DPITCH_IO=0/1/2 for
+float32/float16/bfloat16), csrc/pitch_channel.hip once per element type and csrc/pitch_abi.cpp, and link the
+shared library next to this file. Object files go to <repo>/_build/.
 """
 from __future__ import annotations
 
@@ -21,6 +22,7 @@ REPO = PKG.parent
 BUILD = REPO / "_build"
 LIB = PKG / "libpitch_amd.so"
 DIMS = [2 ** k for k in range(1, 11)]
+IO_TYPES = [0, 1, 2]   # element type of uncompressed vectors: float32, float16, bfloat16
 ARCH = os.environ.get("PITCH_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -55,15 +57,16 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     _run([sys.executable, str(CSRC / "gen_tables.py"), str(PKG / "data" / "codebooks.json"),
           str(CSRC / "pitch_tables.inc")])
-    units = [(CSRC / "pitch_vector.hip", BUILD / f"vector_d{d}.o", [f"-DPITCH_DIM={d}"]) for d in DIMS]
-    units += [(CSRC / "pitch_channel.hip", BUILD / "channel.o", []),
-              (CSRC / "pitch_abi.cpp", BUILD / "abi.o", [])]
+    units = [(CSRC / "pitch_vector.hip", BUILD / f"vector_d{d}_io{io}.o", [f"-DPITCH_DIM={d}", f"-DPITCH_IO={io}"], d)
+             for d in DIMS for io in IO_TYPES]
+    units += [(CSRC / "pitch_channel.hip", BUILD / f"channel_io{io}.o", [f"-DPITCH_IO={io}"], 512) for io in IO_TYPES]
+    units += [(CSRC / "pitch_abi.cpp", BUILD / "abi.o", [], 0)]
     # largest dims first: they take longest to compile
-    units.sort(key=lambda u: -int(u[2][0].split("=")[1]) if u[2] else 0)
+    units.sort(key=lambda u: -u[3])
     jobs = jobs or min(8, os.cpu_count() or 4)
 
     def compile_one(u):
-        src, obj, extra = u
+        src, obj, extra, _ = u
         cmd = [hipcc, *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)

@@ -110,20 +110,153 @@ T* at(const void* base, uint64_t off) {
   return (T*)((const char*)base + off);
 }
 
-hipError_t launch_vec(uint32_t dim, bool encode, bool polar, int bits, const pitch::VecArgs& a, hipStream_t s) {
-  switch (dim) {
-    case 2: return pitch::launch_vec_d2(encode, polar, bits, a, s);
-    case 4: return pitch::launch_vec_d4(encode, polar, bits, a, s);
-    case 8: return pitch::launch_vec_d8(encode, polar, bits, a, s);
-    case 16: return pitch::launch_vec_d16(encode, polar, bits, a, s);
-    case 32: return pitch::launch_vec_d32(encode, polar, bits, a, s);
-    case 64: return pitch::launch_vec_d64(encode, polar, bits, a, s);
-    case 128: return pitch::launch_vec_d128(encode, polar, bits, a, s);
-    case 256: return pitch::launch_vec_d256(encode, polar, bits, a, s);
-    case 512: return pitch::launch_vec_d512(encode, polar, bits, a, s);
-    case 1024: return pitch::launch_vec_d1024(encode, polar, bits, a, s);
+using VecLaunch = hipError_t (*)(bool, bool, int, const pitch::VecArgs&, hipStream_t);
+
+#define PITCH_VEC_ROW(D) {pitch::launch_vec_d##D##_io0, pitch::launch_vec_d##D##_io1, pitch::launch_vec_d##D##_io2}
+constexpr VecLaunch kVecLaunch[10][3] = {PITCH_VEC_ROW(2),   PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),  PITCH_VEC_ROW(16),
+                                         PITCH_VEC_ROW(32),  PITCH_VEC_ROW(64),  PITCH_VEC_ROW(128), PITCH_VEC_ROW(256),
+                                         PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
+#undef PITCH_VEC_ROW
+
+hipError_t launch_vec(uint32_t dim, uint32_t io, bool encode, bool polar, int bits, const pitch::VecArgs& a,
+                      hipStream_t s) {
+  if (!is_pow2(dim) || dim < 2 || dim > 1024 || io > 2) return hipErrorInvalidValue;
+  int li = 0;
+  while ((2u << li) < dim) ++li;
+  return kVecLaunch[li][io](encode, polar, bits, a, s);
+}
+
+hipError_t launch_channel(uint32_t io, bool encode, int bits, const pitch::ChanArgs& a, hipStream_t s) {
+  switch (io) {
+    case PITCH_IO_F32: return pitch::launch_channel_io0(encode, bits, a, s);
+    case PITCH_IO_F16: return pitch::launch_channel_io1(encode, bits, a, s);
+    case PITCH_IO_BF16: return pitch::launch_channel_io2(encode, bits, a, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Bytes per element of an uncompressed buffer, or 0 for an unknown type.
+uint32_t io_bytes(uint32_t io) { return io == PITCH_IO_F32 ? 4u : (io == PITCH_IO_F16 || io == PITCH_IO_BF16 ? 2u : 0u); }
+
+int check_io(uint32_t io) {
+  if (io_bytes(io) == 0) return fail(PITCH_ERR_INVALID_INPUT, "unknown element type %u", io);
+  return PITCH_OK;
+}
+
+int encode_impl(const pitch_config_t* config, uint32_t io, const void* input, uint64_t input_bytes,
+                uint64_t input_offset, void* codes, uint64_t codes_bytes, uint64_t codes_offset, void* scales,
+                uint64_t scales_bytes, uint64_t scales_offset, uint64_t count, void* stream) {
+  PITCH_TRY(validate_config(config));
+  PITCH_TRY(check_io(io));
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (mul_overflows(count, (uint64_t)dim * 4u)) return fail(PITCH_ERR_INVALID_INPUT, "count is too large");
+  PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * io_bytes(io), "input"));
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
+  PITCH_TRY(check_buffer(scales, scales_bytes, scales_offset, count * 4u, "scales"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(input, dev, "input"));
+  PITCH_TRY(check_device(codes, dev, "codes"));
+  PITCH_TRY(check_device(scales, dev, "scales"));
+  pitch::VecArgs a{};
+  a.in = at<const char>(input, input_offset);
+  a.codes_out = at<uint32_t>(codes, codes_offset);
+  a.scales_out = at<float>(scales, scales_offset);
+  a.count = count;
+  a.seed = config->seed;
+  const hipError_t e = launch_vec(dim, io, true, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
+                                  (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int decode_impl(const pitch_config_t* config, uint32_t io, const void* codes, uint64_t codes_bytes,
+                uint64_t codes_offset, const void* scales, uint64_t scales_bytes, uint64_t scales_offset,
+                void* output, uint64_t output_bytes, uint64_t output_offset, uint64_t count, void* stream) {
+  PITCH_TRY(validate_config(config));
+  PITCH_TRY(check_io(io));
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (mul_overflows(count, (uint64_t)dim * 4u)) return fail(PITCH_ERR_INVALID_INPUT, "count is too large");
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
+  PITCH_TRY(check_buffer(scales, scales_bytes, scales_offset, count * 4u, "scales"));
+  PITCH_TRY(check_buffer(output, output_bytes, output_offset, count * dim * io_bytes(io), "output"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(codes, dev, "codes"));
+  PITCH_TRY(check_device(scales, dev, "scales"));
+  PITCH_TRY(check_device(output, dev, "output"));
+  pitch::VecArgs a{};
+  a.codes_in = at<const uint32_t>(codes, codes_offset);
+  a.scales_in = at<const float>(scales, scales_offset);
+  a.out = at<char>(output, output_offset);
+  a.count = count;
+  a.seed = config->seed;
+  const hipError_t e = launch_vec(dim, io, false, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
+                                  (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int channel_encode_impl(const pitch_channel_config_t* config, uint32_t io, const void* input, uint64_t input_bytes,
+                        uint64_t input_offset, void* codes, uint64_t codes_bytes, uint64_t codes_offset,
+                        void* ranges, uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count, void* stream) {
+  PITCH_TRY(validate_channel_config(config));
+  PITCH_TRY(check_io(io));
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (count > 0xFFFFFFFFull) return fail(PITCH_ERR_INVALID_INPUT, "per-channel count must be below 2^32 tokens");
+  const uint64_t groups = (count + config->group_size - 1) / config->group_size;
+  PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * io_bytes(io), "input"));
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
+  PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(input, dev, "input"));
+  PITCH_TRY(check_device(codes, dev, "codes"));
+  PITCH_TRY(check_device(ranges, dev, "ranges"));
+  pitch::ChanArgs a{};
+  a.in = at<const char>(input, input_offset);
+  a.codes_out = at<uint32_t>(codes, codes_offset);
+  a.ranges_out = at<uint16_t>(ranges, ranges_offset);
+  a.count = (uint32_t)count;
+  a.dim = dim;
+  a.group = config->group_size;
+  a.nwords = cs / 4u;
+  const hipError_t e = launch_channel(io, true, (int)config->bits, a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int channel_decode_impl(const pitch_channel_config_t* config, uint32_t io, const void* codes, uint64_t codes_bytes,
+                        uint64_t codes_offset, const void* ranges, uint64_t ranges_bytes, uint64_t ranges_offset,
+                        void* output, uint64_t output_bytes, uint64_t output_offset, uint64_t count, void* stream) {
+  PITCH_TRY(validate_channel_config(config));
+  PITCH_TRY(check_io(io));
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
+  if (count > 0xFFFFFFFFull) return fail(PITCH_ERR_INVALID_INPUT, "per-channel count must be below 2^32 tokens");
+  const uint64_t groups = (count + config->group_size - 1) / config->group_size;
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
+  PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
+  PITCH_TRY(check_buffer(output, output_bytes, output_offset, count * dim * io_bytes(io), "output"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(codes, dev, "codes"));
+  PITCH_TRY(check_device(ranges, dev, "ranges"));
+  PITCH_TRY(check_device(output, dev, "output"));
+  pitch::ChanArgs a{};
+  a.codes_in = at<const uint32_t>(codes, codes_offset);
+  a.ranges_in = at<const uint16_t>(ranges, ranges_offset);
+  a.out = at<char>(output, output_offset);
+  a.count = (uint32_t)count;
+  a.dim = dim;
+  a.group = config->group_size;
+  a.nwords = cs / 4u;
+  const hipError_t e = launch_channel(io, false, (int)config->bits, a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));
+  return ok();
 }
 
 }  // namespace
@@ -176,7 +309,7 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
 
 extern "C" {
 
-uint32_t pitch_version(void) { return 0x000100u; }
+uint32_t pitch_version(void) { return 0x000200u; }
 
 const char* pitch_last_error(void) { return g_last_error.c_str(); }
 
@@ -203,56 +336,32 @@ int pitch_enqueue_encode(const pitch_config_t* config, const void* input, uint64
                          uint64_t input_offset, void* codes, uint64_t codes_bytes, uint64_t codes_offset,
                          void* scales, uint64_t scales_bytes, uint64_t scales_offset, uint64_t count,
                          void* stream) {
-  PITCH_TRY(validate_config(config));
-  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
-  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
-  if (mul_overflows(count, (uint64_t)dim * 4u)) return fail(PITCH_ERR_INVALID_INPUT, "count is too large");
-  PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * 4u, "input"));
-  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
-  PITCH_TRY(check_buffer(scales, scales_bytes, scales_offset, count * 4u, "scales"));
-  int dev = 0;
-  PITCH_TRY(current_device(&dev));
-  PITCH_TRY(check_device(input, dev, "input"));
-  PITCH_TRY(check_device(codes, dev, "codes"));
-  PITCH_TRY(check_device(scales, dev, "scales"));
-  pitch::VecArgs a{};
-  a.in = at<const float>(input, input_offset);
-  a.codes_out = at<uint32_t>(codes, codes_offset);
-  a.scales_out = at<float>(scales, scales_offset);
-  a.count = count;
-  a.seed = config->seed;
-  const hipError_t e = launch_vec(dim, true, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
-                                  (hipStream_t)stream);
-  if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
-  return ok();
+  return encode_impl(config, PITCH_IO_F32, input, input_bytes, input_offset, codes, codes_bytes, codes_offset,
+                     scales, scales_bytes, scales_offset, count, stream);
+}
+
+int pitch_enqueue_encode_io(const pitch_config_t* config, uint32_t io_type, const void* input,
+                            uint64_t input_bytes, uint64_t input_offset, void* codes, uint64_t codes_bytes,
+                            uint64_t codes_offset, void* scales, uint64_t scales_bytes, uint64_t scales_offset,
+                            uint64_t count, void* stream) {
+  return encode_impl(config, io_type, input, input_bytes, input_offset, codes, codes_bytes, codes_offset, scales,
+                     scales_bytes, scales_offset, count, stream);
 }
 
 int pitch_enqueue_decode(const pitch_config_t* config, const void* codes, uint64_t codes_bytes,
                          uint64_t codes_offset, const void* scales, uint64_t scales_bytes,
                          uint64_t scales_offset, void* output, uint64_t output_bytes, uint64_t output_offset,
                          uint64_t count, void* stream) {
-  PITCH_TRY(validate_config(config));
-  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
-  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
-  if (mul_overflows(count, (uint64_t)dim * 4u)) return fail(PITCH_ERR_INVALID_INPUT, "count is too large");
-  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
-  PITCH_TRY(check_buffer(scales, scales_bytes, scales_offset, count * 4u, "scales"));
-  PITCH_TRY(check_buffer(output, output_bytes, output_offset, count * dim * 4u, "output"));
-  int dev = 0;
-  PITCH_TRY(current_device(&dev));
-  PITCH_TRY(check_device(codes, dev, "codes"));
-  PITCH_TRY(check_device(scales, dev, "scales"));
-  PITCH_TRY(check_device(output, dev, "output"));
-  pitch::VecArgs a{};
-  a.codes_in = at<const uint32_t>(codes, codes_offset);
-  a.scales_in = at<const float>(scales, scales_offset);
-  a.out = at<float>(output, output_offset);
-  a.count = count;
-  a.seed = config->seed;
-  const hipError_t e = launch_vec(dim, false, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
-                                  (hipStream_t)stream);
-  if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));
-  return ok();
+  return decode_impl(config, PITCH_IO_F32, codes, codes_bytes, codes_offset, scales, scales_bytes, scales_offset,
+                     output, output_bytes, output_offset, count, stream);
+}
+
+int pitch_enqueue_decode_io(const pitch_config_t* config, uint32_t io_type, const void* codes,
+                            uint64_t codes_bytes, uint64_t codes_offset, const void* scales, uint64_t scales_bytes,
+                            uint64_t scales_offset, void* output, uint64_t output_bytes, uint64_t output_offset,
+                            uint64_t count, void* stream) {
+  return decode_impl(config, io_type, codes, codes_bytes, codes_offset, scales, scales_bytes, scales_offset,
+                     output, output_bytes, output_offset, count, stream);
 }
 
 int pitch_enqueue_channel_encode(const pitch_channel_config_t* config, const void* input,
@@ -260,30 +369,17 @@ int pitch_enqueue_channel_encode(const pitch_channel_config_t* config, const voi
                                  uint64_t codes_bytes, uint64_t codes_offset, void* ranges,
                                  uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count,
                                  void* stream) {
-  PITCH_TRY(validate_channel_config(config));
-  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
-  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
-  if (count > 0xFFFFFFFFull) return fail(PITCH_ERR_INVALID_INPUT, "per-channel count must be below 2^32 tokens");
-  const uint64_t groups = (count + config->group_size - 1) / config->group_size;
-  PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * 4u, "input"));
-  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
-  PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
-  int dev = 0;
-  PITCH_TRY(current_device(&dev));
-  PITCH_TRY(check_device(input, dev, "input"));
-  PITCH_TRY(check_device(codes, dev, "codes"));
-  PITCH_TRY(check_device(ranges, dev, "ranges"));
-  pitch::ChanArgs a{};
-  a.in = at<const float>(input, input_offset);
-  a.codes_out = at<uint32_t>(codes, codes_offset);
-  a.ranges_out = at<uint16_t>(ranges, ranges_offset);
-  a.count = (uint32_t)count;
-  a.dim = dim;
-  a.group = config->group_size;
-  a.nwords = cs / 4u;
-  const hipError_t e = pitch::launch_channel(true, (int)config->bits, a, (hipStream_t)stream);
-  if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
-  return ok();
+  return channel_encode_impl(config, PITCH_IO_F32, input, input_bytes, input_offset, codes, codes_bytes,
+                             codes_offset, ranges, ranges_bytes, ranges_offset, count, stream);
+}
+
+int pitch_enqueue_channel_encode_io(const pitch_channel_config_t* config, uint32_t io_type, const void* input,
+                                    uint64_t input_bytes, uint64_t input_offset, void* codes,
+                                    uint64_t codes_bytes, uint64_t codes_offset, void* ranges,
+                                    uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count,
+                                    void* stream) {
+  return channel_encode_impl(config, io_type, input, input_bytes, input_offset, codes, codes_bytes, codes_offset,
+                             ranges, ranges_bytes, ranges_offset, count, stream);
 }
 
 int pitch_enqueue_channel_decode(const pitch_channel_config_t* config, const void* codes,
@@ -291,30 +387,17 @@ int pitch_enqueue_channel_decode(const pitch_channel_config_t* config, const voi
                                  uint64_t ranges_bytes, uint64_t ranges_offset, void* output,
                                  uint64_t output_bytes, uint64_t output_offset, uint64_t count,
                                  void* stream) {
-  PITCH_TRY(validate_channel_config(config));
-  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
-  if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
-  if (count > 0xFFFFFFFFull) return fail(PITCH_ERR_INVALID_INPUT, "per-channel count must be below 2^32 tokens");
-  const uint64_t groups = (count + config->group_size - 1) / config->group_size;
-  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
-  PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
-  PITCH_TRY(check_buffer(output, output_bytes, output_offset, count * dim * 4u, "output"));
-  int dev = 0;
-  PITCH_TRY(current_device(&dev));
-  PITCH_TRY(check_device(codes, dev, "codes"));
-  PITCH_TRY(check_device(ranges, dev, "ranges"));
-  PITCH_TRY(check_device(output, dev, "output"));
-  pitch::ChanArgs a{};
-  a.codes_in = at<const uint32_t>(codes, codes_offset);
-  a.ranges_in = at<const uint16_t>(ranges, ranges_offset);
-  a.out = at<float>(output, output_offset);
-  a.count = (uint32_t)count;
-  a.dim = dim;
-  a.group = config->group_size;
-  a.nwords = cs / 4u;
-  const hipError_t e = pitch::launch_channel(false, (int)config->bits, a, (hipStream_t)stream);
-  if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));
-  return ok();
+  return channel_decode_impl(config, PITCH_IO_F32, codes, codes_bytes, codes_offset, ranges, ranges_bytes,
+                             ranges_offset, output, output_bytes, output_offset, count, stream);
+}
+
+int pitch_enqueue_channel_decode_io(const pitch_channel_config_t* config, uint32_t io_type, const void* codes,
+                                    uint64_t codes_bytes, uint64_t codes_offset, const void* ranges,
+                                    uint64_t ranges_bytes, uint64_t ranges_offset, void* output,
+                                    uint64_t output_bytes, uint64_t output_offset, uint64_t count,
+                                    void* stream) {
+  return channel_decode_impl(config, io_type, codes, codes_bytes, codes_offset, ranges, ranges_bytes,
+                             ranges_offset, output, output_bytes, output_offset, count, stream);
 }
 
 static int pack_common(bool pack, uint32_t dim, uint32_t bits, const void* src, uint64_t src_bytes,

@@ -1,4 +1,6 @@
-// Per-channel (KIVI-style) key encode/decode.
+// Per-channel (KIVI-style) key encode/decode for one element type of the uncompressed keys (PITCH_IO: 0 float32,
+// 1 float16, 2 bfloat16; 16-bit keys are widened to float32 exactly, decoded float32 values are rounded to
+// nearest even). The generic pack/unpack kernels are built with PITCH_IO = 0.
 //
 // Semantics follow reference/pitch_reference.py:145-174 bit for bit: per group of G tokens and per channel,
 // float32 min and max rounded to fp16 (round to nearest even), step = (f32(hi16) - f32(lo16)) / (2^b - 1)
@@ -10,6 +12,10 @@
 #include <hip/hip_fp16.h>
 
 #include "pitch_device.h"
+
+#ifndef PITCH_IO
+#define PITCH_IO 0
+#endif
 
 namespace pitch {
 namespace {
@@ -68,7 +74,7 @@ __device__ __forceinline__ void pack_rows(const uint8_t* stage, uint32_t ntok, u
 
 // ------------------------------------------------------------------------------------------- encode
 // dim % 4 == 0: thread (phase pp, column chunk col) owns channels [4col, 4col+4) of tokens pp, pp+P, ...
-template <int B>
+template <int B, int IO>
 __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
   const float levels = (float)((1 << B) - 1);
   __shared__ float4 s_lo[kBlock], s_hi[kBlock];
@@ -84,7 +90,7 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
   for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
     const uint32_t first = g * p.group;
     const uint32_t n = min(p.group, p.count - first);
-    const float* src = p.in + (uint64_t)first * dim + 4u * col;
+    const uint64_t src = (uint64_t)first * dim + 4u * col;  // element index of this thread's first channel
 
     // pass 1: channel minima and maxima over the group
     float4 lo = make_float4(__builtin_inff(), __builtin_inff(), __builtin_inff(), __builtin_inff());
@@ -94,14 +100,18 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
     for (int i = 0; i < kMaxR; ++i) {
       const uint32_t tk = pp + i * P;
       if (active && tk < n) {
-        const f32x4 x = *(const f32x4*)(src + (uint64_t)tk * dim);
-        cache[i] = make_float4(x.x, x.y, x.z, x.w);
+        float v[4];
+        load_elems<IO, 4>(p.in, src + (uint64_t)tk * dim, v);
+        const float4 x = make_float4(v[0], v[1], v[2], v[3]);
+        cache[i] = x;
         lo = make_float4(fminf(lo.x, x.x), fminf(lo.y, x.y), fminf(lo.z, x.z), fminf(lo.w, x.w));
         hi = make_float4(fmaxf(hi.x, x.x), fmaxf(hi.y, x.y), fmaxf(hi.z, x.z), fmaxf(hi.w, x.w));
       }
     }
     for (uint32_t tk = pp + kMaxR * P; active && tk < n; tk += P) {
-      const f32x4 x = *(const f32x4*)(src + (uint64_t)tk * dim);
+      float v[4];
+      load_elems<IO, 4>(p.in, src + (uint64_t)tk * dim, v);
+      const float4 x = make_float4(v[0], v[1], v[2], v[3]);
       lo = make_float4(fminf(lo.x, x.x), fminf(lo.y, x.y), fminf(lo.z, x.z), fminf(lo.w, x.w));
       hi = make_float4(fmaxf(hi.x, x.x), fmaxf(hi.y, x.y), fmaxf(hi.z, x.z), fmaxf(hi.w, x.w));
     }
@@ -150,8 +160,9 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
             if (tb == 0 && (uint32_t)j == i) { x = cache[j]; cached = true; }
           }
           if (!cached) {
-            const f32x4 y = *(const f32x4*)(src + (uint64_t)tk * dim);
-            x = make_float4(y.x, y.y, y.z, y.w);
+            float v[4];
+            load_elems<IO, 4>(p.in, src + (uint64_t)tk * dim, v);
+            x = make_float4(v[0], v[1], v[2], v[3]);
           }
           const uint32_t c = kivi_code(x.x, bs[0], st[0], levels) | (kivi_code(x.y, bs[1], st[1], levels) << 8) |
                              (kivi_code(x.z, bs[2], st[2], levels) << 16) |
@@ -184,7 +195,7 @@ constexpr float kKiviGuard = 1e-4f;
 constexpr int kSlab = 64;        // channels per wave
 constexpr int kGroupMaxW = 64;   // largest group this kernel takes (16 tokens per lane)
 
-template <int B>
+template <int B, int IO>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KIVI_WAVES))) void chan_encode_w(ChanArgs p) {
   constexpr int TPL = kGroupMaxW / 4;  // tokens per lane
   const float levels = (float)((1 << B) - 1);
@@ -203,15 +214,16 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
     const uint32_t first = g * G, n = min(G, p.count - first);
     const uint32_t ch0 = sl * kSlab, cw = min((uint32_t)kSlab, dim - ch0);  // cw is a multiple of 4
     const bool cact = 4u * c < cw;
-    const float* src = p.in + (uint64_t)first * dim + ch0 + (cact ? 4u * c : 0u);
+    const uint64_t src = (uint64_t)first * dim + ch0 + (cact ? 4u * c : 0u);  // element index
 
     // loads: rows past the group's end re-read its last row (no effect on the range)
     float4 x[TPL];
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
       const uint32_t tk = r + 4u * i;
-      const f32x4 v = *(const f32x4*)(src + (uint64_t)(tk < n ? tk : n - 1) * dim);
-      x[i] = make_float4(v.x, v.y, v.z, v.w);
+      float v[4];
+      load_elems<IO, 4>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
+      x[i] = make_float4(v[0], v[1], v[2], v[3]);
     }
     float4 lo = x[0], hi = x[0];
 #pragma unroll
@@ -298,7 +310,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
 }
 
 // dim % 4 != 0: one channel per thread for the ranges, one code per thread for quantisation
-template <int B>
+template <int B, int IO>
 __global__ __launch_bounds__(kBlock) void chan_encode1(ChanArgs p) {
   const float levels = (float)((1 << B) - 1);
   __shared__ float s_base[1024], s_step[1024];
@@ -309,11 +321,13 @@ __global__ __launch_bounds__(kBlock) void chan_encode1(ChanArgs p) {
   for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
     const uint32_t first = g * p.group;
     const uint32_t n = min(p.group, p.count - first);
-    const float* src = p.in + (uint64_t)first * dim;
+    const uint64_t src = (uint64_t)first * dim;  // element index of the group's first token
     for (uint32_t ch = tid; ch < dim; ch += kBlock) {
       float lo = __builtin_inff(), hi = -__builtin_inff();
       for (uint32_t tk = 0; tk < n; ++tk) {
-        const float x = src[(uint64_t)tk * dim + ch];
+        float xv[1];
+        load_elems<IO, 1>(p.in, src + (uint64_t)tk * dim + ch, xv);
+        const float x = xv[0];
         lo = fminf(lo, x);
         hi = fmaxf(hi, x);
       }
@@ -328,7 +342,9 @@ __global__ __launch_bounds__(kBlock) void chan_encode1(ChanArgs p) {
       const uint32_t nt = min(TT, n - tb);
       for (uint32_t it = tid; it < nt * dim; it += kBlock) {
         const uint32_t tok = it / dim, ch = it - tok * dim;
-        s_stage[it] = (uint8_t)kivi_code(src[(uint64_t)(tb + tok) * dim + ch], s_base[ch], s_step[ch], levels);
+        float xv[1];
+        load_elems<IO, 1>(p.in, src + (uint64_t)(tb + tok) * dim + ch, xv);
+        s_stage[it] = (uint8_t)kivi_code(xv[0], s_base[ch], s_step[ch], levels);
       }
       __syncthreads();
       pack_rows<B>(s_stage, nt, dim, p.nwords, p.codes_out + (uint64_t)(first + tb) * p.nwords);
@@ -338,7 +354,7 @@ __global__ __launch_bounds__(kBlock) void chan_encode1(ChanArgs p) {
 }
 
 // ------------------------------------------------------------------------------------------- decode
-template <int B>
+template <int B, int IO>
 __global__ __launch_bounds__(kBlock) void chan_decode4(ChanArgs p) {
   const float levels = (float)((1 << B) - 1);
   constexpr uint32_t kMask = (1u << B) - 1u;
@@ -378,7 +394,7 @@ __global__ __launch_bounds__(kBlock) void chan_decode4(ChanArgs p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[r] = (float)((bits >> (B * r)) & kMask) * st[r] + bs[r];
         // a token row is written by consecutive lanes as whole cache lines: stream it past the caches
-        __builtin_nontemporal_store(f32x4{o[0], o[1], o[2], o[3]}, (f32x4*)(p.out + tk * dim + 4u * col));
+        store_elems<IO, 4>(p.out, tk * dim + 4u * col, o, true);
       }
     }
   }
@@ -388,7 +404,7 @@ __global__ __launch_bounds__(kBlock) void chan_decode4(ChanArgs p) {
 // workgroup. A lane loads the fp16 ranges of its four channels once, then for each 64-token chunk of the
 // group issues all its code-word loads before decoding; lane (r, c) holds channels 4c .. 4c+3 of tokens
 // r, r + 64 / TPL, ..., so one store instruction writes 256 / SW whole slab rows of SW * 4 bytes.
-template <int B, int SW>
+template <int B, int SW, int IO>
 __global__ __launch_bounds__(kBlock) void chan_decode_w(ChanArgs p) {
   constexpr int QW = SW / 4;        // lanes per slab row
   constexpr int RPI = 64 / QW;      // rows per store instruction
@@ -439,15 +455,14 @@ __global__ __launch_bounds__(kBlock) void chan_decode_w(ChanArgs p) {
           float o[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) o[k] = (float)((bits >> (B * k)) & kMask) * st[k] + bs[k];
-          __builtin_nontemporal_store(f32x4{o[0], o[1], o[2], o[3]},
-                                      (f32x4*)(p.out + (uint64_t)(first + tk) * dim + ch));
+          store_elems<IO, 4>(p.out, (uint64_t)(first + tk) * dim + ch, o, true);
         }
       }
     }
   }
 }
 
-template <int B>
+template <int B, int IO>
 __global__ __launch_bounds__(kBlock) void chan_decode1(ChanArgs p) {
   const float levels = (float)((1 << B) - 1);
   constexpr uint32_t kMask = (1u << B) - 1u;
@@ -463,40 +478,42 @@ __global__ __launch_bounds__(kBlock) void chan_decode1(ChanArgs p) {
     const uint32_t pos = ch * B, wi = pos >> 5, sh = pos & 31u;
     const uint32_t lo = cw[wi], hi = (sh + B > 32u) ? cw[wi + 1] : 0u;
     const uint32_t code = __builtin_amdgcn_alignbit(hi, lo, sh) & kMask;
-    p.out[idx] = (float)code * step + base;
+    const float o[1] = {(float)code * step + base};
+    store_elems<IO, 1>(p.out, idx, o, false);
   }
 }
 
-template <int B>
+template <int B, int IO>
 hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
   const bool vec4 = (a.dim & 3u) == 0u;
   if (encode && vec4 && a.group <= (uint32_t)kGroupMaxW) {
     const uint64_t items = (((uint64_t)a.count + a.group - 1) / a.group) * ((a.dim + kSlab - 1) / kSlab);
-    const uint64_t grid = persistent_grid((const void*)&chan_encode_w<B>, (items + 3) / 4);
-    hipLaunchKernelGGL((chan_encode_w<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    const uint64_t grid = persistent_grid((const void*)&chan_encode_w<B, IO>, (items + 3) / 4);
+    hipLaunchKernelGGL((chan_encode_w<B, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else if (encode) {
     const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;
-    const void* k = vec4 ? (const void*)&chan_encode4<B> : (const void*)&chan_encode1<B>;
+    const void* k = vec4 ? (const void*)&chan_encode4<B, IO> : (const void*)&chan_encode1<B, IO>;
     const uint64_t grid = persistent_grid(k, groups);
-    if (vec4) hipLaunchKernelGGL((chan_encode4<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
-    else hipLaunchKernelGGL((chan_encode1<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    if (vec4) hipLaunchKernelGGL((chan_encode4<B, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    else hipLaunchKernelGGL((chan_encode1<B, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else if (vec4 && a.group % 64u == 0u) {
     const uint64_t items = (((uint64_t)a.count + a.group - 1) / a.group) * ((a.dim + kSlab - 1) / kSlab);
-    const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, kSlab>, (items + 3) / 4);
-    hipLaunchKernelGGL((chan_decode_w<B, kSlab>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, kSlab, IO>, (items + 3) / 4);
+    hipLaunchKernelGGL((chan_decode_w<B, kSlab, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else if (vec4) {
     const uint32_t P = kBlock / (a.dim >> 2);
     const uint64_t need = ((uint64_t)a.count + P * kDecR - 1) / (P * kDecR);
-    const uint64_t grid = persistent_grid((const void*)&chan_decode4<B>, need);
-    hipLaunchKernelGGL((chan_decode4<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    const uint64_t grid = persistent_grid((const void*)&chan_decode4<B, IO>, need);
+    hipLaunchKernelGGL((chan_decode4<B, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else {
     const uint64_t need = ((uint64_t)a.count * a.dim + kBlock - 1) / kBlock;
-    const uint64_t grid = persistent_grid((const void*)&chan_decode1<B>, need);
-    hipLaunchKernelGGL((chan_decode1<B>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    const uint64_t grid = persistent_grid((const void*)&chan_decode1<B, IO>, need);
+    hipLaunchKernelGGL((chan_decode1<B, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   }
   return hipGetLastError();
 }
 
+#if PITCH_IO == 0
 // ------------------------------------------------------------------------------------------- pack
 __global__ __launch_bounds__(kBlock) void pack_generic(PackArgs p) {
   const uint32_t nwords = (p.dim * p.bits + 31u) / 32u;
@@ -531,21 +548,27 @@ __global__ __launch_bounds__(kBlock) void unpack_generic(PackArgs p) {
   }
 }
 
+#endif  // PITCH_IO == 0
+
 }  // namespace
 
-hipError_t launch_channel(bool encode, int bits, const ChanArgs& a, hipStream_t s) {
+#define PITCH_CAT2(a, b) a##b
+#define PITCH_CAT(a, b) PITCH_CAT2(a, b)
+
+hipError_t PITCH_CAT(launch_channel_io, PITCH_IO)(bool encode, int bits, const ChanArgs& a, hipStream_t s) {
   switch (bits) {
-    case 2: return launch_b<2>(encode, a, s);
-    case 3: return launch_b<3>(encode, a, s);
-    case 4: return launch_b<4>(encode, a, s);
-    case 5: return launch_b<5>(encode, a, s);
-    case 6: return launch_b<6>(encode, a, s);
-    case 7: return launch_b<7>(encode, a, s);
-    case 8: return launch_b<8>(encode, a, s);
+    case 2: return launch_b<2, PITCH_IO>(encode, a, s);
+    case 3: return launch_b<3, PITCH_IO>(encode, a, s);
+    case 4: return launch_b<4, PITCH_IO>(encode, a, s);
+    case 5: return launch_b<5, PITCH_IO>(encode, a, s);
+    case 6: return launch_b<6, PITCH_IO>(encode, a, s);
+    case 7: return launch_b<7, PITCH_IO>(encode, a, s);
+    case 8: return launch_b<8, PITCH_IO>(encode, a, s);
     default: return hipErrorInvalidValue;
   }
 }
 
+#if PITCH_IO == 0
 hipError_t launch_pack(bool pack, const PackArgs& a, hipStream_t s) {
   if (pack) {
     const uint64_t nwords = (a.dim * a.bits + 31u) / 32u;
@@ -558,5 +581,6 @@ hipError_t launch_pack(bool pack, const PackArgs& a, hipStream_t s) {
   }
   return hipGetLastError();
 }
+#endif
 
 }  // namespace pitch

@@ -148,6 +148,117 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
 typedef uint32_t u32x3 __attribute__((ext_vector_type(3), aligned(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
 
+// ---------------------------------------------------------------------------------------------------
+// Element type of the uncompressed vectors: what encode reads and decode writes. IO = 0 float32, 1 float16,
+// 2 bfloat16 (PITCH_IO_F32 / PITCH_IO_F16 / PITCH_IO_BF16 of the C ABI). 16-bit elements are widened to
+// float32 exactly on load; float32 results are rounded to nearest even on store (v_cvt_pk_f16_f32 /
+// v_cvt_pk_bf16_f32; a value beyond the 16-bit range becomes infinity, as any RNE conversion does).
+template <int IO>
+struct Io {
+  static_assert(IO >= 0 && IO <= 2, "I/O element type");
+  static constexpr int kBytes = IO == 0 ? 4 : 2;
+  static constexpr int kPerChunk = 16 / kBytes;  // elements per 16-byte access
+};
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// The two 16-bit elements of w (element 0 in the low half) as float32.
+template <int IO>
+__device__ __forceinline__ void widen2(uint32_t w, float& a, float& b) {
+  if constexpr (IO == 1) {
+    a = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+    b = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  } else {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xFFFF0000u);
+  }
+}
+
+// (a, b) rounded to the 16-bit type and packed, a in the low half.
+template <int IO>
+__device__ __forceinline__ uint32_t narrow2(float a, float b) {
+  const f32x2 v{a, b};
+  if constexpr (IO == 1) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+template <int IO>
+__device__ __forceinline__ float widen1(uint16_t h) {
+  float a, b;
+  widen2<IO>((uint32_t)h, a, b);
+  return a;
+}
+
+// Loads elements [i, i + N) of an IO-typed array as float32 (N = 1, 2, 4 or 8; one access of N elements).
+template <int IO, int N>
+__device__ __forceinline__ void load_elems(const void* base, uint64_t i, float (&f)[N]) {
+  if constexpr (IO == 0) {
+    const float* p = (const float*)base + i;
+    if constexpr (N == 8) {
+      const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else if constexpr (N == 4) {
+      const f32x4 a = *(const f32x4*)p;
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    } else if constexpr (N == 2) {
+      const f32x2 a = *(const f32x2*)p;
+      f[0] = a.x; f[1] = a.y;
+    } else {
+      f[0] = *p;
+    }
+  } else {
+    const uint16_t* p = (const uint16_t*)base + i;
+    if constexpr (N == 8) {
+      const u32x4 w = *(const u32x4*)p;
+      widen2<IO>(w.x, f[0], f[1]); widen2<IO>(w.y, f[2], f[3]);
+      widen2<IO>(w.z, f[4], f[5]); widen2<IO>(w.w, f[6], f[7]);
+    } else if constexpr (N == 4) {
+      const u32x2 w = *(const u32x2*)p;
+      widen2<IO>(w.x, f[0], f[1]); widen2<IO>(w.y, f[2], f[3]);
+    } else if constexpr (N == 2) {
+      widen2<IO>(*(const uint32_t*)p, f[0], f[1]);
+    } else {
+      f[0] = widen1<IO>(*p);
+    }
+  }
+}
+
+// Stores f[0, N) at elements [i, i + N) of an IO-typed array in one access, non-temporal when NT.
+template <typename V>
+__device__ __forceinline__ void store_v(V* p, V v, bool nt) {
+  if (nt) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+template <int IO, int N>
+__device__ __forceinline__ void store_elems(void* base, uint64_t i, const float (&f)[N], bool nt) {
+  if constexpr (IO == 0) {
+    float* p = (float*)base + i;
+    if constexpr (N == 8) {
+      store_v((f32x4*)p, f32x4{f[0], f[1], f[2], f[3]}, nt);
+      store_v((f32x4*)(p + 4), f32x4{f[4], f[5], f[6], f[7]}, nt);
+    } else if constexpr (N == 4) {
+      store_v((f32x4*)p, f32x4{f[0], f[1], f[2], f[3]}, nt);
+    } else if constexpr (N == 2) {
+      store_v((f32x2*)p, f32x2{f[0], f[1]}, nt);
+    } else {
+      store_v(p, f[0], nt);
+    }
+  } else {
+    uint16_t* p = (uint16_t*)base + i;
+    if constexpr (N == 8) {
+      store_v((u32x4*)p, u32x4{narrow2<IO>(f[0], f[1]), narrow2<IO>(f[2], f[3]), narrow2<IO>(f[4], f[5]),
+                               narrow2<IO>(f[6], f[7])}, nt);
+    } else if constexpr (N == 4) {
+      store_v((u32x2*)p, u32x2{narrow2<IO>(f[0], f[1]), narrow2<IO>(f[2], f[3])}, nt);
+    } else if constexpr (N == 2) {
+      store_v((uint32_t*)p, narrow2<IO>(f[0], f[1]), nt);
+    } else {
+      store_v(p, (uint16_t)(narrow2<IO>(f[0], 0.f) & 0xFFFFu), nt);
+    }
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void store_words(uint32_t* dst, const uint32_t (&w)[N]) {
   int i = 0;

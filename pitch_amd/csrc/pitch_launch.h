@@ -8,12 +8,12 @@ namespace pitch {
 
 // Arguments of one per-vector encode or decode launch (pointers already advanced by the byte offsets).
 struct VecArgs {
-  const float* in;           // encode: count * dim fp32
+  const void* in;            // encode: count * dim elements of the I/O type
   const uint32_t* codes_in;  // decode: count * code_stride bytes
   uint32_t* codes_out;       // encode
   const float* scales_in;    // decode: count fp32
   float* scales_out;         // encode
-  float* out;                // decode: count * dim fp32
+  void* out;                 // decode: count * dim elements of the I/O type
   uint64_t count;
   uint32_t seed;
   uint32_t reserved;
@@ -24,12 +24,12 @@ struct VecArgs {
 
 // Arguments of one per-channel (KIVI) launch.
 struct ChanArgs {
-  const float* in;
+  const void* in;   // encode: count * dim elements of the I/O type
   const uint32_t* codes_in;
   uint32_t* codes_out;
   const uint16_t* ranges_in;  // fp16 bits, [group][min row][max row]
   uint16_t* ranges_out;
-  float* out;
+  void* out;        // decode: count * dim elements of the I/O type
   uint32_t count;   // tokens
   uint32_t dim;     // channels
   uint32_t group;   // tokens per group
@@ -54,8 +54,12 @@ int device_cu_count();
 // but no more than the work needs.
 uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256);
 
+// Per-vector launch for one dimension D and I/O element type IO (0 float32, 1 float16, 2 bfloat16); one
+// object file per (D, IO) defines launch_vec_d<D>_io<IO>.
+#define PITCH_DECLARE_VEC_LAUNCH_IO(D, IO) \
+  hipError_t launch_vec_d##D##_io##IO(bool encode, bool polar, int bits, const VecArgs& a, hipStream_t s);
 #define PITCH_DECLARE_VEC_LAUNCH(D) \
-  hipError_t launch_vec_d##D(bool encode, bool polar, int bits, const VecArgs& a, hipStream_t s);
+  PITCH_DECLARE_VEC_LAUNCH_IO(D, 0) PITCH_DECLARE_VEC_LAUNCH_IO(D, 1) PITCH_DECLARE_VEC_LAUNCH_IO(D, 2)
 PITCH_DECLARE_VEC_LAUNCH(2)
 PITCH_DECLARE_VEC_LAUNCH(4)
 PITCH_DECLARE_VEC_LAUNCH(8)
@@ -67,8 +71,12 @@ PITCH_DECLARE_VEC_LAUNCH(256)
 PITCH_DECLARE_VEC_LAUNCH(512)
 PITCH_DECLARE_VEC_LAUNCH(1024)
 #undef PITCH_DECLARE_VEC_LAUNCH
+#undef PITCH_DECLARE_VEC_LAUNCH_IO
 
-hipError_t launch_channel(bool encode, int bits, const ChanArgs& a, hipStream_t s);
+// Per-channel launch for one I/O element type; one object file per IO defines launch_channel_io<IO>.
+hipError_t launch_channel_io0(bool encode, int bits, const ChanArgs& a, hipStream_t s);
+hipError_t launch_channel_io1(bool encode, int bits, const ChanArgs& a, hipStream_t s);
+hipError_t launch_channel_io2(bool encode, int bits, const ChanArgs& a, hipStream_t s);
 hipError_t launch_pack(bool pack, const PackArgs& a, hipStream_t s);
 
 }  // namespace pitch

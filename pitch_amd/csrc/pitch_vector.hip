@@ -1,4 +1,5 @@
-// Per-vector TurboQuant and single-level PolarQuant encode/decode for one dimension (PITCH_DIM).
+// Per-vector TurboQuant and single-level PolarQuant encode/decode for one dimension (PITCH_DIM) and one
+// element type of the uncompressed vectors (PITCH_IO: 0 float32, 1 float16, 2 bfloat16).
 //
 // Encode follows reference/pitch_reference.py:92-102 (TurboQuant) and :109-121 (PolarQuant); decode
 // :104-107 and :123-129. The Metal kernels they replace are PITCHKernels.metal:114-246, which run one
@@ -14,6 +15,9 @@
 
 #ifndef PITCH_DIM
 #error "compile with -DPITCH_DIM=<dim>"
+#endif
+#ifndef PITCH_IO
+#define PITCH_IO 0
 #endif
 #ifndef PITCH_LPV_EMAX
 #define PITCH_LPV_EMAX 32  // most coordinates one lane of the TurboQuant encoder holds
@@ -188,34 +192,12 @@ struct TqQuant {
   }
 };
 
-template <int W>
-__device__ __forceinline__ void load_chunk(const float* src, float (&f)[W]) {
-  if constexpr (W == 4) {
-    const f32x4 q = *(const f32x4*)src;
-    f[0] = q.x; f[1] = q.y; f[2] = q.z; f[3] = q.w;
-  } else {
-    const f32x2 q = *(const f32x2*)src;
-    f[0] = q.x; f[1] = q.y;
-  }
-}
-
 #ifndef PITCH_NT_STORE
 #define PITCH_NT_STORE 1  // decoded vectors are streamed out with nontemporal stores (0: regular stores)
 #endif
 
-template <int W>
-__device__ __forceinline__ void store_chunk(float* dst, const float (&f)[W]) {
-  if constexpr (W == 4) {
-    if (PITCH_NT_STORE) __builtin_nontemporal_store(f32x4{f[0], f[1], f[2], f[3]}, (f32x4*)dst);
-    else *(f32x4*)dst = f32x4{f[0], f[1], f[2], f[3]};
-  } else {
-    if (PITCH_NT_STORE) __builtin_nontemporal_store(f32x2{f[0], f[1]}, (f32x2*)dst);
-    else *(f32x2*)dst = f32x2{f[0], f[1]};
-  }
-}
-
 // ----------------------------------------------------------------------------------------------------
-template <int D, int B, bool POLAR>
+template <int D, int B, bool POLAR, int IO>
 __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
   using G = Geom<D>;
   constexpr int L = 1 << B;
@@ -246,12 +228,13 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
     constexpr bool TAIL = decltype(tail_c)::value;
     const uint64_t v = base + slot;
     const bool valid = !TAIL || v < p.count;
-    const float* src = p.in + (valid ? v : p.count - 1) * D;
+    const uint64_t row = (valid ? v : p.count - 1) * D;
 
     // load every chunk before converting (all loads in flight together), then apply the signs (exact)
     float f[G::E];
 #pragma unroll
-    for (int k = 0; k < G::CH; ++k) load_chunk<G::W>(src + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
+    for (int k = 0; k < G::CH; ++k)
+      load_elems<IO, G::W>(p.in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
     __builtin_amdgcn_sched_barrier(0);
     double x[G::E];
 #pragma unroll
@@ -461,7 +444,7 @@ __device__ __forceinline__ void decode_chunk(uint32_t bits, const float* s_tab, 
 #define PITCH_DEC_WAVES 1  // minimum waves per SIMD requested for the decoders (caps their VGPRs)
 #endif
 
-template <int D, int B, bool POLAR>
+template <int D, int B, bool POLAR, int IO>
 __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p) {
   using G = Geom<D>;
   using TB = DecTab<B, POLAR, G::W>;
@@ -546,27 +529,29 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       const uint64_t wbase = base + (uint64_t)(tid >> 6) * G::V;  // first vector of this wave
-      float* dstw = p.out + wbase * D;
+      constexpr int K = Io<IO>::kPerChunk;  // elements per 16-byte store
+      static_assert((G::V * D) % (64 * K) == 0, "whole 16-byte stores per lane");
 #pragma unroll
-      for (int m = 0; m < G::V * D / 4 / 64; ++m) {
+      for (int m = 0; m < G::V * D / K / 64; ++m) {
         const int q = lane + 64 * m;          // 16-byte chunk of the wave's output block
-        const int vq = q / (D / 4), cq = q % (D / 4);
-        const float4 val = *(const float4*)(ws + vq * kVecStride + 4 * cq);
-        if (!TAIL || wbase + vq < p.count) {
-          float o[4] = {val.x, val.y, val.z, val.w};
-          store_chunk<4>(dstw + 4 * q, o);
+        const int vq = q / (D / K), cq = q % (D / K);
+        float o[K];
+#pragma unroll
+        for (int h = 0; h < K / 4; ++h) {
+          const float4 val = *(const float4*)(ws + vq * kVecStride + K * cq + 4 * h);
+          o[4 * h] = val.x; o[4 * h + 1] = val.y; o[4 * h + 2] = val.z; o[4 * h + 3] = val.w;
         }
+        if (!TAIL || wbase + vq < p.count) store_elems<IO, K>(p.out, wbase * D + (uint64_t)K * q, o, PITCH_NT_STORE);
       }
       __builtin_amdgcn_wave_barrier();
     } else if (valid) {
-      float* dst = p.out + v * D;
 #pragma unroll
       for (int k = 0; k < G::CH; ++k) {
         float o[G::W];
 #pragma unroll
         for (int r = 0; r < G::W; ++r)
           o[r] = __uint_as_float(__float_as_uint(y[k * G::W + r] * f) ^ flip[k * G::W + r]);
-        store_chunk<G::W>(dst + G::W * (k * G::T + t), o);
+        store_elems<IO, G::W>(p.out, v * D + G::W * (k * G::T + t), o, PITCH_NT_STORE);
       }
     }
   };
@@ -608,19 +593,22 @@ void fill_lane_flips(uint32_t seed, uint32_t* out) {
 
 // ----------------------------------------------------------------------------------------------------
 // Lane-per-vector TurboQuant encoder, D in 8..128. A workgroup is one wave; it stages V = 64 / T vectors per
-// iteration through LDS with coalesced 1 KB loads, after which each team of T lanes (T = 1 up to D = 64, 2 at
-// D = 128) holds its vector as E = D / T contiguous float64 coordinates: coordinate c = t * E + e. The
-// transform runs in registers (plus one DPP exchange at D = 128), the rotation signs are wave-uniform
-// scalars, codes are packed in registers and written back through LDS as contiguous wave stores.
-template <int D>
+// iteration through LDS with coalesced 1 KB loads (16-bit inputs are widened to float32 at staging), after
+// which each team of T lanes (T = 1 up to D = 32, D / 32 above) holds its vector as E = D / T contiguous
+// float64 coordinates: coordinate c = t * E + e. The transform runs in registers plus DPP exchanges across
+// the team, the rotation signs are applied at staging, codes are packed in registers and written back
+// through LDS as contiguous wave stores.
+template <int D, int IO>
 struct Lpv {
   static constexpr int T = D <= PITCH_LPV_EMAX ? 1 : D / PITCH_LPV_EMAX;  // lanes per vector
   static constexpr int E = D / T;
   static constexpr int V = 64 / T;        // vectors per wave iteration
   static constexpr int HALF = E + 4;      // staged floats per team lane (padding spreads lanes over the banks)
   static constexpr int STRIDE = T * HALF; // staged floats per vector
-  static constexpr int QPV = D / 4;       // 16-byte chunks per vector
+  static constexpr int K = Io<IO>::kPerChunk;  // input elements per 16-byte chunk
+  static constexpr int QPV = D / K;       // 16-byte chunks per vector
   static constexpr int QPL = V * QPV / 64;  // 16-byte chunks each lane loads per iteration
+  static_assert(E % K == 0 && (V * QPV) % 64 == 0, "a chunk stays inside one team lane's coordinates");
 };
 
 // Transform of E contiguous coordinates per lane across a team of T lanes (bits >= log2 E cross lanes).
@@ -647,31 +635,46 @@ __device__ __forceinline__ void fwht_contig(F (&v)[E], int t) {
   });
 }
 
-// Coalesced load of the wave's block of V vectors (vectors past the end re-read the last one).
-template <int D>
-__device__ __forceinline__ void lpv_fetch(const float* in, uint64_t base, uint64_t count, int lane,
-                                         f32x4 (&pf)[Lpv<D>::QPL]) {
-  using Lp = Lpv<D>;
+// Coalesced load of the wave's block of V vectors as raw 16-byte chunks (vectors past the end re-read the
+// last one).
+template <int D, int IO>
+__device__ __forceinline__ void lpv_fetch(const void* in, uint64_t base, uint64_t count, int lane,
+                                         u32x4 (&pf)[Lpv<D, IO>::QPL]) {
+  using Lp = Lpv<D, IO>;
+  constexpr int EB = Io<IO>::kBytes;
+  const char* bytes = (const char*)in;
   if (base + Lp::V <= count) {
-    // whole block: the wave reads V * D contiguous floats, 1 KB per instruction
-    const float* blk = in + base * D + 4 * lane;
+    // whole block: the wave reads V * D contiguous elements, 1 KB per instruction
+    const char* blk = bytes + base * D * EB + 16 * lane;
 #pragma unroll
-    for (int i = 0; i < Lp::QPL; ++i) pf[i] = *(const f32x4*)(blk + 256 * i);
+    for (int i = 0; i < Lp::QPL; ++i) pf[i] = *(const u32x4*)(blk + 1024 * i);
   } else {
 #pragma unroll
     for (int i = 0; i < Lp::QPL; ++i) {
       const int q = lane + 64 * i;
       const int vq = q / Lp::QPV, pq = q % Lp::QPV;
       const uint64_t vg = base + vq < count ? base + vq : count - 1;
-      pf[i] = *(const f32x4*)(in + vg * D + 4 * pq);
+      pf[i] = *(const u32x4*)(bytes + (vg * D + Lp::K * pq) * EB);
     }
   }
 }
 
-template <int D, int B>
+// The K elements of a raw 16-byte chunk as float32 (exact).
+template <int IO>
+__device__ __forceinline__ void chunk_floats(const u32x4& w, float (&f)[Io<IO>::kPerChunk]) {
+  if constexpr (IO == 0) {
+    f[0] = __uint_as_float(w.x); f[1] = __uint_as_float(w.y); f[2] = __uint_as_float(w.z); f[3] = __uint_as_float(w.w);
+  } else {
+    widen2<IO>(w.x, f[0], f[1]); widen2<IO>(w.y, f[2], f[3]);
+    widen2<IO>(w.z, f[4], f[5]); widen2<IO>(w.w, f[6], f[7]);
+  }
+}
+
+template <int D, int B, int IO>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(PITCH_ENC_WAVES)))
 void tq_encode_lpv(VecArgs p) {
-  using Lp = Lpv<D>;
+  using Lp = Lpv<D, IO>;
+  constexpr int K = Lp::K;
   constexpr int E = Lp::E, T = Lp::T, V = Lp::V;
   constexpr int L = 1 << B;
   constexpr int NW = (D * B + 31) / 32;   // code words per vector
@@ -688,37 +691,41 @@ void tq_encode_lpv(VecArgs p) {
 #if PITCH_ENC_PREFETCH
   // software pipeline: the next block's loads are in flight while this block is computed; the first block's
   // loads are issued before the table set-up so the two latencies overlap
-  f32x4 pf[Lp::QPL];
-  if ((uint64_t)blockIdx.x * V < p.count) lpv_fetch<D>(p.in, (uint64_t)blockIdx.x * V, p.count, lane, pf);
+  u32x4 pf[Lp::QPL];
+  if ((uint64_t)blockIdx.x * V < p.count) lpv_fetch<D, IO>(p.in, (uint64_t)blockIdx.x * V, p.count, lane, pf);
 #endif
   Q::load(s_q, lane, 64);
-  // Every 16-byte chunk this lane stages holds coordinates 4 * pq .. 4 * pq + 3 with pq = lane % QPV (64 is a
-  // multiple of QPV), so the rotation signs are applied at staging with four fixed sign-bit masks.
+  // Every 16-byte chunk this lane stages holds coordinates K * pq .. K * pq + K - 1 with pq = lane % QPV (64 is
+  // a multiple of QPV), so the rotation signs are applied at staging with K fixed sign-bit masks.
   static_assert(64 % Lp::QPV == 0, "staged chunk positions are fixed per lane");
-  uint32_t smask[4];
+  uint32_t smask[K];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    smask[r] = sign_is_negative(p.seed, (uint32_t)(4 * (lane % Lp::QPV) + r)) ? 0x80000000u : 0u;
+  for (int r = 0; r < K; ++r)
+    smask[r] = sign_is_negative(p.seed, (uint32_t)(K * (lane % Lp::QPV) + r)) ? 0x80000000u : 0u;
   __syncthreads();
   for (uint64_t base = (uint64_t)blockIdx.x * V; base < p.count; base += (uint64_t)gridDim.x * V) {
     // stage the wave's block of V vectors in LDS with coalesced loads
     {
 #if !PITCH_ENC_PREFETCH
-      f32x4 pf[Lp::QPL];
-      lpv_fetch<D>(p.in, base, p.count, lane, pf);
+      u32x4 pf[Lp::QPL];
+      lpv_fetch<D, IO>(p.in, base, p.count, lane, pf);
 #endif
 #pragma unroll
       for (int i = 0; i < Lp::QPL; ++i) {
         const int q = lane + 64 * i;
         const int vq = q / Lp::QPV, pq = q % Lp::QPV;
-        const int h = (4 * pq) / E, pe = 4 * pq - h * E;
-        *(float4*)(s_in + vq * Lp::STRIDE + h * Lp::HALF + pe) =
-            float4{__uint_as_float(__float_as_uint(pf[i].x) ^ smask[0]), __uint_as_float(__float_as_uint(pf[i].y) ^ smask[1]),
-                   __uint_as_float(__float_as_uint(pf[i].z) ^ smask[2]), __uint_as_float(__float_as_uint(pf[i].w) ^ smask[3])};
+        const int h = (K * pq) / E, pe = K * pq - h * E;
+        float fv[K];
+        chunk_floats<IO>(pf[i], fv);
+#pragma unroll
+        for (int r = 0; r < K; ++r) fv[r] = __uint_as_float(__float_as_uint(fv[r]) ^ smask[r]);
+#pragma unroll
+        for (int r = 0; r < K; r += 4)
+          *(float4*)(s_in + vq * Lp::STRIDE + h * Lp::HALF + pe + r) = float4{fv[r], fv[r + 1], fv[r + 2], fv[r + 3]};
       }
 #if PITCH_ENC_PREFETCH
       const uint64_t nb = base + (uint64_t)gridDim.x * V;
-      if (nb < p.count) lpv_fetch<D>(p.in, nb, p.count, lane, pf);
+      if (nb < p.count) lpv_fetch<D, IO>(p.in, nb, p.count, lane, pf);
 #endif
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -773,36 +780,37 @@ void tq_encode_lpv(VecArgs p) {
 template <int D>
 constexpr bool use_lpv_encoder() { return D >= 8 && D <= 128; }
 
-template <int D, int B, bool POLAR>
+template <int D, int B, bool POLAR, int IO>
 hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   using G = Geom<D>;
   VecArgs a = args;
   if constexpr (!POLAR && use_lpv_encoder<D>()) {
     if (encode) {
-      const uint64_t need = (a.count + Lpv<D>::V - 1) / Lpv<D>::V;
-      const void* k = (const void*)&tq_encode_lpv<D, B>;
+      constexpr int V = Lpv<D, IO>::V;
+      const uint64_t need = (a.count + V - 1) / V;
+      const void* k = (const void*)&tq_encode_lpv<D, B, IO>;
       const uint64_t grid = persistent_grid(k, need, 64);
-      hipLaunchKernelGGL((tq_encode_lpv<D, B>), dim3((uint32_t)grid), dim3(64), 0, s, a);
+      hipLaunchKernelGGL((tq_encode_lpv<D, B, IO>), dim3((uint32_t)grid), dim3(64), 0, s, a);
       return hipGetLastError();
     }
   }
   fill_lane_flips<D>(a.seed, a.lane_flips);
   const uint64_t need = (a.count + G::VPB - 1) / G::VPB;
   if (encode) {
-    const void* k = (const void*)&vec_encode<D, B, POLAR>;
+    const void* k = (const void*)&vec_encode<D, B, POLAR, IO>;
     const uint64_t grid = persistent_grid(k, need);
-    hipLaunchKernelGGL((vec_encode<D, B, POLAR>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((vec_encode<D, B, POLAR, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else {
-    const void* k = (const void*)&vec_decode<D, B, POLAR>;
+    const void* k = (const void*)&vec_decode<D, B, POLAR, IO>;
     const uint64_t grid = persistent_grid(k, need);
-    hipLaunchKernelGGL((vec_decode<D, B, POLAR>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((vec_decode<D, B, POLAR, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   }
   return hipGetLastError();
 }
 
 template <int D, int B>
 hipError_t launch_bits(bool encode, bool polar, const VecArgs& a, hipStream_t s) {
-  return polar ? launch_one<D, B, true>(encode, a, s) : launch_one<D, B, false>(encode, a, s);
+  return polar ? launch_one<D, B, true, PITCH_IO>(encode, a, s) : launch_one<D, B, false, PITCH_IO>(encode, a, s);
 }
 
 }  // namespace
@@ -810,8 +818,8 @@ hipError_t launch_bits(bool encode, bool polar, const VecArgs& a, hipStream_t s)
 #define PITCH_CAT2(a, b) a##b
 #define PITCH_CAT(a, b) PITCH_CAT2(a, b)
 
-hipError_t PITCH_CAT(launch_vec_d, PITCH_DIM)(bool encode, bool polar, int bits, const VecArgs& a,
-                                             hipStream_t s) {
+hipError_t PITCH_CAT(PITCH_CAT(PITCH_CAT(launch_vec_d, PITCH_DIM), _io), PITCH_IO)(bool encode, bool polar, int bits,
+                                                                              const VecArgs& a, hipStream_t s) {
   switch (bits) {
     case 2: return launch_bits<PITCH_DIM, 2>(encode, polar, a, s);
     case 3: return launch_bits<PITCH_DIM, 3>(encode, polar, a, s);

@@ -60,7 +60,7 @@ def test_error_codes_match_header():
 
 
 def test_version(lib):
-    assert lib.pitch_version() == 0x000100
+    assert lib.pitch_version() == 0x000200
 
 
 def _config(lib, method, dim, bits, seed=0x50495443):
@@ -224,3 +224,52 @@ def test_pack_entry_validation(lib):
         == _lib.ERR_INVALID_INPUT
     assert lib.pitch_enqueue_pack_codes(64, 4, big.p, 63, 0, big.p, big.nbytes, 0, 1, None) \
         == _lib.ERR_INVALID_INPUT
+
+
+# ----------------------------------------------------------------------------- element-type entry points
+def test_io_entry_points_validate_type_and_sizes(lib):
+    """The *_io entry points size the uncompressed buffer by the element type and reject unknown types before
+    looking for a device."""
+    cfg = _lib.PitchConfigC(0, 64, 4, 0)
+    codes, scales = Host(4 * 32), Host(16)
+
+    def enc(io, inp):
+        return lib.pitch_enqueue_encode_io(ctypes.byref(cfg), io, inp.p, inp.nbytes, 0, codes.p, codes.nbytes, 0,
+                                           scales.p, scales.nbytes, 0, 4, None)
+
+    def dec(io, out):
+        return lib.pitch_enqueue_decode_io(ctypes.byref(cfg), io, codes.p, codes.nbytes, 0, scales.p,
+                                           scales.nbytes, 0, out.p, out.nbytes, 0, 4, None)
+
+    assert enc(3, Host(1024)) == _lib.ERR_INVALID_INPUT and "element type" in _lib.last_error()
+    assert dec(7, Host(1024)) == _lib.ERR_INVALID_INPUT and "element type" in _lib.last_error()
+    for io in (_lib.IO_F16, _lib.IO_BF16):
+        assert enc(io, Host(4 * 64 * 2 - 4)) == _lib.ERR_INVALID_INPUT and "input" in _lib.last_error()
+        assert dec(io, Host(4 * 64 * 2 - 4)) == _lib.ERR_INVALID_INPUT and "output" in _lib.last_error()
+        # exactly count * dim * 2 bytes passes the size check and stops at the device check
+        for rc in (enc(io, Host(4 * 64 * 2)), dec(io, Host(4 * 64 * 2))):
+            assert rc in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+            assert "needs" not in _lib.last_error()
+    assert enc(_lib.IO_F32, Host(4 * 64 * 4 - 4)) == _lib.ERR_INVALID_INPUT
+
+
+def test_channel_io_entry_points_validate_type_and_sizes(lib):
+    cfg = _lib.PitchChannelConfigC(64, 4, 64, 0)
+    n = 100
+    codes, ranges = Host(n * 32), Host(2 * 256)
+
+    def enc(io, inp):
+        return lib.pitch_enqueue_channel_encode_io(ctypes.byref(cfg), io, inp.p, inp.nbytes, 0, codes.p,
+                                                   codes.nbytes, 0, ranges.p, ranges.nbytes, 0, n, None)
+
+    def dec(io, out):
+        return lib.pitch_enqueue_channel_decode_io(ctypes.byref(cfg), io, codes.p, codes.nbytes, 0, ranges.p,
+                                                   ranges.nbytes, 0, out.p, out.nbytes, 0, n, None)
+
+    assert enc(3, Host(n * 256)) == _lib.ERR_INVALID_INPUT and "element type" in _lib.last_error()
+    for io in (_lib.IO_F16, _lib.IO_BF16):
+        assert enc(io, Host(n * 128 - 4)) == _lib.ERR_INVALID_INPUT and "input" in _lib.last_error()
+        assert dec(io, Host(n * 128 - 4)) == _lib.ERR_INVALID_INPUT and "output" in _lib.last_error()
+        for rc in (enc(io, Host(n * 128)), dec(io, Host(n * 128))):
+            assert rc in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+            assert "needs" not in _lib.last_error()
