@@ -35,10 +35,15 @@ def per_vector_bytes(d: int, b: int) -> int:
     return 4 * d + ((d * b + 31) // 32) * 4 + 4
 
 
-def kivi_bytes(n: int, d: int, b: int, G: int, heads: int = 1) -> int:
-    """n tokens per head: n*(4d + codeStride) + groups * 4d per head."""
+def per_vector_bytes16(d: int, b: int) -> int:
+    """Per-vector algorithmic bytes with float16 / bfloat16 vectors: 2d + codeStride + 4."""
+    return 2 * d + ((d * b + 31) // 32) * 4 + 4
+
+
+def kivi_bytes(n: int, d: int, b: int, G: int, heads: int = 1, elem: int = 4) -> int:
+    """n tokens per head: n*(elem*d + codeStride) + groups * 4d per head (elem = bytes per key element)."""
     cs = ((d * b + 31) // 32) * 4
-    return heads * (n * (4 * d + cs) + ((n + G - 1) // G) * 4 * d)
+    return heads * (n * (elem * d + cs) + ((n + G - 1) // G) * 4 * d)
 
 
 class Timer:
@@ -347,6 +352,59 @@ def run_extras(torch, q, P, O, timer, gen, dev, args, x, sets) -> dict:
                                          "vectors_per_s_decode": round(n4 / ms_d * 1e3, 1),
                                          "parity_code_diffs_near_boundary": diffs}
         del c, s_, o
+    out.update(run_io16(torch, q, P, timer, gen, dev, args, x, keys4))
+    return out
+
+
+def run_io16(torch, q, P, timer, gen, dev, args, x, keys4) -> dict:
+    """float16 / bfloat16 cache I/O: config 2 (TurboQuant d=64 b=4), config 4 (TurboQuant d=128 b=4) and
+    config 3 KIVI, encode and decode, with algorithmic bytes counted at 2 bytes per element."""
+    out = {}
+    steps, warm = max(20, args.steps // 4), 5
+    for io in ("float16", "bfloat16"):
+        dt = getattr(torch, io)
+        for label, src, d in (("cfg2_tq_d64_b4", x.reshape(-1, 64), 64), ("cfg4_tq_d128_b4", keys4, 128)):
+            n = src.shape[0]
+            cfg = P.QuantConfig("turboQuant", d, 4)
+            # enough buffer sets that the inputs of consecutive calls never fit the 256 MB Infinity Cache
+            nsets = args.sets if d == 64 else 2
+            bufs = []
+            for s in range(nsets):
+                xs = torch.roll(src, s * 997, 0).to(dt).contiguous()
+                c = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=dev)
+                nm = torch.empty(n, dtype=torch.float32, device=dev)
+                q.enqueueEncode(xs, c, nm, n, cfg)
+                bufs.append((xs, c, nm, torch.empty((n, d), dtype=dt, device=dev)))
+            ms_e = timer.time(lambda i: q.enqueueEncode(bufs[i % nsets][0], bufs[i % nsets][1], bufs[i % nsets][2],
+                                                        n, cfg), steps, warm)
+            ms_d = timer.time(lambda i: q.enqueueDecode(bufs[i % nsets][1], bufs[i % nsets][2], bufs[i % nsets][3],
+                                                        n, cfg), steps, warm)
+            nb = n * per_vector_bytes16(d, 4)
+            out[f"{label}_{io}"] = {"encode_gbps": round(nb / ms_e / 1e6, 1), "decode_gbps": round(nb / ms_d / 1e6, 1),
+                                    "encode_ms": round(ms_e, 5), "decode_ms": round(ms_d, 5),
+                                    "encode_pct_peak": round(nb / ms_e / 1e6 / PEAK_GBPS * 100, 1),
+                                    "decode_pct_peak": round(nb / ms_d / 1e6 / PEAK_GBPS * 100, 1),
+                                    "vectors_per_s_decode": round(n / ms_d * 1e3, 1)}
+            del bufs
+        ccfg = P.ChannelQuantConfig(64, 4, 64)
+        nt = 8 * 32768
+        kb_list = []
+        for s in range(args.sets):
+            kk = biased_keys(torch, gen, dev, 8, 32768, 64).reshape(nt, 64).to(dt).contiguous()
+            c = torch.empty(nt * ccfg.codeStride, dtype=torch.uint8, device=dev)
+            r = torch.empty(ccfg.groupCount(nt) * 2 * 64, dtype=torch.float16, device=dev)
+            kb_list.append((kk, c, r, torch.empty_like(kk)))
+        ms_e = timer.time(lambda i: q.enqueuePerChannelEncode(kb_list[i % len(kb_list)][0], kb_list[i % len(kb_list)][1],
+                                                              kb_list[i % len(kb_list)][2], nt, ccfg), steps, warm)
+        ms_d = timer.time(lambda i: q.enqueuePerChannelDecode(kb_list[i % len(kb_list)][1], kb_list[i % len(kb_list)][2],
+                                                              kb_list[i % len(kb_list)][3], nt, ccfg), steps, warm)
+        kb = kivi_bytes(nt, 64, 4, 64, elem=2)
+        out[f"cfg3_kivi_d64_b4_G64_{io}"] = {"encode_gbps": round(kb / ms_e / 1e6, 1),
+                                              "decode_gbps": round(kb / ms_d / 1e6, 1),
+                                              "encode_ms": round(ms_e, 5), "decode_ms": round(ms_d, 5),
+                                              "encode_pct_peak": round(kb / ms_e / 1e6 / PEAK_GBPS * 100, 1),
+                                              "decode_pct_peak": round(kb / ms_d / 1e6 / PEAK_GBPS * 100, 1)}
+        del kb_list
     return out
 
 
