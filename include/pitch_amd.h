@@ -154,6 +154,43 @@ int pitch_enqueue_channel_decode_io(const pitch_channel_config_t* config, uint32
                                     uint64_t output_bytes, uint64_t output_offset, uint64_t count,
                                     void* stream);
 
+/* Decode-phase attention over compressed caches (no counterpart in the reference: it evaluates attention on
+ * decoded caches, reference/attention_extra.py:70-74, and names decoding inside attention as its next step,
+ * README.md:96). For each of kv_heads KV heads and each of its q_per_kv query heads:
+ *   out = softmax(scale * q . K^T) V,  lse = log sum exp(scale * q . K^T)  (natural log)
+ * where K and V are the decodes of the per-vector codes (TurboQuant or PolarQuant, any bit width 2..8, key and
+ * value configs may differ in method, bits and seed but not in dimension, which must be 64 or 128). The codes
+ * are read as stored; no decoded vector is written. Queries and outputs are fp32 [kv_heads][q_per_kv][dim].
+ * The cache vector of (KV head h, token t) is t * token_stride + h * head_stride, in units of vectors, for
+ * both the codes (code_stride bytes each) and the scales (4 bytes each): a token-major [t][h] cache has
+ * token_stride = number of heads and head_stride = 1; a head-major [h][t] one has token_stride = 1. */
+typedef struct pitch_attention_desc {
+  uint32_t q_per_kv;     /* query heads per KV head (grouped-query attention), 1..8 */
+  uint32_t kv_heads;     /* KV heads in the call, 1..65535 */
+  uint64_t tokens;       /* cached tokens per KV head, >= 1 */
+  uint64_t token_stride; /* vectors between consecutive tokens of one head */
+  uint64_t head_stride;  /* vectors between consecutive KV heads */
+  float scale;           /* softmax scale applied to q . k, e.g. 1 / sqrt(dim) */
+  uint32_t reserved;     /* 0 */
+} pitch_attention_desc_t;
+
+/* Bytes of device workspace pitch_enqueue_attention_decode needs for these arguments. */
+int pitch_attention_workspace_size(const pitch_config_t* key_config, const pitch_config_t* value_config,
+                                   const pitch_attention_desc_t* desc, uint64_t* bytes);
+
+/* Enqueues the attention described above on the stream. lse may be NULL. The workspace (at least
+ * pitch_attention_workspace_size bytes of device memory) must not be used by another call until this one has
+ * completed on the stream. */
+int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch_config_t* value_config,
+                                   const pitch_attention_desc_t* desc, const void* q, uint64_t q_bytes,
+                                   uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,
+                                   uint64_t key_codes_offset, const void* key_scales, uint64_t key_scales_bytes,
+                                   uint64_t key_scales_offset, const void* value_codes, uint64_t value_codes_bytes,
+                                   uint64_t value_codes_offset, const void* value_scales,
+                                   uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output,
+                                   uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes,
+                                   uint64_t lse_offset, void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Packs count rows of dim unpacked codes (one uint8 per code, each < 2^bits) into count * code_stride
  * bytes, code i at bits [i * bits, i * bits + bits) of the row's little-endian 32-bit words.
  * Replaces pack_codes (reference/pitch_reference.py:68-78). */

@@ -311,6 +311,34 @@ def round_io(x, io: str) -> np.ndarray:
     return from_io_bits(to_io_bits(x, io), io)
 
 
+# ----------------------------------------------------------------------------- attention on decoded caches
+def log_softmax(S: np.ndarray) -> np.ndarray:
+    """Row-wise log-softmax, float64. reference/attention_eval.py:31-33."""
+    m = S.max(axis=-1, keepdims=True)
+    return S - m - np.log(np.exp(S - m).sum(axis=-1, keepdims=True))
+
+
+def attend(Q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float):
+    """Attention of queries Q (m, d) over keys K (T, d) and values V (T, d), float64: S = Q K^T * scale,
+    log-softmax, exp(lp) V. reference/attention_extra.py:70-74 without the causal mask, since a decode-step query
+    sees every cached token. Returns (O (m, d), lse (m,)) with lse = log sum_t exp(S_t)."""
+    S = (np.asarray(Q, np.float64) @ np.asarray(K, np.float64).T) * scale
+    lp = log_softmax(S)
+    m = S.max(axis=-1)
+    lse = m + np.log(np.exp(S - m[:, None]).sum(axis=-1))
+    return np.exp(lp) @ np.asarray(V, np.float64), lse
+
+
+def attention_decode(Q, k_codes, k_scales, v_codes, v_scales, k_method: str, k_bits: int, v_method: str,
+                     v_bits: int, scale: float, k_seed: int = DEFAULT_SEED, v_seed: int = DEFAULT_SEED):
+    """Attention over the decodes of compressed caches, the way the reference evaluates it
+    (reference/attention_extra.py:11-14 decodes with pitch_reference, then attend): K = decode(k_codes, k_scales),
+    V = decode(v_codes, v_scales), with float32 scales widened (attention_extra.py:13). Q (m, d); codes (T, d)."""
+    K = DECODERS[k_method](k_codes, np.asarray(k_scales, np.float32).astype(np.float64), k_bits, k_seed)
+    V = DECODERS[v_method](v_codes, np.asarray(v_scales, np.float32).astype(np.float64), v_bits, v_seed)
+    return attend(Q, K, V, scale)
+
+
 # ----------------------------------------------------------------------------- boundary classification
 # The parity bar for per-vector codes: a code may differ from the oracle's only at a coordinate whose
 # rotated value lies within REL_BAND of a decision boundary, relative to max(|boundary|, floor). The floor

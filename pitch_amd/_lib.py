@@ -30,6 +30,12 @@ class PitchConfigC(ctypes.Structure):
                 ("seed", ctypes.c_uint32)]
 
 
+class PitchAttentionDescC(ctypes.Structure):
+    _fields_ = [("q_per_kv", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("tokens", ctypes.c_uint64),
+                ("token_stride", ctypes.c_uint64), ("head_stride", ctypes.c_uint64), ("scale", ctypes.c_float),
+                ("reserved", ctypes.c_uint32)]
+
+
 class PitchChannelConfigC(ctypes.Structure):
     _fields_ = [("dim", ctypes.c_uint32), ("bits", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
                 ("reserved", ctypes.c_uint32)]
@@ -60,6 +66,11 @@ SIGNATURES = {
                                                _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_channel_decode_io": (_int, [ctypes.POINTER(PitchChannelConfigC), _u32, _vp, _u64, _u64, _vp,
                                                _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_attention_workspace_size": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
+                                              ctypes.POINTER(PitchAttentionDescC), ctypes.POINTER(_u64)]),
+    "pitch_enqueue_attention_decode": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
+                                              ctypes.POINTER(PitchAttentionDescC)] + [_vp, _u64, _u64] * 7
+                                       + [_vp, _u64, _vp]),
     "pitch_enqueue_pack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_unpack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
 }

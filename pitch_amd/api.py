@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import base64
 import ctypes
+import math
 import enum
 import json
 from dataclasses import dataclass, field
@@ -623,6 +624,39 @@ class PITCH:
             rc = self._lib.pitch_enqueue_decode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
 
+    # ---- attention over compressed caches (no counterpart in the reference; README.md:96)
+    def enqueueAttentionDecode(self, q, keyCodes, keyScales, valueCodes, valueScales, output, tokens: int,
+                               keyConfig: QuantConfig, valueConfig: QuantConfig | None = None, qPerKv: int = 1,
+                               kvHeads: int = 1, tokenStride: int = 1, headStride: int | None = None,
+                               scale: float | None = None, lse=None, workspace=None, stream=None) -> None:
+        """out = softmax(scale * q K^T) V over caches held as codes: q and output are fp32
+        [kvHeads][qPerKv][dim]; the vector of (head h, token t) is t * tokenStride + h * headStride (default
+        headStride = tokens, a head-major cache). scale defaults to 1 / sqrt(dim). lse, when given, receives the
+        natural-log sum of exp of the scaled scores per query. Without a workspace one is allocated."""
+        torch = _torch()
+        valueConfig = valueConfig or keyConfig
+        scale = 1.0 / math.sqrt(keyConfig.dim) if scale is None else scale
+        headStride = int(tokens) if headStride is None else headStride
+        desc = _attention_desc(qPerKv, kvHeads, tokens, tokenStride, headStride, scale)
+        if workspace is None:
+            nbytes = attention_workspace_bytes(keyConfig, valueConfig, tokens, qPerKv, kvHeads)
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        args = []
+        for t, name in ((q, "query"), (keyCodes, "key codes"), (keyScales, "key scales"), (valueCodes, "value codes"),
+                        (valueScales, "value scales"), (output, "output")):
+            p_, b_ = _buf(t, name)
+            args += [p_, b_, 0]
+        if lse is not None:
+            p_, b_ = _buf(lse, "lse")
+            args += [p_, b_, 0]
+        else:
+            args += [None, 0, 0]
+        wp, wb = _buf(workspace, "workspace")
+        rc = self._lib.pitch_enqueue_attention_decode(ctypes.byref(keyConfig._c()), ctypes.byref(valueConfig._c()),
+                                                      ctypes.byref(desc), *args, wp, wb,
+                                                      _stream_handle(stream, self.device))
+        _raise_for(rc)
+
     # ---- per-channel (PerChannel.swift:182-290)
     def encodePerChannel(self, vectors, dim: int | None = None, bits: int | None = None, groupSize: int = 64,
                          config: ChannelQuantConfig | None = None) -> ChannelCompressedBlock:
@@ -696,6 +730,27 @@ class PITCH:
         else:
             rc = self._lib.pitch_enqueue_channel_decode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
+
+
+def _attention_desc(q_per_kv: int, kv_heads: int, tokens: int, token_stride: int, head_stride: int,
+                    scale: float) -> _lib.PitchAttentionDescC:
+    for name, v in (("qPerKv", q_per_kv), ("kvHeads", kv_heads), ("tokens", tokens), ("tokenStride", token_stride),
+                    ("headStride", head_stride)):
+        if not isinstance(v, (int, np.integer)) or v < 0:
+            raise InvalidInput(f"{name} {v} must be a non-negative integer")
+    return _lib.PitchAttentionDescC(int(q_per_kv), int(kv_heads), int(tokens), int(token_stride), int(head_stride),
+                                    float(scale), 0)
+
+
+def attention_workspace_bytes(keyConfig: QuantConfig, valueConfig: QuantConfig, tokens: int, qPerKv: int = 1,
+                              kvHeads: int = 1) -> int:
+    """Device workspace pitch_enqueue_attention_decode needs for a call of this shape."""
+    desc = _attention_desc(qPerKv, kvHeads, tokens, 1, tokens, 1.0)
+    out = ctypes.c_uint64(0)
+    _raise_for(_lib_or_raise().pitch_attention_workspace_size(ctypes.byref(keyConfig._c()),
+                                                              ctypes.byref(valueConfig._c()), ctypes.byref(desc),
+                                                              ctypes.byref(out)))
+    return int(out.value)
 
 
 def _check_offsets(*offs) -> None:
@@ -845,6 +900,30 @@ def channel_decode(codes, ranges, b: int, G: int = CHANNEL_DEFAULT_GROUP, dtype=
     with torch.cuda.device(codes.device):
         _pitch_for(codes).enqueuePerChannelDecode(packed, ranges.to(torch.float16).contiguous(), out, n, cfg)
     return out
+
+
+def attention_decode(q, k_codes, k_scales, v_codes, v_scales, b: int, method: str = "turboQuant",
+                     seed: int = DEFAULT_SEED, scale: float | None = None, v_bits: int | None = None,
+                     v_method: str | None = None, v_seed: int | None = None):
+    """Decode-step attention over compressed caches: q (kv_heads, q_per_kv, d) fp32, packed codes
+    (kv_heads, T, codeStride) uint8 and scales (kv_heads, T) as the encoders write them, head-major. Returns
+    (out (kv_heads, q_per_kv, d) fp32, lse (kv_heads, q_per_kv)), equal to softmax(scale q K^T) V over the
+    decoded caches (reference/attention_extra.py:70-74) without writing them."""
+    torch = _torch()
+    if q.dim() == 2:
+        q = q.unsqueeze(0)
+    H, nq, d = q.shape
+    T = k_codes.shape[1]
+    kc = QuantConfig(method, d, b, seed)
+    vc = QuantConfig(v_method or method, d, v_bits or b, seed if v_seed is None else v_seed)
+    out = torch.empty((H, nq, d), dtype=torch.float32, device=q.device)
+    lse = torch.empty((H, nq), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _pitch_for(q).enqueueAttentionDecode(q.to(torch.float32).contiguous(), k_codes.contiguous(),
+                                             k_scales.to(torch.float32).contiguous(), v_codes.contiguous(),
+                                             v_scales.to(torch.float32).contiguous(), out, T, kc, vc, qPerKv=nq,
+                                             kvHeads=H, tokenStride=1, headStride=T, scale=scale, lse=lse)
+    return out, lse
 
 
 def rand_signs(seed: int, d: int):

@@ -4,8 +4,8 @@
 
 Steps: generate csrc/pitch_tables.inc from data/codebooks.json, compile csrc/pitch_vector.hip once per
 dimension and element type of the uncompressed vectors (-DPITCH_DIM=2..1024, -DPITCH_IO=0/1/2 for
-float32/float16/bfloat16), csrc/pitch_channel.hip once per element type and csrc/pitch_abi.cpp, and link the
-shared library next to this file. Object files go to <repo>/_build/.
+float32/float16/bfloat16), csrc/pitch_channel.hip once per element type, csrc/pitch_attention.hip once per
+attention dimension (64, 128) and csrc/pitch_abi.cpp, and link the shared library next to this file. Object files go to <repo>/_build/.
 """
 from __future__ import annotations
 
@@ -23,6 +23,7 @@ BUILD = REPO / "_build"
 LIB = PKG / "libpitch_amd.so"
 DIMS = [2 ** k for k in range(1, 11)]
 IO_TYPES = [0, 1, 2]   # element type of uncompressed vectors: float32, float16, bfloat16
+ATTENTION_DIMS = [64, 128]
 ARCH = os.environ.get("PITCH_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -60,6 +61,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     units = [(CSRC / "pitch_vector.hip", BUILD / f"vector_d{d}_io{io}.o", [f"-DPITCH_DIM={d}", f"-DPITCH_IO={io}"], d)
              for d in DIMS for io in IO_TYPES]
     units += [(CSRC / "pitch_channel.hip", BUILD / f"channel_io{io}.o", [f"-DPITCH_IO={io}"], 512) for io in IO_TYPES]
+    units += [(CSRC / "pitch_attention.hip", BUILD / f"attention_d{d}.o", [f"-DPITCH_DIM={d}"], 2048 + d)
+              for d in ATTENTION_DIMS]
     units += [(CSRC / "pitch_abi.cpp", BUILD / "abi.o", [], 0)]
     # largest dims first: they take longest to compile
     units.sort(key=lambda u: -u[3])

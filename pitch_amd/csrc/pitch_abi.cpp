@@ -259,6 +259,41 @@ int channel_decode_impl(const pitch_channel_config_t* config, uint32_t io, const
   return ok();
 }
 
+uint32_t padded_queries(uint32_t nq) { return nq <= 1 ? 1u : (nq <= 2 ? 2u : (nq <= 4 ? 4u : 8u)); }
+
+int validate_attention(const pitch_config_t* k, const pitch_config_t* v, const pitch_attention_desc_t* d) {
+  PITCH_TRY(validate_config(k));
+  PITCH_TRY(validate_config(v));
+  if (!d) return fail(PITCH_ERR_INVALID_INPUT, "attention descriptor is null");
+  if (k->dim != v->dim)
+    return fail(PITCH_ERR_CONFIGURATION_MISMATCH, "key dimension %u and value dimension %u differ", k->dim, v->dim);
+  if (k->dim != 64 && k->dim != 128)
+    return fail(PITCH_ERR_INVALID_DIMENSION, "attention over compressed caches supports dimension 64 or 128, got %u",
+                k->dim);
+  if (d->q_per_kv < 1 || d->q_per_kv > 8)
+    return fail(PITCH_ERR_INVALID_INPUT, "query heads per KV head %u must be in 1...8", d->q_per_kv);
+  if (d->kv_heads < 1 || d->kv_heads > 65535)
+    return fail(PITCH_ERR_INVALID_INPUT, "KV heads %u must be in 1...65535", d->kv_heads);
+  if (d->tokens < 1) return fail(PITCH_ERR_INVALID_INPUT, "tokens must be at least 1");
+  if (d->tokens > (1ull << 36)) return fail(PITCH_ERR_INVALID_INPUT, "tokens is too large");
+  if (!(d->scale == d->scale) || d->scale == __builtin_inff() || d->scale == -__builtin_inff())
+    return fail(PITCH_ERR_INVALID_INPUT, "softmax scale must be finite");
+  return PITCH_OK;
+}
+
+// Largest vector index the call touches, with overflow checks: (tokens - 1) * token_stride +
+// (kv_heads - 1) * head_stride.
+int attention_extent(const pitch_attention_desc_t* d, uint64_t* vectors) {
+  const uint64_t a = d->tokens - 1, b = (uint64_t)d->kv_heads - 1;
+  if (mul_overflows(a, d->token_stride) || mul_overflows(b, d->head_stride))
+    return fail(PITCH_ERR_INVALID_INPUT, "cache strides overflow");
+  const uint64_t x = a * d->token_stride, y = b * d->head_stride;
+  if (x > UINT64_MAX - y - 1) return fail(PITCH_ERR_INVALID_INPUT, "cache strides overflow");
+  *vectors = x + y + 1;
+  if (mul_overflows(*vectors, 4096u)) return fail(PITCH_ERR_INVALID_INPUT, "cache strides overflow");
+  return PITCH_OK;
+}
+
 }  // namespace
 
 namespace pitch {
@@ -275,6 +310,17 @@ int device_cu_count() {
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 1;
   cache[dev] = n;
   return n;
+}
+
+uint32_t attention_chunk_tokens(uint64_t tokens, uint32_t kv_heads) {
+  // 256, 512 or 1024 tokens per workgroup: the largest that still gives about 1024 workgroups
+  const uint64_t blocks = (tokens + 255) / 256 * kv_heads;
+  return blocks >= 4096 ? 1024u : (blocks >= 2048 ? 512u : 256u);
+}
+
+uint64_t attention_workspace_floats(uint32_t dim, uint32_t nqp, uint32_t kv_heads, uint64_t tokens, uint32_t chunk) {
+  const uint64_t chunks = (tokens + chunk - 1) / chunk;
+  return (uint64_t)kv_heads * nqp * (dim + tokens + chunks * (2 + dim));
 }
 
 uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size) {
@@ -398,6 +444,84 @@ int pitch_enqueue_channel_decode_io(const pitch_channel_config_t* config, uint32
                                     void* stream) {
   return channel_decode_impl(config, io_type, codes, codes_bytes, codes_offset, ranges, ranges_bytes,
                              ranges_offset, output, output_bytes, output_offset, count, stream);
+}
+
+int pitch_attention_workspace_size(const pitch_config_t* key_config, const pitch_config_t* value_config,
+                                   const pitch_attention_desc_t* desc, uint64_t* bytes) {
+  PITCH_TRY(validate_attention(key_config, value_config, desc));
+  if (!bytes) return fail(PITCH_ERR_INVALID_INPUT, "bytes is null");
+  const uint32_t chunk = pitch::attention_chunk_tokens(desc->tokens, desc->kv_heads);
+  *bytes = 4u * pitch::attention_workspace_floats(key_config->dim, padded_queries(desc->q_per_kv), desc->kv_heads,
+                                                  desc->tokens, chunk);
+  return ok();
+}
+
+int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch_config_t* value_config,
+                                   const pitch_attention_desc_t* desc, const void* q, uint64_t q_bytes,
+                                   uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,
+                                   uint64_t key_codes_offset, const void* key_scales, uint64_t key_scales_bytes,
+                                   uint64_t key_scales_offset, const void* value_codes, uint64_t value_codes_bytes,
+                                   uint64_t value_codes_offset, const void* value_scales,
+                                   uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output,
+                                   uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes,
+                                   uint64_t lse_offset, void* workspace, uint64_t workspace_bytes, void* stream) {
+  PITCH_TRY(validate_attention(key_config, value_config, desc));
+  const uint32_t dim = key_config->dim, nq = desc->q_per_kv, nqp = padded_queries(nq);
+  const uint32_t kcs = code_stride_of(dim, key_config->bits), vcs = code_stride_of(dim, value_config->bits);
+  uint64_t vectors = 0;
+  PITCH_TRY(attention_extent(desc, &vectors));
+  const uint64_t queries = (uint64_t)desc->kv_heads * nq;
+  PITCH_TRY(check_buffer(q, q_bytes, q_offset, queries * dim * 4u, "query"));
+  PITCH_TRY(check_buffer(key_codes, key_codes_bytes, key_codes_offset, vectors * kcs, "key codes"));
+  PITCH_TRY(check_buffer(key_scales, key_scales_bytes, key_scales_offset, vectors * 4u, "key scales"));
+  PITCH_TRY(check_buffer(value_codes, value_codes_bytes, value_codes_offset, vectors * vcs, "value codes"));
+  PITCH_TRY(check_buffer(value_scales, value_scales_bytes, value_scales_offset, vectors * 4u, "value scales"));
+  PITCH_TRY(check_buffer(output, output_bytes, output_offset, queries * dim * 4u, "output"));
+  if (lse) PITCH_TRY(check_buffer(lse, lse_bytes, lse_offset, queries * 4u, "lse"));
+  const uint32_t chunk = pitch::attention_chunk_tokens(desc->tokens, desc->kv_heads);
+  const uint64_t ws_need = 4u * pitch::attention_workspace_floats(dim, nqp, desc->kv_heads, desc->tokens, chunk);
+  PITCH_TRY(check_buffer(workspace, workspace_bytes, 0, ws_need, "workspace"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(q, dev, "query"));
+  PITCH_TRY(check_device(key_codes, dev, "key codes"));
+  PITCH_TRY(check_device(key_scales, dev, "key scales"));
+  PITCH_TRY(check_device(value_codes, dev, "value codes"));
+  PITCH_TRY(check_device(value_scales, dev, "value scales"));
+  PITCH_TRY(check_device(output, dev, "output"));
+  if (lse) PITCH_TRY(check_device(lse, dev, "lse"));
+  PITCH_TRY(check_device(workspace, dev, "workspace"));
+  pitch::AttnArgs a{};
+  a.q = at<const float>(q, q_offset);
+  a.k_codes = at<const uint32_t>(key_codes, key_codes_offset);
+  a.k_scales = at<const float>(key_scales, key_scales_offset);
+  a.v_codes = at<const uint32_t>(value_codes, value_codes_offset);
+  a.v_scales = at<const float>(value_scales, value_scales_offset);
+  a.out = at<float>(output, output_offset);
+  a.lse = lse ? at<float>(lse, lse_offset) : nullptr;
+  a.ws = (float*)workspace;
+  a.tokens = desc->tokens;
+  a.token_stride = desc->token_stride;
+  a.head_stride = desc->head_stride;
+  a.dim = dim;
+  a.nq = nq;
+  a.nqp = nqp;
+  a.kv_heads = desc->kv_heads;
+  a.kbits = key_config->bits;
+  a.vbits = value_config->bits;
+  a.kpolar = key_config->method == PITCH_METHOD_POLAR;
+  a.vpolar = value_config->method == PITCH_METHOD_POLAR;
+  a.kseed = key_config->seed;
+  a.vseed = value_config->seed;
+  a.chunk = chunk;
+  a.chunks = (uint32_t)((desc->tokens + chunk - 1) / chunk);
+  // softmax scale, log2(e) (scores in log2 units) and the key decode's 1 / sqrt(d), folded into the query
+  a.qscale = (float)((double)desc->scale * 1.4426950408889634 / __builtin_sqrt((double)dim));
+  a.oscale = (float)(1.0 / __builtin_sqrt((double)dim));
+  const hipError_t e = dim == 64 ? pitch::launch_attention_d64(a, (hipStream_t)stream)
+                                 : pitch::launch_attention_d128(a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Attention failed: %s", hipGetErrorString(e));
+  return ok();
 }
 
 static int pack_common(bool pack, uint32_t dim, uint32_t bits, const void* src, uint64_t src_bytes,

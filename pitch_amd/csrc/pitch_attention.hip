@@ -1,0 +1,448 @@
+// Decode-phase attention over compressed K and V caches, without decompressing them (one dimension per
+// object file: PITCH_DIM = 64 or 128).
+//
+// The reference evaluates attention on decoded caches: S = Q K^T * scale, log-softmax, P V
+// (reference/attention_extra.py:70-74, attention_eval.py:31-33), and names decoding inside attention as its
+// next step (README.md:96). For the per-vector codecs the decode is x = s (.) H(t[c]) * n / sqrt(d)
+// (pitch_reference.py:104-107, 123-129): t is the method's value table (Lloyd-Max centroids, or radius fraction
+// times (cos, sin) for PolarQuant pairs), n the stored scale, s the rotation signs and H the symmetric
+// Walsh-Hadamard matrix. Hence
+//   q . k_t       = n_t / sqrt(d) * sum_j (H (s_K (.) q))_j t[c_tj]     (the query is rotated once)
+//   sum_t p_t v_t = s_V (.) H( sum_t p_t n_t t[c_t] ) / sqrt(d)          (one inverse rotation per query)
+// so no token is transformed: per token and coordinate pair the kernels do one LDS table read and a few FMAs
+// on the codes as stored. Kernels of one call (flash-decoding over chunks of a KV head's tokens):
+//   attn_prep     q'' = H(s_K (.) q) * scale * log2(e) / sqrt(d), per (KV head, query head), into the workspace
+//   attn_scores   one thread per token: scores in log2 units into LDS, chunk max m_c, p = 2^(s - m_c), l_c
+//   attn_values   16 lanes per token: a_c = sum_t p_t n_t t[c_t] in the rotated domain
+//   attn_combine  merges the chunks, divides by the softmax sum, inverse rotation, output and log-sum-exp
+// Query heads of one KV head (grouped-query attention) share every table read; their count is padded to
+// 1, 2, 4 or 8 (padded queries are zero and never written out).
+#include "pitch_device.h"
+
+#ifndef PITCH_DIM
+#error "compile with -DPITCH_DIM=<dim>"
+#endif
+
+namespace pitch {
+namespace {
+
+constexpr int kMaxChunk = 1024;          // tokens per workgroup; a chunk's scores stay in LDS
+constexpr float kLn2 = 0x1.62e430p-1f;   // ln(2)
+
+// Workspace regions (floats): rotated queries [kv][D/2][nqp][2], weights p [kv][T][nqp],
+// chunk (max, sum) [kv][nqp][chunks][2], chunk accumulators [kv][nqp][chunks][D].
+struct WsLayout {
+  uint64_t p, ml, acc;
+  __host__ __device__ explicit WsLayout(const AttnArgs& a) {
+    p = (uint64_t)a.kv_heads * a.dim * a.nqp;
+    ml = p + (uint64_t)a.kv_heads * a.tokens * a.nqp;
+    acc = ml + (uint64_t)a.kv_heads * a.nqp * a.chunks * 2;
+  }
+};
+
+// Value table of a code pair: codes c0 (bits [0, B)) and c1 (bits [B, 2B)) -> the two rotated-domain values
+// their decode gives before the scale. B <= 5: one table of 2^(2B) float2. B >= 6: U[c0] * W[c1] element-wise
+// from two 2^B-entry float2 tables (TurboQuant: U = (cb, 1), W = (1, cb); PolarQuant: U = (r, r),
+// W = (cos, sin)). Built from the same constant tables as the decoders (gen_tables.py).
+template <int D, int B>
+struct PairLut {
+  static constexpr int L = 1 << B;
+  static constexpr bool kPair = B <= 5;
+  static constexpr int N = kPair ? (1 << (2 * B)) : 2 * L;  // float2 entries
+
+  __device__ static void build(float2* s, bool polar) {
+    if (polar) {
+      constexpr int off = pitch_polar_offset(B);
+      const float* rad = pitch_polar_radius_tab + off;
+      const float* cs = pitch_polar_cos_tab + off;
+      const float* sn = pitch_polar_sin_tab + off;
+      if constexpr (kPair) {
+        for (int i = threadIdx.x; i < N; i += blockDim.x) {
+          const float r = rad[i & (L - 1)];
+          s[i] = make_float2(r * cs[i >> B], r * sn[i >> B]);
+        }
+      } else {
+        for (int i = threadIdx.x; i < L; i += blockDim.x) {
+          s[i] = make_float2(rad[i], rad[i]);
+          s[L + i] = make_float2(cs[i], sn[i]);
+        }
+      }
+    } else {
+      const float* cb = pitch_codebook_tab + pitch_codebook_offset(ilog2(D), B);
+      if constexpr (kPair) {
+        for (int i = threadIdx.x; i < N; i += blockDim.x) s[i] = make_float2(cb[i & (L - 1)], cb[i >> B]);
+      } else {
+        for (int i = threadIdx.x; i < L; i += blockDim.x) {
+          s[i] = make_float2(cb[i], 1.f);
+          s[L + i] = make_float2(1.f, cb[i]);
+        }
+      }
+    }
+  }
+
+  __device__ static float2 get(const float2* s, uint32_t bits) {
+    if constexpr (kPair) {
+      return s[bits & (uint32_t)(N - 1)];
+    } else {
+      const float2 u = s[bits & (uint32_t)(L - 1)], w = s[L + ((bits >> B) & (uint32_t)(L - 1))];
+      return make_float2(u.x * w.x, u.y * w.y);
+    }
+  }
+};
+
+// One packed code row of NW words.
+template <int NW>
+__device__ __forceinline__ void load_row(const uint32_t* row, uint32_t (&w)[NW]) {
+  int i = 0;
+#pragma unroll
+  for (; i + 4 <= NW; i += 4) {
+    const u32x4 v = *(const u32x4*)(row + i);
+    w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+  }
+#pragma unroll
+  for (; i + 2 <= NW; i += 2) {
+    const u32x2 v = *(const u32x2*)(row + i);
+    w[i] = v.x; w[i + 1] = v.y;
+  }
+}
+
+// Sum or max over the 256 threads of a workgroup, per element; every thread gets the results.
+template <int NQ, bool MAX>
+__device__ __forceinline__ void block_reduce(float (&v)[NQ], float* s_red) {
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_xor(v[h], off);
+      v[h] = MAX ? fmaxf(v[h], o) : v[h] + o;
+    }
+  }
+  const int wid = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) s_red[wid * NQ + h] = v[h];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    const float a = s_red[h], b = s_red[NQ + h], c = s_red[2 * NQ + h], d = s_red[3 * NQ + h];
+    v[h] = MAX ? fmaxf(fmaxf(a, b), fmaxf(c, d)) : (a + b) + (c + d);
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------------- prep
+// One wave per (KV head, padded query head): q'' = H(s_K (.) q) * qscale, stored as [pair][query][2].
+template <int D>
+__global__ __launch_bounds__(64) void attn_prep(AttnArgs a) {
+  constexpr int E = D / 64;
+  const uint32_t kv = blockIdx.x / a.nqp, h = blockIdx.x % a.nqp;
+  const int lane = threadIdx.x;
+  float v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int j = lane * E + e;
+    const float x = h < a.nq ? a.q[((uint64_t)kv * a.nq + h) * D + j] : 0.f;
+    v[e] = sign_is_negative(a.kseed, (uint32_t)j) ? -x : x;
+  }
+  fwht_contig<E, 64, float>(v, lane);
+  float* qp = a.ws + (uint64_t)kv * D * a.nqp;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int j = lane * E + e;
+    qp[((uint64_t)(j >> 1) * a.nqp + h) * 2 + (j & 1)] = v[e] * a.qscale;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- scores
+// Workgroup (chunk, KV head); thread = token. qp (the rotated queries of this KV head, read-only here) is
+// passed separately so its wave-uniform reads can be scalar loads.
+template <int D, int B, int NQ>
+__global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* __restrict__ qp_all) {
+  using P = PairLut<D, B>;
+  constexpr int NW = D * B / 32;
+  __shared__ float2 s_tab[P::N];
+  __shared__ float s_s[kMaxChunk * NQ];
+  __shared__ float s_red[4 * NQ];
+  const int tid = threadIdx.x;
+  const uint32_t kv = blockIdx.y, c = blockIdx.x;
+  const uint64_t t0 = (uint64_t)c * a.chunk;
+  const uint32_t n = (uint32_t)min((uint64_t)a.chunk, a.tokens - t0);
+  P::build(s_tab, a.kpolar != 0);
+  __syncthreads();
+  const float* __restrict__ qp = qp_all + (uint64_t)kv * D * NQ;
+
+  for (uint32_t i0 = 0; i0 < n; i0 += kBlock) {
+    const uint32_t i = i0 + tid;
+    const bool valid = i < n;
+    const uint64_t vi = (t0 + (valid ? i : 0)) * a.token_stride + (uint64_t)kv * a.head_stride;
+    uint32_t w[NW];
+    load_row<NW>(a.k_codes + vi * NW, w);
+    const float nk = a.k_scales[vi];
+    float acc[NQ];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) acc[h] = 0.f;
+#pragma unroll
+    for (int p = 0; p < D / 2; ++p) {
+      const int pos = 2 * B * p, wi = pos >> 5, sh = pos & 31;
+      const uint32_t bits = (sh + 2 * B <= 32) ? (w[wi] >> sh) : __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh);
+      const float2 t = P::get(s_tab, bits);
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        acc[h] = __builtin_fmaf(qp[(p * NQ + h) * 2], t.x, acc[h]);
+        acc[h] = __builtin_fmaf(qp[(p * NQ + h) * 2 + 1], t.y, acc[h]);
+      }
+    }
+    if (valid) {
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) s_s[i * NQ + h] = acc[h] * nk;
+    }
+  }
+  __syncthreads();
+
+  // chunk maximum, weights p = 2^(s - m) and their sum
+  float m[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) m[h] = -__builtin_inff();
+  for (uint32_t i = tid; i < n; i += kBlock) {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) m[h] = fmaxf(m[h], s_s[i * NQ + h]);
+  }
+  block_reduce<NQ, true>(m, s_red);
+  const WsLayout L(a);
+  float* pw = a.ws + L.p + ((uint64_t)kv * a.tokens + t0) * NQ;
+  float l[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) l[h] = 0.f;
+  for (uint32_t i = tid; i < n; i += kBlock) {
+    float e[NQ];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      e[h] = exp2f(s_s[i * NQ + h] - m[h]);
+      l[h] += e[h];
+    }
+    if constexpr (NQ % 4 == 0) {
+#pragma unroll
+      for (int h = 0; h < NQ; h += 4) *(f32x4*)(pw + (uint64_t)i * NQ + h) = f32x4{e[h], e[h + 1], e[h + 2], e[h + 3]};
+    } else {
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) pw[(uint64_t)i * NQ + h] = e[h];
+    }
+  }
+  block_reduce<NQ, false>(l, s_red);
+  if (tid == 0) {
+    float* ml = a.ws + L.ml;
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const uint64_t k = (((uint64_t)kv * NQ + h) * a.chunks + c) * 2;
+      ml[k] = m[h];
+      ml[k + 1] = l[h];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- values
+// Workgroup (chunk, KV head). Per block of 256 tokens, each thread stages one token's code row and weights
+// p * n in LDS; then lane (r, g) of wave w takes token 16 * step + 4 * w + r and the g-th 16th of its code pairs,
+// accumulating sum_t p_t n_t t[c_t] for its 2 * PPL coordinates and every query head.
+template <int D, int B, int NQ>
+__global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
+  using P = PairLut<D, B>;
+  constexpr int NW = D * B / 32;
+  constexpr int RS = NW + 1;         // staged row stride in words (odd: consecutive rows start on other banks)
+  constexpr int PPL = D / 32;        // code pairs per lane
+  constexpr int LB = PPL * 2 * B;    // code bits per lane
+  static_assert(LB <= 64, "a lane's codes fit two words after alignment");
+  __shared__ float2 s_tab[P::N];
+  __shared__ uint32_t s_code[kBlock * RS + 4];
+  __shared__ __attribute__((aligned(16))) float s_w[kBlock * NQ];
+  __shared__ float s_acc[4 * NQ * D];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, r = lane >> 4, g = lane & 15;
+  const uint32_t kv = blockIdx.y, c = blockIdx.x;
+  const uint64_t t0 = (uint64_t)c * a.chunk;
+  const uint32_t n = (uint32_t)min((uint64_t)a.chunk, a.tokens - t0);
+  P::build(s_tab, a.vpolar != 0);
+  const WsLayout L(a);
+  const float* pw = a.ws + L.p + ((uint64_t)kv * a.tokens + t0) * NQ;
+  const int bit0 = g * LB, wlo = bit0 >> 5;
+  const uint32_t sh = (uint32_t)(bit0 & 31);
+
+  float acc[NQ][2 * PPL];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h)
+#pragma unroll
+    for (int e = 0; e < 2 * PPL; ++e) acc[h][e] = 0.f;
+
+  for (uint32_t i0 = 0; i0 < n; i0 += kBlock) {
+    __syncthreads();  // the previous block's readers are done (and, the first time, the table is built)
+    {
+      const uint32_t i = i0 + tid;
+      const bool valid = i < n;
+      const uint32_t iv = valid ? i : 0u;
+      const uint64_t vi = (t0 + iv) * a.token_stride + (uint64_t)kv * a.head_stride;
+      uint32_t w[NW];
+      load_row<NW>(a.v_codes + vi * NW, w);
+#pragma unroll
+      for (int k = 0; k < NW; ++k) s_code[tid * RS + k] = w[k];
+      const float nv = valid ? a.v_scales[vi] : 0.f;
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) s_w[tid * NQ + h] = pw[(uint64_t)iv * NQ + h] * nv;
+    }
+    __syncthreads();
+    const uint32_t nt = min((uint32_t)kBlock, n - i0);
+    for (uint32_t s0 = 0; s0 < nt; s0 += 16) {
+      const uint32_t tok = s0 + wid * 4 + r;
+      if (tok < nt) {
+        const uint32_t* row = s_code + tok * RS + wlo;
+        const uint32_t w0 = row[0], w1 = row[1];
+        const uint32_t x0 = __builtin_amdgcn_alignbit(w1, w0, sh);
+        uint32_t x1 = 0u;  // bits [sh + 32, sh + 64) of the lane's window, needed when it holds over 32 bits
+        if constexpr (LB > 32) x1 = __builtin_amdgcn_alignbit(row[2], w1, sh);
+        float wt[NQ];
+        if constexpr (NQ % 4 == 0) {
+#pragma unroll
+          for (int h = 0; h < NQ; h += 4) {
+            const float4 q4 = *(const float4*)(s_w + tok * NQ + h);
+            wt[h] = q4.x; wt[h + 1] = q4.y; wt[h + 2] = q4.z; wt[h + 3] = q4.w;
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < NQ; ++h) wt[h] = s_w[tok * NQ + h];
+        }
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) {
+          constexpr int W2 = 2 * B;
+          const int o = W2 * j;
+          const uint32_t bits = (o + W2 <= 32) ? (x0 >> o)
+                                : (o >= 32 ? (x1 >> (o - 32)) : __builtin_amdgcn_alignbit(x1, x0, (uint32_t)o));
+          const float2 t = P::get(s_tab, bits);
+#pragma unroll
+          for (int h = 0; h < NQ; ++h) {
+            acc[h][2 * j] = __builtin_fmaf(wt[h], t.x, acc[h][2 * j]);
+            acc[h][2 * j + 1] = __builtin_fmaf(wt[h], t.y, acc[h][2 * j + 1]);
+          }
+        }
+      }
+    }
+  }
+  // sum over the four token rows of the wave (lanes g, g + 16, g + 32, g + 48), then over the waves
+#pragma unroll
+  for (int h = 0; h < NQ; ++h)
+#pragma unroll
+    for (int e = 0; e < 2 * PPL; ++e) {
+      acc[h][e] += __shfl_xor(acc[h][e], 16);
+      acc[h][e] += __shfl_xor(acc[h][e], 32);
+    }
+  if (r == 0) {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h)
+#pragma unroll
+      for (int e = 0; e < 2 * PPL; ++e) s_acc[(wid * NQ + h) * D + 2 * PPL * g + e] = acc[h][e];
+  }
+  __syncthreads();
+  float* A = a.ws + L.acc;
+  for (int x = tid; x < NQ * D; x += kBlock) {
+    const int h = x / D, j = x % D;
+    const float v = (s_acc[h * D + j] + s_acc[(NQ + h) * D + j]) + (s_acc[(2 * NQ + h) * D + j] + s_acc[(3 * NQ + h) * D + j]);
+    A[(((uint64_t)kv * NQ + h) * a.chunks + c) * D + j] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- combine
+// Workgroup per (KV head, real query head): merges the chunks' (m, l, a), then o = s_V (.) H(a / l) / sqrt(d)
+// and lse = (M + log2 l) * ln 2.
+template <int D>
+__global__ __launch_bounds__(kBlock) void attn_combine(AttnArgs a) {
+  constexpr int E = D / 64;
+  __shared__ float s_red[4];
+  __shared__ float s_part[4 * (D + 1)];
+  const uint32_t kv = blockIdx.x / a.nq, h = blockIdx.x % a.nq;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const WsLayout L(a);
+  const float* ml = a.ws + L.ml + ((uint64_t)kv * a.nqp + h) * a.chunks * 2;
+  const float* A = a.ws + L.acc + ((uint64_t)kv * a.nqp + h) * a.chunks * D;
+  float M = -__builtin_inff();
+  for (uint32_t c = tid; c < a.chunks; c += kBlock) M = fmaxf(M, ml[2 * c]);
+  for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+  if (lane == 0) s_red[wid] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  float ls = 0.f, acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  for (uint32_t c = wid; c < a.chunks; c += 4) {
+    const float f = exp2f(ml[2 * c] - M);
+    ls = __builtin_fmaf(ml[2 * c + 1], f, ls);
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = __builtin_fmaf(A[(uint64_t)c * D + lane * E + e], f, acc[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) s_part[wid * (D + 1) + lane * E + e] = acc[e];
+  if (lane == 0) s_part[wid * (D + 1) + D] = ls;
+  __syncthreads();
+  if (wid != 0) return;  // no barrier follows
+  float y[E];
+  const float lsum = (s_part[D] + s_part[(D + 1) + D]) + (s_part[2 * (D + 1) + D] + s_part[3 * (D + 1) + D]);
+  const float inv = 1.f / lsum;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int j = lane * E + e;
+    y[e] = ((s_part[j] + s_part[(D + 1) + j]) + (s_part[2 * (D + 1) + j] + s_part[3 * (D + 1) + j])) * inv;
+  }
+  fwht_contig<E, 64, float>(y, lane);
+  float* out = a.out + ((uint64_t)kv * a.nq + h) * D;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int j = lane * E + e;
+    const float o = y[e] * a.oscale;
+    out[j] = sign_is_negative(a.vseed, (uint32_t)j) ? -o : o;
+  }
+  if (lane == 0 && a.lse) a.lse[(uint64_t)kv * a.nq + h] = (M + log2f(lsum)) * kLn2;
+}
+
+template <int NQ>
+hipError_t launch_nq(const AttnArgs& a, hipStream_t s) {
+  constexpr int D = PITCH_DIM;
+  const dim3 grid(a.chunks, a.kv_heads);
+  const float* qp = a.ws;
+  switch (a.kbits) {
+#define PITCH_SCORES(B) \
+  case B: hipLaunchKernelGGL((attn_scores<D, B, NQ>), grid, dim3(kBlock), 0, s, a, qp); break;
+    PITCH_SCORES(2) PITCH_SCORES(3) PITCH_SCORES(4) PITCH_SCORES(5) PITCH_SCORES(6) PITCH_SCORES(7) PITCH_SCORES(8)
+#undef PITCH_SCORES
+    default: return hipErrorInvalidValue;
+  }
+  switch (a.vbits) {
+#define PITCH_VALUES(B) \
+  case B: hipLaunchKernelGGL((attn_values<D, B, NQ>), grid, dim3(kBlock), 0, s, a); break;
+    PITCH_VALUES(2) PITCH_VALUES(3) PITCH_VALUES(4) PITCH_VALUES(5) PITCH_VALUES(6) PITCH_VALUES(7) PITCH_VALUES(8)
+#undef PITCH_VALUES
+    default: return hipErrorInvalidValue;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+#define PITCH_CAT2(a, b) a##b
+#define PITCH_CAT(a, b) PITCH_CAT2(a, b)
+
+hipError_t PITCH_CAT(launch_attention_d, PITCH_DIM)(const AttnArgs& a, hipStream_t s) {
+  constexpr int D = PITCH_DIM;
+  static_assert(D == 64 || D == 128, "attention dimensions");
+  if (a.dim != (uint32_t)D || a.chunk == 0 || a.chunk > (uint32_t)kMaxChunk || a.chunks == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
+  hipError_t e;
+  switch (a.nqp) {
+    case 1: e = launch_nq<1>(a, s); break;
+    case 2: e = launch_nq<2>(a, s); break;
+    case 4: e = launch_nq<4>(a, s); break;
+    case 8: e = launch_nq<8>(a, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((attn_combine<D>), dim3(a.kv_heads * a.nq), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace pitch

@@ -129,6 +129,31 @@ __device__ __forceinline__ void fwht(F (&v)[Geom<D>::E], int t) {
   });
 }
 
+// Unnormalised Walsh-Hadamard transform of E contiguous coordinates per lane across a team of T lanes:
+// coordinate c = t * E + e; stages in the reference's order, bits >= log2 E cross lanes.
+template <int E, int T, typename F>
+__device__ __forceinline__ void fwht_contig(F (&v)[E], int t) {
+  static_for<0, ilog2(E) + ilog2(T)>([&](auto bit_c) {
+    constexpr int bit = decltype(bit_c)::value;
+    if constexpr (bit < ilog2(E)) {
+      constexpr int m = 1 << bit;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if (!(e & m)) {
+          const F a = v[e], b = v[e | m];
+          v[e] = a + b;
+          v[e | m] = a - b;
+        }
+      }
+    } else {
+      constexpr int lm = 1 << (bit - ilog2(E));
+      const F sg = (t & lm) ? F(-1) : F(1);
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[e] = fma_t(v[e], sg, xchg<lm>(v[e]));
+    }
+  });
+}
+
 // Reduction over the team (all lanes end with the result).
 template <int T, typename F, typename Op>
 __device__ __forceinline__ F team_reduce(F x, Op op) {

@@ -47,6 +47,34 @@ struct PackArgs {
   uint32_t bits;
 };
 
+// Arguments of one decode-phase attention launch over compressed K and V caches (see pitch_attention.hip).
+// Vector index of (KV head h, token t) in both caches: t * token_stride + h * head_stride.
+struct AttnArgs {
+  const float* q;            // [kv_heads][nq][dim] fp32 queries
+  const uint32_t* k_codes;   // per-vector codes of the keys
+  const float* k_scales;     // key norms (TurboQuant) or rmax (PolarQuant)
+  const uint32_t* v_codes;
+  const float* v_scales;
+  float* out;                // [kv_heads][nq][dim] fp32
+  float* lse;                // [kv_heads][nq] natural-log sum of exp of the scaled scores, or null
+  float* ws;                 // workspace (attention_workspace_floats floats)
+  uint64_t tokens;           // cached tokens per KV head
+  uint64_t token_stride;
+  uint64_t head_stride;
+  uint32_t dim, nq, nqp;     // head dim; query heads per KV head; nq rounded up to 1, 2, 4 or 8
+  uint32_t kv_heads;
+  uint32_t kbits, vbits, kpolar, vpolar, kseed, vseed;
+  uint32_t chunk, chunks;    // tokens per workgroup and chunks per KV head
+  float qscale;              // softmax scale * log2(e) / sqrt(dim), folded into the rotated queries
+  float oscale;              // 1 / sqrt(dim) of the value decode
+};
+
+// Chunk length (tokens per workgroup) the attention kernels use for a call, and the workspace it needs.
+uint32_t attention_chunk_tokens(uint64_t tokens, uint32_t kv_heads);
+uint64_t attention_workspace_floats(uint32_t dim, uint32_t nqp, uint32_t kv_heads, uint64_t tokens, uint32_t chunk);
+hipError_t launch_attention_d64(const AttnArgs& a, hipStream_t s);
+hipError_t launch_attention_d128(const AttnArgs& a, hipStream_t s);
+
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 

@@ -611,30 +611,6 @@ struct Lpv {
   static_assert(E % K == 0 && (V * QPV) % 64 == 0, "a chunk stays inside one team lane's coordinates");
 };
 
-// Transform of E contiguous coordinates per lane across a team of T lanes (bits >= log2 E cross lanes).
-template <int E, int T, typename F>
-__device__ __forceinline__ void fwht_contig(F (&v)[E], int t) {
-  static_for<0, ilog2(E) + ilog2(T)>([&](auto bit_c) {
-    constexpr int bit = decltype(bit_c)::value;
-    if constexpr (bit < ilog2(E)) {
-      constexpr int m = 1 << bit;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        if (!(e & m)) {
-          const F a = v[e], b = v[e | m];
-          v[e] = a + b;
-          v[e | m] = a - b;
-        }
-      }
-    } else {
-      constexpr int lm = 1 << (bit - ilog2(E));
-      const F sg = (t & lm) ? F(-1) : F(1);
-#pragma unroll
-      for (int e = 0; e < E; ++e) v[e] = fma_t(v[e], sg, xchg<lm>(v[e]));
-    }
-  });
-}
-
 // Coalesced load of the wave's block of V vectors as raw 16-byte chunks (vectors past the end re-read the
 // last one).
 template <int D, int IO>

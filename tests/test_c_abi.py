@@ -273,3 +273,75 @@ def test_channel_io_entry_points_validate_type_and_sizes(lib):
         for rc in (enc(io, Host(n * 128)), dec(io, Host(n * 128))):
             assert rc in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
             assert "needs" not in _lib.last_error()
+
+
+# ----------------------------------------------------------------------------- attention over compressed caches
+def _attn_desc(nq=4, kv=2, T=100, ts=1, hs=100, scale=0.125):
+    return _lib.PitchAttentionDescC(nq, kv, T, ts, hs, scale, 0)
+
+
+def _attn(lib, kc, vc, desc, sizes=None, ws=None, lse=True):
+    """Calls pitch_enqueue_attention_decode with host buffers sized by `sizes` (never reaching a kernel)."""
+    dim = kc.dim
+    nq, kv, T = desc.q_per_kv, desc.kv_heads, desc.tokens
+    vecs = min((T - 1) * desc.token_stride + (kv - 1) * desc.head_stride + 1, 1 << 20)
+    kcs, vcs = ((dim * kc.bits + 31) // 32) * 4, ((dim * vc.bits + 31) // 32) * 4
+    need = dict(q=kv * nq * dim * 4, kcodes=vecs * kcs, kscales=vecs * 4, vcodes=vecs * vcs, vscales=vecs * 4,
+                out=kv * nq * dim * 4, lse=kv * nq * 4)
+    need.update(sizes or {})
+    bufs = {k: Host(v) for k, v in need.items()}
+    if ws is None:
+        n = ctypes.c_uint64(0)
+        assert lib.pitch_attention_workspace_size(ctypes.byref(kc), ctypes.byref(vc), ctypes.byref(desc),
+                                                  ctypes.byref(n)) == 0
+        ws = n.value
+    w = Host(ws)
+    args = []
+    for k in ("q", "kcodes", "kscales", "vcodes", "vscales", "out"):
+        args += [bufs[k].p, bufs[k].nbytes, 0]
+    args += [bufs["lse"].p, bufs["lse"].nbytes, 0] if lse else [None, 0, 0]
+    return lib.pitch_enqueue_attention_decode(ctypes.byref(kc), ctypes.byref(vc), ctypes.byref(desc), *args,
+                                              w.p, w.nbytes, None)
+
+
+def test_attention_workspace_size(lib):
+    kc = _lib.PitchConfigC(0, 128, 4, 0)
+    n = ctypes.c_uint64(0)
+    sizes = []
+    for T in (1, 1000, 100000):
+        assert lib.pitch_attention_workspace_size(ctypes.byref(kc), ctypes.byref(kc), ctypes.byref(_attn_desc(4, 8, T)),
+                                                  ctypes.byref(n)) == 0
+        sizes.append(n.value)
+    assert 0 < sizes[0] < sizes[1] < sizes[2]
+    # at least the rotated queries and one weight per token and query head
+    assert sizes[2] >= 4 * 8 * 4 * (128 + 100000)
+
+
+def test_attention_validation(lib):
+    k = _lib.PitchConfigC(0, 128, 4, 0)
+    v = _lib.PitchConfigC(1, 128, 2, 9)
+    d = _attn_desc()
+    assert _attn(lib, k, _lib.PitchConfigC(0, 64, 4, 0), d, ws=1 << 20) == _lib.ERR_CONFIGURATION_MISMATCH
+    assert _attn(lib, _lib.PitchConfigC(0, 256, 4, 0), _lib.PitchConfigC(0, 256, 4, 0), d, ws=1 << 20) \
+        == _lib.ERR_INVALID_DIMENSION
+    for bad in (_attn_desc(nq=0), _attn_desc(nq=9), _attn_desc(kv=0), _attn_desc(T=0), _attn_desc(scale=float("inf"))):
+        assert _attn(lib, k, v, bad, ws=1 << 20) == _lib.ERR_INVALID_INPUT
+    base = _attn(lib, k, v, d)                      # exact sizes pass every check before the device check
+    assert base in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE) and "needs" not in _lib.last_error()
+    # one byte short in any buffer fails the size check
+    vecs = 99 + 100 + 1
+    short = dict(q=2 * 4 * 128 * 4 - 4, kcodes=vecs * 64 - 4, kscales=vecs * 4 - 4, vcodes=vecs * 32 - 4,
+                 vscales=vecs * 4 - 4, out=2 * 4 * 128 * 4 - 4, lse=2 * 4 * 4 - 4)
+    for name, size in short.items():
+        assert _attn(lib, k, v, d, sizes={name: size}) == _lib.ERR_INVALID_INPUT, name
+        assert "needs" in _lib.last_error()
+    n = ctypes.c_uint64(0)
+    lib.pitch_attention_workspace_size(ctypes.byref(k), ctypes.byref(v), ctypes.byref(d), ctypes.byref(n))
+    assert _attn(lib, k, v, d, ws=n.value - 4) == _lib.ERR_INVALID_INPUT and "workspace" in _lib.last_error()
+    # lse is optional; token-major strides size the caches by the largest vector index
+    assert _attn(lib, k, v, d, lse=False) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+    tm = _attn_desc(nq=1, kv=3, T=50, ts=3, hs=1)
+    assert _attn(lib, k, v, tm, sizes={"kscales": (49 * 3 + 2 + 1) * 4 - 4}) == _lib.ERR_INVALID_INPUT
+    small = {x: 4096 for x in ("q", "kcodes", "kscales", "vcodes", "vscales", "out", "lse")}
+    assert _attn(lib, k, v, _attn_desc(T=2, ts=1 << 62, hs=1 << 62), sizes=small, ws=1 << 20) == _lib.ERR_INVALID_INPUT
+    assert "overflow" in _lib.last_error()
