@@ -8,8 +8,9 @@ A step is one full-cache decode of the GPT-2-small-shaped value cache (32768 tok
 HBM. Steps rotate over --sets independent buffer sets (default 8, ~0.9 GB) so the 256 MB Infinity Cache
 cannot serve them. value = algorithmic bytes per step / time per step, with algorithmic bytes
 n * (4d + codeStride + 4). One JSON line is printed; --extras adds the other BASELINE configs
-(bulk encode, append-encode latency, KIVI, d=128 TurboQuant/PolarQuant) under "extra", and --full adds
-config 5 (Llama-3-8B long context, ~80 GB of buffers) and the d=1024 sweep.
+(bulk encode, append-encode latency, KIVI, d=128 TurboQuant/PolarQuant), float16/bfloat16 caches and
+decode-step attention over compressed caches under "extra", and --full adds config 5 (Llama-3-8B long
+context, ~80 GB of buffers) and the d=1024 sweep.
 
 Before timing, encode output is checked against the CPU oracle on a sample (codes may differ only at
 near-boundary coordinates); the benchmark refuses to report otherwise.
@@ -353,6 +354,66 @@ def run_extras(torch, q, P, O, timer, gen, dev, args, x, sets) -> dict:
                                          "parity_code_diffs_near_boundary": diffs}
         del c, s_, o
     out.update(run_io16(torch, q, P, timer, gen, dev, args, x, keys4))
+    out.update(run_attention(torch, q, P, O, timer, gen, dev, args))
+    return out
+
+
+def run_attention(torch, q, P, O, timer, gen, dev, args) -> dict:
+    """Decode-step attention directly over TurboQuant b=4 K and V caches (pitch_enqueue_attention_decode),
+    against decoding both caches to fp32 and attending with torch (the reference's flow: decode, then attend).
+    Algorithmic bytes per call are the compressed caches' codes and scales: kv_heads * T * 2 * (cs + 4)."""
+    import numpy as np
+    out = {}
+    steps, warm = max(20, args.steps // 4), 5
+    for label, kv, nq, d, T in (("cfg2_gpt2_attention_T32768", 12, 1, 64, 32768),
+                                ("cfg5_llama3_8b_layer_attention_T32768", 8, 4, 128, 32768),
+                                ("cfg5_llama3_8b_layer_attention_T131072", 8, 4, 128, 131072)):
+        cfg = P.QuantConfig("turboQuant", d, 4)
+        n = kv * T
+        K = torch.randn(kv, T, d, generator=gen, device=dev)
+        V = torch.randn(kv, T, d, generator=gen, device=dev)
+        kc = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=dev)
+        vc = torch.empty_like(kc)
+        ks = torch.empty(n, device=dev)
+        vs = torch.empty_like(ks)
+        q.enqueueEncode(K, kc, ks, n, cfg)
+        q.enqueueEncode(V, vc, vs, n, cfg)
+        del K, V
+        Q = torch.randn(kv, nq, d, generator=gen, device=dev)
+        o = torch.empty(kv, nq, d, device=dev)
+        lse = torch.empty(kv, nq, device=dev)
+        ws = torch.empty(P.attention_workspace_bytes(cfg, cfg, T, nq, kv), dtype=torch.uint8, device=dev)
+        ms = timer.time(lambda i: q.enqueueAttentionDecode(Q, kc, ks, vc, vs, o, T, cfg, qPerKv=nq, kvHeads=kv,
+                                                           lse=lse, workspace=ws), steps, warm)
+        Kd = torch.empty(n, d, device=dev)
+        Vd = torch.empty(n, d, device=dev)
+
+        def decode_then_attend(i):
+            q.enqueueDecode(kc, ks, Kd, n, cfg)
+            q.enqueueDecode(vc, vs, Vd, n, cfg)
+            S = torch.bmm(Q, Kd.view(kv, T, d).transpose(1, 2).contiguous()) / math.sqrt(d)
+            return torch.bmm(torch.softmax(S, -1), Vd.view(kv, T, d))
+
+        ms_b = timer.time(decode_then_attend, max(5, steps // 4), 2)
+        # parity: head 0 against the float64 oracle over the same codes
+        torch.cuda.synchronize()
+        cs = cfg.codeStride
+        ck = O.unpack_codes(kc[:T * cs].cpu().numpy().tobytes(), T, d, 4)
+        cv = O.unpack_codes(vc[:T * cs].cpu().numpy().tobytes(), T, d, 4)
+        ro, rl = O.attention_decode(Q[0].cpu().numpy().astype(np.float64), ck, ks[:T].cpu().numpy(), cv,
+                                    vs[:T].cpu().numpy(), "turboQuant", 4, "turboQuant", 4, 1 / math.sqrt(d))
+        got = o[0].cpu().numpy().astype(np.float64)
+        rel = float(max(np.linalg.norm(got[i] - ro[i]) / np.linalg.norm(ro[i]) for i in range(nq)))
+        if rel > 1e-5:
+            raise SystemExit(f"attention parity failed for {label}: rel L2 {rel}")
+        nb = n * 2 * (cs + 4)
+        out[label] = {"kv_heads": kv, "q_per_kv": nq, "dim": d, "tokens": T, "ms": round(ms, 5),
+                      "cache_tokens_per_s": round(n / ms * 1e3, 1), "codes_gbps": round(nb / ms / 1e6, 1),
+                      "codes_pct_peak": round(nb / ms / 1e6 / PEAK_GBPS * 100, 1),
+                      "decode_then_attend_ms": round(ms_b, 4), "speedup_vs_decode_then_attend": round(ms_b / ms, 2),
+                      "parity_max_rel_l2_head0": rel}
+        del kc, vc, ks, vs, Kd, Vd, ws
+        torch.cuda.empty_cache()
     return out
 
 

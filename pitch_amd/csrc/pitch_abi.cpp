@@ -313,9 +313,17 @@ int device_cu_count() {
 }
 
 uint32_t attention_chunk_tokens(uint64_t tokens, uint32_t kv_heads) {
-  // 256, 512 or 1024 tokens per workgroup: the largest that still gives about 1024 workgroups
-  const uint64_t blocks = (tokens + 255) / 256 * kv_heads;
-  return blocks >= 4096 ? 1024u : (blocks >= 2048 ? 512u : 256u);
+  // PITCH_ATTN_CHUNK (64 ... 1024, a power of two) overrides the choice (tuning aid); otherwise the largest
+  // chunk that still gives at least 512 workgroups (two per compute unit), between 128 and 1024 tokens
+  static const uint32_t override_chunk = [] {
+    const char* e = std::getenv("PITCH_ATTN_CHUNK");
+    const int v = e ? std::atoi(e) : 0;
+    return (v >= 64 && v <= 1024 && (v & (v - 1)) == 0) ? (uint32_t)v : 0u;
+  }();
+  if (override_chunk) return override_chunk;
+  uint32_t chunk = 1024;
+  while (chunk > 128 && (tokens + chunk - 1) / chunk * kv_heads < 512) chunk >>= 1;
+  return chunk;
 }
 
 uint64_t attention_workspace_floats(uint32_t dim, uint32_t nqp, uint32_t kv_heads, uint64_t tokens, uint32_t chunk) {

@@ -172,13 +172,23 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
   __syncthreads();
   const float* __restrict__ qp = qp_all + (uint64_t)kv * D * NQ;
 
+  // software pipeline: the next token's code row and scale are loaded before this token's scores are computed
+  auto fetch = [&](uint32_t i, uint32_t (&w)[NW], float& nk) {
+    const uint64_t vi = (t0 + (i < n ? i : 0u)) * a.token_stride + (uint64_t)kv * a.head_stride;
+    load_row<NW>(a.k_codes + vi * NW, w);
+    nk = a.k_scales[vi];
+  };
+  uint32_t wn[NW];
+  float nkn;
+  fetch(tid, wn, nkn);
   for (uint32_t i0 = 0; i0 < n; i0 += kBlock) {
     const uint32_t i = i0 + tid;
     const bool valid = i < n;
-    const uint64_t vi = (t0 + (valid ? i : 0)) * a.token_stride + (uint64_t)kv * a.head_stride;
     uint32_t w[NW];
-    load_row<NW>(a.k_codes + vi * NW, w);
-    const float nk = a.k_scales[vi];
+#pragma unroll
+    for (int k = 0; k < NW; ++k) w[k] = wn[k];
+    const float nk = nkn;
+    if (i0 + kBlock < n) fetch(i + kBlock, wn, nkn);
     float acc[NQ];
 #pragma unroll
     for (int h = 0; h < NQ; ++h) acc[h] = 0.f;
@@ -273,22 +283,28 @@ __global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
 #pragma unroll
     for (int e = 0; e < 2 * PPL; ++e) acc[h][e] = 0.f;
 
+  // software pipeline: each thread loads the code row, scale and weights of its token of the next block while
+  // the current block is accumulated
+  auto fetch = [&](uint32_t i, uint32_t (&w)[NW], float (&wt)[NQ]) {
+    const bool valid = i < n;
+    const uint32_t iv = valid ? i : 0u;
+    const uint64_t vi = (t0 + iv) * a.token_stride + (uint64_t)kv * a.head_stride;
+    load_row<NW>(a.v_codes + vi * NW, w);
+    const float nv = valid ? a.v_scales[vi] : 0.f;
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) wt[h] = pw[(uint64_t)iv * NQ + h] * nv;
+  };
+  uint32_t rown[NW];
+  float wtn[NQ];
+  fetch(tid, rown, wtn);
   for (uint32_t i0 = 0; i0 < n; i0 += kBlock) {
     __syncthreads();  // the previous block's readers are done (and, the first time, the table is built)
-    {
-      const uint32_t i = i0 + tid;
-      const bool valid = i < n;
-      const uint32_t iv = valid ? i : 0u;
-      const uint64_t vi = (t0 + iv) * a.token_stride + (uint64_t)kv * a.head_stride;
-      uint32_t w[NW];
-      load_row<NW>(a.v_codes + vi * NW, w);
 #pragma unroll
-      for (int k = 0; k < NW; ++k) s_code[tid * RS + k] = w[k];
-      const float nv = valid ? a.v_scales[vi] : 0.f;
+    for (int k = 0; k < NW; ++k) s_code[tid * RS + k] = rown[k];
 #pragma unroll
-      for (int h = 0; h < NQ; ++h) s_w[tid * NQ + h] = pw[(uint64_t)iv * NQ + h] * nv;
-    }
+    for (int h = 0; h < NQ; ++h) s_w[tid * NQ + h] = wtn[h];
     __syncthreads();
+    if (i0 + kBlock < n) fetch(i0 + kBlock + tid, rown, wtn);
     const uint32_t nt = min((uint32_t)kBlock, n - i0);
     for (uint32_t s0 = 0; s0 < nt; s0 += 16) {
       const uint32_t tok = s0 + wid * 4 + r;
@@ -370,11 +386,27 @@ __global__ __launch_bounds__(kBlock) void attn_combine(AttnArgs a) {
   float ls = 0.f, acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  for (uint32_t c = wid; c < a.chunks; c += 4) {
-    const float f = exp2f(ml[2 * c] - M);
-    ls = __builtin_fmaf(ml[2 * c + 1], f, ls);
+  // chunks c = wid, wid + 4, ...; loads are issued kU chunks at a time so they overlap
+  constexpr int kU = 16;
+  for (uint32_t c0 = wid; c0 < a.chunks; c0 += 4 * kU) {
+    float mv[kU], lv[kU], av[kU][E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] = __builtin_fmaf(A[(uint64_t)c * D + lane * E + e], f, acc[e]);
+    for (int u = 0; u < kU; ++u) {
+      const uint32_t c = c0 + 4 * u;
+      const bool in = c < a.chunks;
+      const uint32_t cc = in ? c : c0;
+      mv[u] = in ? ml[2 * cc] : -__builtin_inff();
+      lv[u] = ml[2 * cc + 1];
+#pragma unroll
+      for (int e = 0; e < E; ++e) av[u][e] = A[(uint64_t)cc * D + lane * E + e];
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const float f = exp2f(mv[u] - M);  // 0 for chunks past the end
+      ls = __builtin_fmaf(lv[u], f, ls);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = __builtin_fmaf(av[u][e], f, acc[e]);
+    }
   }
 #pragma unroll
   for (int e = 0; e < E; ++e) s_part[wid * (D + 1) + lane * E + e] = acc[e];
@@ -430,7 +462,7 @@ hipError_t launch_nq(const AttnArgs& a, hipStream_t s) {
 hipError_t PITCH_CAT(launch_attention_d, PITCH_DIM)(const AttnArgs& a, hipStream_t s) {
   constexpr int D = PITCH_DIM;
   static_assert(D == 64 || D == 128, "attention dimensions");
-  if (a.dim != (uint32_t)D || a.chunk == 0 || a.chunk > (uint32_t)kMaxChunk || a.chunks == 0) return hipErrorInvalidValue;
+  if (a.dim != (uint32_t)D || a.chunk < 64 || a.chunk > (uint32_t)kMaxChunk || a.chunks == 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
   hipError_t e;
   switch (a.nqp) {
