@@ -116,6 +116,35 @@ int pitch_enqueue_decode_io(const pitch_config_t* config, uint32_t io_type, cons
                             uint64_t scales_offset, void* output, uint64_t output_bytes, uint64_t output_offset,
                             uint64_t count, void* stream);
 
+/* Key-projection bias removal for the per-vector methods (reference/mechanism_eval.py:88-97,113-116: a model
+ * whose key projection adds a bias b before RoPE has keys k = R_t W x + R_t b; compressing k - R_t b and adding
+ * R_t b back restores the per-vector methods, README.md:28; "not yet built into the kernels", README.md:100).
+ * Vector v of a call is token first_position + v / heads of head v % heads (a token-major [t][h] cache) and
+ * carries o = b_h * cos_t + rotate_half(b_h) * sin_t, rotate_half(x) = (-x[dim/2:], x[:dim/2]), in float32 with
+ * each product and the sum rounded once. All three tables are fp32 device memory. */
+typedef struct pitch_key_bias {
+  const void* bias;        /* [heads][dim]: the key projection's bias per KV head, before RoPE */
+  uint64_t bias_bytes;
+  const void* cos;         /* [positions][dim]: the model's RoPE cosines (rotate_half layout) */
+  const void* sin;         /* [positions][dim]: the model's RoPE sines */
+  uint64_t table_bytes;    /* bytes of cos and of sin each; positions = table_bytes / (4 * dim) */
+  uint64_t first_position; /* position of the call's first token */
+  uint32_t heads;          /* KV heads per token */
+  uint32_t reserved;       /* 0 */
+} pitch_key_bias_t;
+
+/* pitch_enqueue_encode of x - o (fp32 input): the scales are the norms (or rmax) of the debiased keys. */
+int pitch_enqueue_encode_key_bias(const pitch_config_t* config, const pitch_key_bias_t* key_bias, const void* input,
+                                  uint64_t input_bytes, uint64_t input_offset, void* codes, uint64_t codes_bytes,
+                                  uint64_t codes_offset, void* scales, uint64_t scales_bytes, uint64_t scales_offset,
+                                  uint64_t count, void* stream);
+
+/* pitch_enqueue_decode followed by + o (fp32 output). */
+int pitch_enqueue_decode_key_bias(const pitch_config_t* config, const pitch_key_bias_t* key_bias, const void* codes,
+                                  uint64_t codes_bytes, uint64_t codes_offset, const void* scales,
+                                  uint64_t scales_bytes, uint64_t scales_offset, void* output, uint64_t output_bytes,
+                                  uint64_t output_offset, uint64_t count, void* stream);
+
 /* Encodes count tokens of one head's keys (token-major, dim channels) per channel over groups of
  * group_size tokens: writes count * code_stride bytes of codes and ceil(count / group_size) * range_stride
  * bytes of fp16 ranges laid out [group][min row of dim][max row of dim].
@@ -153,6 +182,19 @@ int pitch_enqueue_channel_decode_io(const pitch_channel_config_t* config, uint32
                                     uint64_t ranges_bytes, uint64_t ranges_offset, void* output,
                                     uint64_t output_bytes, uint64_t output_offset, uint64_t count,
                                     void* stream);
+
+/* Appends new_tokens tokens to one head's per-channel cache that already holds total_tokens - new_tokens of
+ * them, re-encoding every group the new tokens touch: a partial last group is encoded again over all of its
+ * tokens, so its fp16 ranges always cover the tokens it holds ("the newest, partial group can be kept in full
+ * precision or re-encoded as it grows", README.md:85; the reference's ChannelCompressedBlock.append refuses
+ * to append after a partial group, Sources/PITCH/PerChannel.swift:120-130). input holds the head's keys of
+ * tokens [0, total_tokens) in the element type io_type (only the touched groups are read); codes and ranges
+ * are the head's whole cache buffers, laid out as pitch_enqueue_channel_encode writes them. The result is
+ * byte for byte that of one pitch_enqueue_channel_encode_io over all total_tokens tokens. */
+int pitch_enqueue_channel_append(const pitch_channel_config_t* config, uint32_t io_type, const void* input,
+                                 uint64_t input_bytes, uint64_t input_offset, void* codes, uint64_t codes_bytes,
+                                 uint64_t codes_offset, void* ranges, uint64_t ranges_bytes, uint64_t ranges_offset,
+                                 uint64_t total_tokens, uint64_t new_tokens, void* stream);
 
 /* Decode-phase attention over compressed caches (no counterpart in the reference: it evaluates attention on
  * decoded caches, reference/attention_extra.py:70-74, and names decoding inside attention as its next step,

@@ -311,6 +311,27 @@ def round_io(x, io: str) -> np.ndarray:
     return from_io_bits(to_io_bits(x, io), io)
 
 
+# ----------------------------------------------------------------------------- key-bias removal
+def rotate_half(x: np.ndarray) -> np.ndarray:
+    """(-x[d/2:], x[:d/2]) along the last axis: the rotate_half of the RoPE models the reference evaluates
+    (reference/mechanism_eval.py:84, the model module's own rotate_half)."""
+    d = x.shape[-1]
+    return np.concatenate([-x[..., d // 2:], x[..., :d // 2]], axis=-1)
+
+
+def key_bias_offsets(bias, cos, sin, first_position: int, count: int, heads: int) -> np.ndarray:
+    """R_t b_h for vectors 0..count-1 of a token-major [t][h] cache: token first_position + v // heads, head
+    v % heads; bb * cos + rotate_half(bb) * sin in float32 with each product and the sum rounded once
+    (reference/mechanism_eval.py:88-97, rotated_bias)."""
+    f32 = np.float32
+    v = np.arange(count)
+    t = first_position + v // heads
+    b = np.asarray(bias, f32)[v % heads]
+    t1 = (b * np.asarray(cos, f32)[t]).astype(f32)
+    t2 = (rotate_half(b) * np.asarray(sin, f32)[t]).astype(f32)
+    return (t1 + t2).astype(f32)
+
+
 # ----------------------------------------------------------------------------- attention on decoded caches
 def log_softmax(S: np.ndarray) -> np.ndarray:
     """Row-wise log-softmax, float64. reference/attention_eval.py:31-33."""

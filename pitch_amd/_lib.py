@@ -36,6 +36,12 @@ class PitchAttentionDescC(ctypes.Structure):
                 ("reserved", ctypes.c_uint32)]
 
 
+class PitchKeyBiasC(ctypes.Structure):
+    _fields_ = [("bias", ctypes.c_void_p), ("bias_bytes", ctypes.c_uint64), ("cos", ctypes.c_void_p),
+                ("sin", ctypes.c_void_p), ("table_bytes", ctypes.c_uint64), ("first_position", ctypes.c_uint64),
+                ("heads", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
 class PitchChannelConfigC(ctypes.Structure):
     _fields_ = [("dim", ctypes.c_uint32), ("bits", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
                 ("reserved", ctypes.c_uint32)]
@@ -66,6 +72,12 @@ SIGNATURES = {
                                                _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_channel_decode_io": (_int, [ctypes.POINTER(PitchChannelConfigC), _u32, _vp, _u64, _u64, _vp,
                                                _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_encode_key_bias": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchKeyBiasC), _vp, _u64,
+                                             _u64, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_decode_key_bias": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchKeyBiasC), _vp, _u64,
+                                             _u64, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_enqueue_channel_append": (_int, [ctypes.POINTER(PitchChannelConfigC), _u32, _vp, _u64, _u64, _vp, _u64,
+                                            _u64, _vp, _u64, _u64, _u64, _u64, _vp]),
     "pitch_attention_workspace_size": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
                                               ctypes.POINTER(PitchAttentionDescC), ctypes.POINTER(_u64)]),
     "pitch_enqueue_attention_decode": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),

@@ -485,6 +485,28 @@ def _validate_values(x, limit: float, what: str) -> None:
         raise InvalidInput(f"input magnitude {largest} exceeds {limit}; {what}")
 
 
+@dataclass
+class KeyBias:
+    """RoPE'd key-projection bias removed before encoding and restored after decoding (mechanism_eval.py:88-116):
+    bias [heads][dim], cos and sin [positions][dim] fp32 device tensors (the model's own rotary tables), the
+    position of the call's first token and the KV heads per token of a token-major cache."""
+    bias: object
+    cos: object
+    sin: object
+    firstPosition: int = 0
+    heads: int = 1
+
+    def _c(self) -> _lib.PitchKeyBiasC:
+        bp, bb = _buf(self.bias, "key bias")
+        cp, cb = _buf(self.cos, "RoPE cos")
+        sp, sb = _buf(self.sin, "RoPE sin")
+        if cb != sb:
+            raise InvalidInput("RoPE cos and sin tables differ in size")
+        if not isinstance(self.firstPosition, (int, np.integer)) or self.firstPosition < 0:
+            raise InvalidInput(f"firstPosition {self.firstPosition} must be a non-negative integer")
+        return _lib.PitchKeyBiasC(bp, bb, cp, sp, cb, int(self.firstPosition), int(self.heads), 0)
+
+
 # ----------------------------------------------------------------------------------------- PITCH
 class PITCH:
     """Public entry point (Sources/PITCH/PITCH.swift:15-189 and the PerChannel extension :182-290)."""
@@ -592,9 +614,11 @@ class PITCH:
 
     # ---- GPU-resident API (PITCH.swift:144-165)
     def enqueueEncode(self, input, codes, scales, count: int, config: QuantConfig, inputOffset: int = 0,
-                      codesOffset: int = 0, scalesOffset: int = 0, stream=None, elementType=None) -> None:
+                      codesOffset: int = 0, scalesOffset: int = 0, stream=None, elementType=None,
+                      keyBias: KeyBias | None = None) -> None:
         """Launches encoding of count vectors; results are valid once the stream reaches this point. The input's
-        element type is elementType, else the tensor's dtype when float16/bfloat16, else float32."""
+        element type is elementType, else the tensor's dtype when float16/bfloat16, else float32. With keyBias
+        (float32 only) the vectors x - R_t b are encoded."""
         ip, ib = _buf(input, "input")
         cp, cb = _buf(codes, "codes")
         sp, sb = _buf(scales, "scales")
@@ -602,15 +626,21 @@ class PITCH:
         io = _io_type(input, elementType)
         args = (ip, ib, inputOffset, cp, cb, codesOffset, sp, sb, scalesOffset, _count(count),
                 _stream_handle(stream, self.device))
-        if io == _lib.IO_F32:
+        if keyBias is not None:
+            if io != _lib.IO_F32:
+                raise InvalidInput("key-bias removal takes float32 vectors")
+            rc = self._lib.pitch_enqueue_encode_key_bias(ctypes.byref(config._c()), ctypes.byref(keyBias._c()), *args)
+        elif io == _lib.IO_F32:
             rc = self._lib.pitch_enqueue_encode(ctypes.byref(config._c()), *args)
         else:
             rc = self._lib.pitch_enqueue_encode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
 
     def enqueueDecode(self, codes, scales, output, count: int, config: QuantConfig, codesOffset: int = 0,
-                      scalesOffset: int = 0, outputOffset: int = 0, stream=None, elementType=None) -> None:
-        """Launches decoding of count vectors into output, whose element type is chosen as for enqueueEncode."""
+                      scalesOffset: int = 0, outputOffset: int = 0, stream=None, elementType=None,
+                      keyBias: KeyBias | None = None) -> None:
+        """Launches decoding of count vectors into output, whose element type is chosen as for enqueueEncode.
+        With keyBias (float32 only) R_t b is added back."""
         cp, cb = _buf(codes, "codes")
         sp, sb = _buf(scales, "scales")
         op, ob = _buf(output, "output")
@@ -618,10 +648,30 @@ class PITCH:
         io = _io_type(output, elementType)
         args = (cp, cb, codesOffset, sp, sb, scalesOffset, op, ob, outputOffset, _count(count),
                 _stream_handle(stream, self.device))
-        if io == _lib.IO_F32:
+        if keyBias is not None:
+            if io != _lib.IO_F32:
+                raise InvalidInput("key-bias removal takes float32 vectors")
+            rc = self._lib.pitch_enqueue_decode_key_bias(ctypes.byref(config._c()), ctypes.byref(keyBias._c()), *args)
+        elif io == _lib.IO_F32:
             rc = self._lib.pitch_enqueue_decode(ctypes.byref(config._c()), *args)
         else:
             rc = self._lib.pitch_enqueue_decode_io(ctypes.byref(config._c()), io, *args)
+        _raise_for(rc)
+
+    def enqueuePerChannelAppend(self, input, codes, ranges, totalTokens: int, newTokens: int,
+                                config: ChannelQuantConfig, inputOffset: int = 0, codesOffset: int = 0,
+                                rangesOffset: int = 0, stream=None, elementType=None) -> None:
+        """Appends newTokens to a head's per-channel cache of totalTokens - newTokens tokens, re-encoding the
+        groups they touch (a growing partial group is re-encoded over all its tokens; README.md:85). input, codes
+        and ranges are the head's whole buffers; the result equals one encode of all totalTokens tokens."""
+        ip, ib = _buf(input, "input")
+        cp, cb = _buf(codes, "codes")
+        rp, rb = _buf(ranges, "ranges")
+        _check_offsets(inputOffset, codesOffset, rangesOffset)
+        rc = self._lib.pitch_enqueue_channel_append(ctypes.byref(config._c()), _io_type(input, elementType), ip, ib,
+                                                    inputOffset, cp, cb, codesOffset, rp, rb, rangesOffset,
+                                                    _count(totalTokens), _count(newTokens),
+                                                    _stream_handle(stream, self.device))
         _raise_for(rc)
 
     # ---- attention over compressed caches (no counterpart in the reference; README.md:96)

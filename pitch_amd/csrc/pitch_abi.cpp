@@ -143,9 +143,39 @@ int check_io(uint32_t io) {
   return PITCH_OK;
 }
 
+// Checks the sizes of a key-bias description for count vectors of dimension dim (no device access).
+int check_key_bias(const pitch_key_bias_t* kb, uint32_t dim, uint64_t count) {
+  if (!kb) return PITCH_OK;
+  if (kb->heads < 1) return fail(PITCH_ERR_INVALID_INPUT, "key bias heads must be at least 1");
+  PITCH_TRY(check_buffer(kb->bias, kb->bias_bytes, 0, (uint64_t)kb->heads * dim * 4u, "key bias"));
+  const uint64_t tokens = (count + kb->heads - 1) / kb->heads;
+  const uint64_t rows = kb->table_bytes / (4ull * dim);
+  if (kb->first_position > rows || rows - kb->first_position < tokens)
+    return fail(PITCH_ERR_INVALID_INPUT, "RoPE tables hold %llu positions; the call needs %llu from position %llu",
+                (unsigned long long)rows, (unsigned long long)tokens, (unsigned long long)kb->first_position);
+  PITCH_TRY(check_buffer(kb->cos, kb->table_bytes, 0, 0, "RoPE cos"));
+  PITCH_TRY(check_buffer(kb->sin, kb->table_bytes, 0, 0, "RoPE sin"));
+  return PITCH_OK;
+}
+
+// Checks that the key-bias tables are memory of the device and fills the launch fields.
+int apply_key_bias(const pitch_key_bias_t* kb, int dev, pitch::VecArgs* a) {
+  if (!kb) return PITCH_OK;
+  PITCH_TRY(check_device(kb->bias, dev, "key bias"));
+  PITCH_TRY(check_device(kb->cos, dev, "RoPE cos"));
+  PITCH_TRY(check_device(kb->sin, dev, "RoPE sin"));
+  a->kb_bias = (const float*)kb->bias;
+  a->kb_cos = (const float*)kb->cos;
+  a->kb_sin = (const float*)kb->sin;
+  a->kb_first = kb->first_position;
+  a->kb_heads = kb->heads;
+  return PITCH_OK;
+}
+
 int encode_impl(const pitch_config_t* config, uint32_t io, const void* input, uint64_t input_bytes,
                 uint64_t input_offset, void* codes, uint64_t codes_bytes, uint64_t codes_offset, void* scales,
-                uint64_t scales_bytes, uint64_t scales_offset, uint64_t count, void* stream) {
+                uint64_t scales_bytes, uint64_t scales_offset, uint64_t count, void* stream,
+                const pitch_key_bias_t* kb = nullptr) {
   PITCH_TRY(validate_config(config));
   PITCH_TRY(check_io(io));
   const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
@@ -154,6 +184,7 @@ int encode_impl(const pitch_config_t* config, uint32_t io, const void* input, ui
   PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * io_bytes(io), "input"));
   PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
   PITCH_TRY(check_buffer(scales, scales_bytes, scales_offset, count * 4u, "scales"));
+  PITCH_TRY(check_key_bias(kb, dim, count));
   int dev = 0;
   PITCH_TRY(current_device(&dev));
   PITCH_TRY(check_device(input, dev, "input"));
@@ -165,6 +196,7 @@ int encode_impl(const pitch_config_t* config, uint32_t io, const void* input, ui
   a.scales_out = at<float>(scales, scales_offset);
   a.count = count;
   a.seed = config->seed;
+  PITCH_TRY(apply_key_bias(kb, dev, &a));
   const hipError_t e = launch_vec(dim, io, true, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
                                   (hipStream_t)stream);
   if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
@@ -173,7 +205,8 @@ int encode_impl(const pitch_config_t* config, uint32_t io, const void* input, ui
 
 int decode_impl(const pitch_config_t* config, uint32_t io, const void* codes, uint64_t codes_bytes,
                 uint64_t codes_offset, const void* scales, uint64_t scales_bytes, uint64_t scales_offset,
-                void* output, uint64_t output_bytes, uint64_t output_offset, uint64_t count, void* stream) {
+                void* output, uint64_t output_bytes, uint64_t output_offset, uint64_t count, void* stream,
+                const pitch_key_bias_t* kb = nullptr) {
   PITCH_TRY(validate_config(config));
   PITCH_TRY(check_io(io));
   const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
@@ -182,6 +215,7 @@ int decode_impl(const pitch_config_t* config, uint32_t io, const void* codes, ui
   PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
   PITCH_TRY(check_buffer(scales, scales_bytes, scales_offset, count * 4u, "scales"));
   PITCH_TRY(check_buffer(output, output_bytes, output_offset, count * dim * io_bytes(io), "output"));
+  PITCH_TRY(check_key_bias(kb, dim, count));
   int dev = 0;
   PITCH_TRY(current_device(&dev));
   PITCH_TRY(check_device(codes, dev, "codes"));
@@ -193,6 +227,7 @@ int decode_impl(const pitch_config_t* config, uint32_t io, const void* codes, ui
   a.out = at<char>(output, output_offset);
   a.count = count;
   a.seed = config->seed;
+  PITCH_TRY(apply_key_bias(kb, dev, &a));
   const hipError_t e = launch_vec(dim, io, false, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
                                   (hipStream_t)stream);
   if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));
@@ -418,6 +453,24 @@ int pitch_enqueue_decode_io(const pitch_config_t* config, uint32_t io_type, cons
                      output, output_bytes, output_offset, count, stream);
 }
 
+int pitch_enqueue_encode_key_bias(const pitch_config_t* config, const pitch_key_bias_t* key_bias, const void* input,
+                                  uint64_t input_bytes, uint64_t input_offset, void* codes, uint64_t codes_bytes,
+                                  uint64_t codes_offset, void* scales, uint64_t scales_bytes, uint64_t scales_offset,
+                                  uint64_t count, void* stream) {
+  if (!key_bias) return fail(PITCH_ERR_INVALID_INPUT, "key bias is null");
+  return encode_impl(config, PITCH_IO_F32, input, input_bytes, input_offset, codes, codes_bytes, codes_offset,
+                     scales, scales_bytes, scales_offset, count, stream, key_bias);
+}
+
+int pitch_enqueue_decode_key_bias(const pitch_config_t* config, const pitch_key_bias_t* key_bias, const void* codes,
+                                  uint64_t codes_bytes, uint64_t codes_offset, const void* scales,
+                                  uint64_t scales_bytes, uint64_t scales_offset, void* output, uint64_t output_bytes,
+                                  uint64_t output_offset, uint64_t count, void* stream) {
+  if (!key_bias) return fail(PITCH_ERR_INVALID_INPUT, "key bias is null");
+  return decode_impl(config, PITCH_IO_F32, codes, codes_bytes, codes_offset, scales, scales_bytes, scales_offset,
+                     output, output_bytes, output_offset, count, stream, key_bias);
+}
+
 int pitch_enqueue_channel_encode(const pitch_channel_config_t* config, const void* input,
                                  uint64_t input_bytes, uint64_t input_offset, void* codes,
                                  uint64_t codes_bytes, uint64_t codes_offset, void* ranges,
@@ -452,6 +505,31 @@ int pitch_enqueue_channel_decode_io(const pitch_channel_config_t* config, uint32
                                     void* stream) {
   return channel_decode_impl(config, io_type, codes, codes_bytes, codes_offset, ranges, ranges_bytes,
                              ranges_offset, output, output_bytes, output_offset, count, stream);
+}
+
+int pitch_enqueue_channel_append(const pitch_channel_config_t* config, uint32_t io_type, const void* input,
+                                 uint64_t input_bytes, uint64_t input_offset, void* codes, uint64_t codes_bytes,
+                                 uint64_t codes_offset, void* ranges, uint64_t ranges_bytes, uint64_t ranges_offset,
+                                 uint64_t total_tokens, uint64_t new_tokens, void* stream) {
+  PITCH_TRY(validate_channel_config(config));
+  PITCH_TRY(check_io(io_type));
+  if (new_tokens < 1) return fail(PITCH_ERR_INVALID_INPUT, "new tokens must be at least 1");
+  if (total_tokens < new_tokens)
+    return fail(PITCH_ERR_INVALID_INPUT, "total tokens %llu is below the %llu new tokens",
+                (unsigned long long)total_tokens, (unsigned long long)new_tokens);
+  if (total_tokens > 0xFFFFFFFFull) return fail(PITCH_ERR_INVALID_INPUT, "per-channel count must be below 2^32 tokens");
+  const uint32_t dim = config->dim, G = config->group_size, cs = code_stride_of(dim, config->bits);
+  const uint64_t esize = io_bytes(io_type);
+  // the whole cache must fit its buffers, as for one encode of total_tokens tokens
+  const uint64_t groups = (total_tokens + G - 1) / G;
+  PITCH_TRY(check_buffer(input, input_bytes, input_offset, total_tokens * dim * esize, "input"));
+  PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, total_tokens * cs, "codes"));
+  PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
+  // re-encode from the start of the group that holds the first new token
+  const uint64_t g0 = (total_tokens - new_tokens) / G, first = g0 * G;
+  return channel_encode_impl(config, io_type, input, input_bytes, input_offset + first * dim * esize, codes,
+                             codes_bytes, codes_offset + first * cs, ranges, ranges_bytes,
+                             ranges_offset + g0 * 4u * dim, total_tokens - first, stream);
 }
 
 int pitch_attention_workspace_size(const pitch_config_t* key_config, const pitch_config_t* value_config,

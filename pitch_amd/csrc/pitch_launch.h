@@ -16,7 +16,13 @@ struct VecArgs {
   void* out;                 // decode: count * dim elements of the I/O type
   uint64_t count;
   uint32_t seed;
-  uint32_t reserved;
+  uint32_t kb_heads;         // key-bias removal: heads per token (0 = no bias)
+  // Key-bias removal (null kb_bias = none): vector v is token kb_first + v / kb_heads of head v % kb_heads and
+  // carries the offset o = b * cos_t + rotate_half(b) * sin_t; encode takes x - o, decode writes x + o.
+  const float* kb_bias;      // [heads][dim]
+  const float* kb_cos;       // [positions][dim]
+  const float* kb_sin;       // [positions][dim]
+  uint64_t kb_first;
   // Rotation signs per team lane: bit e of lane_flips[t] is 1 when the coordinate held as element e by
   // team lane t has sign -1 (filled by the launcher from the seed).
   uint32_t lane_flips[32];

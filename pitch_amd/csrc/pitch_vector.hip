@@ -106,6 +106,25 @@ __device__ __forceinline__ double div_sqrt_d(double y) {
   else return y / C::kSqrt;
 }
 
+// Key-bias offset of coordinates [c, c + N) of vector v: o = b_h * cos_t + rotate_half(b_h) * sin_t with
+// rotate_half(x) = (-x[D/2:], x[:D/2]) (reference/mechanism_eval.py:88-97), each product and the sum rounded once
+// as the reference's float32 torch expression rounds them (the library is built with -ffp-contract=off).
+template <int D, int N>
+__device__ __forceinline__ void key_bias_offset(const VecArgs& p, uint64_t v, int c, float (&o)[N]) {
+  const uint64_t tok = v / p.kb_heads;
+  const uint32_t h = (uint32_t)(v - tok * p.kb_heads);
+  const float* b = p.kb_bias + (uint64_t)h * D;
+  const uint64_t row = (p.kb_first + tok) * D;
+#pragma unroll
+  for (int r = 0; r < N; ++r) {
+    const int j = c + r;
+    const float rh = j < D / 2 ? -b[j + D / 2] : b[j - D / 2];
+    const float t1 = b[j] * p.kb_cos[row + j];
+    const float t2 = rh * p.kb_sin[row + j];
+    o[r] = t1 + t2;
+  }
+}
+
 // TurboQuant quantiser: code = #{edges < u}, searchsorted(edges, u, 'left') (pitch_reference.py:99-101).
 // With a bucket table (gen_tables.py lut_for): j = clamp(floor(u * 2^m + off)), code = c_j + [u > e_j], one
 // 8-byte LDS read per coordinate (e_j as float32 bits, c_j). Lookups are issued in batches of up to 15 (what
@@ -197,7 +216,7 @@ struct TqQuant {
 #endif
 
 // ----------------------------------------------------------------------------------------------------
-template <int D, int B, bool POLAR, int IO>
+template <int D, int B, bool POLAR, int IO, bool KBIAS>
 __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
   using G = Geom<D>;
   constexpr int L = 1 << B;
@@ -236,6 +255,15 @@ __global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
     for (int k = 0; k < G::CH; ++k)
       load_elems<IO, G::W>(p.in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (KBIAS) {  // key-bias removal: encode x - o (mechanism_eval.py:113-116)
+#pragma unroll
+      for (int k = 0; k < G::CH; ++k) {
+        float o[G::W];
+        key_bias_offset<D, G::W>(p, valid ? v : p.count - 1, G::W * (k * G::T + t), o);
+#pragma unroll
+        for (int r = 0; r < G::W; ++r) f[k * G::W + r] = f[k * G::W + r] - o[r];
+      }
+    }
     double x[G::E];
 #pragma unroll
     for (int e = 0; e < G::E; ++e) x[e] = (double)__uint_as_float(__float_as_uint(f[e]) ^ flip[e]);
@@ -444,7 +472,7 @@ __device__ __forceinline__ void decode_chunk(uint32_t bits, const float* s_tab, 
 #define PITCH_DEC_WAVES 1  // minimum waves per SIMD requested for the decoders (caps their VGPRs)
 #endif
 
-template <int D, int B, bool POLAR, int IO>
+template <int D, int B, bool POLAR, int IO, bool KBIAS>
 __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p) {
   using G = Geom<D>;
   using TB = DecTab<B, POLAR, G::W>;
@@ -541,6 +569,13 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
           const float4 val = *(const float4*)(ws + vq * kVecStride + K * cq + 4 * h);
           o[4 * h] = val.x; o[4 * h + 1] = val.y; o[4 * h + 2] = val.z; o[4 * h + 3] = val.w;
         }
+        if constexpr (KBIAS) {  // key-bias removal: restore x + o (mechanism_eval.py:113-116)
+          float ob[K];
+          const uint64_t vv = wbase + vq < p.count ? wbase + vq : p.count - 1;
+          key_bias_offset<D, K>(p, vv, K * cq, ob);
+#pragma unroll
+          for (int r = 0; r < K; ++r) o[r] = o[r] + ob[r];
+        }
         if (!TAIL || wbase + vq < p.count) store_elems<IO, K>(p.out, wbase * D + (uint64_t)K * q, o, PITCH_NT_STORE);
       }
       __builtin_amdgcn_wave_barrier();
@@ -551,6 +586,12 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
 #pragma unroll
         for (int r = 0; r < G::W; ++r)
           o[r] = __uint_as_float(__float_as_uint(y[k * G::W + r] * f) ^ flip[k * G::W + r]);
+        if constexpr (KBIAS) {
+          float ob[G::W];
+          key_bias_offset<D, G::W>(p, v, G::W * (k * G::T + t), ob);
+#pragma unroll
+          for (int r = 0; r < G::W; ++r) o[r] = o[r] + ob[r];
+        }
         store_elems<IO, G::W>(p.out, v * D + G::W * (k * G::T + t), o, PITCH_NT_STORE);
       }
     }
@@ -646,7 +687,7 @@ __device__ __forceinline__ void chunk_floats(const u32x4& w, float (&f)[Io<IO>::
   }
 }
 
-template <int D, int B, int IO>
+template <int D, int B, int IO, bool KBIAS>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(PITCH_ENC_WAVES)))
 void tq_encode_lpv(VecArgs p) {
   using Lp = Lpv<D, IO>;
@@ -693,6 +734,12 @@ void tq_encode_lpv(VecArgs p) {
         const int h = (K * pq) / E, pe = K * pq - h * E;
         float fv[K];
         chunk_floats<IO>(pf[i], fv);
+        if constexpr (KBIAS) {  // key-bias removal: encode x - o (mechanism_eval.py:113-116)
+          float o[K];
+          key_bias_offset<D, K>(p, base + vq < p.count ? base + vq : p.count - 1, K * pq, o);
+#pragma unroll
+          for (int r = 0; r < K; ++r) fv[r] = fv[r] - o[r];
+        }
 #pragma unroll
         for (int r = 0; r < K; ++r) fv[r] = __uint_as_float(__float_as_uint(fv[r]) ^ smask[r]);
 #pragma unroll
@@ -756,7 +803,7 @@ void tq_encode_lpv(VecArgs p) {
 template <int D>
 constexpr bool use_lpv_encoder() { return D >= 8 && D <= 128; }
 
-template <int D, int B, bool POLAR, int IO>
+template <int D, int B, bool POLAR, int IO, bool KBIAS>
 hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   using G = Geom<D>;
   VecArgs a = args;
@@ -764,29 +811,40 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
     if (encode) {
       constexpr int V = Lpv<D, IO>::V;
       const uint64_t need = (a.count + V - 1) / V;
-      const void* k = (const void*)&tq_encode_lpv<D, B, IO>;
+      const void* k = (const void*)&tq_encode_lpv<D, B, IO, KBIAS>;
       const uint64_t grid = persistent_grid(k, need, 64);
-      hipLaunchKernelGGL((tq_encode_lpv<D, B, IO>), dim3((uint32_t)grid), dim3(64), 0, s, a);
+      hipLaunchKernelGGL((tq_encode_lpv<D, B, IO, KBIAS>), dim3((uint32_t)grid), dim3(64), 0, s, a);
       return hipGetLastError();
     }
   }
   fill_lane_flips<D>(a.seed, a.lane_flips);
   const uint64_t need = (a.count + G::VPB - 1) / G::VPB;
   if (encode) {
-    const void* k = (const void*)&vec_encode<D, B, POLAR, IO>;
+    const void* k = (const void*)&vec_encode<D, B, POLAR, IO, KBIAS>;
     const uint64_t grid = persistent_grid(k, need);
-    hipLaunchKernelGGL((vec_encode<D, B, POLAR, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((vec_encode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else {
-    const void* k = (const void*)&vec_decode<D, B, POLAR, IO>;
+    const void* k = (const void*)&vec_decode<D, B, POLAR, IO, KBIAS>;
     const uint64_t grid = persistent_grid(k, need);
-    hipLaunchKernelGGL((vec_decode<D, B, POLAR, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((vec_decode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   }
   return hipGetLastError();
 }
 
+// Key-bias removal is compiled for float32 vectors only (the entry points that take it are float32).
+template <int D, int B, bool POLAR>
+hipError_t launch_method(bool encode, const VecArgs& a, hipStream_t s) {
+  if constexpr (PITCH_IO == 0) {
+    if (a.kb_bias) return launch_one<D, B, POLAR, PITCH_IO, true>(encode, a, s);
+  } else {
+    if (a.kb_bias) return hipErrorInvalidValue;
+  }
+  return launch_one<D, B, POLAR, PITCH_IO, false>(encode, a, s);
+}
+
 template <int D, int B>
 hipError_t launch_bits(bool encode, bool polar, const VecArgs& a, hipStream_t s) {
-  return polar ? launch_one<D, B, true, PITCH_IO>(encode, a, s) : launch_one<D, B, false, PITCH_IO>(encode, a, s);
+  return polar ? launch_method<D, B, true>(encode, a, s) : launch_method<D, B, false>(encode, a, s);
 }
 
 }  // namespace

@@ -345,3 +345,22 @@ def test_attention_validation(lib):
     small = {x: 4096 for x in ("q", "kcodes", "kscales", "vcodes", "vscales", "out", "lse")}
     assert _attn(lib, k, v, _attn_desc(T=2, ts=1 << 62, hs=1 << 62), sizes=small, ws=1 << 20) == _lib.ERR_INVALID_INPUT
     assert "overflow" in _lib.last_error()
+
+
+def test_channel_append_validation(lib):
+    cfg = _lib.PitchChannelConfigC(64, 4, 64, 0)
+    T = 150
+    inp, codes, ranges = Host(T * 256), Host(T * 32), Host(3 * 256)
+
+    def app(total, new, io=0, r=ranges, i=inp):
+        return lib.pitch_enqueue_channel_append(ctypes.byref(cfg), io, i.p, i.nbytes, 0, codes.p, codes.nbytes, 0,
+                                                r.p, r.nbytes, 0, total, new, None)
+
+    assert app(T, 0) == _lib.ERR_INVALID_INPUT
+    assert app(10, 11) == _lib.ERR_INVALID_INPUT
+    assert app(T, 5, io=3) == _lib.ERR_INVALID_INPUT
+    assert app(T + 1, 1) == _lib.ERR_INVALID_INPUT and "needs" in _lib.last_error()      # input too small
+    assert app(T, 1, r=Host(2 * 256)) == _lib.ERR_INVALID_INPUT and "ranges" in _lib.last_error()
+    assert app(T, 1, io=1, i=Host(T * 128)) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+    assert "needs" not in _lib.last_error()
+    assert app(T, 1) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
