@@ -355,6 +355,42 @@ def run_extras(torch, q, P, O, timer, gen, dev, args, x, sets) -> dict:
         del c, s_, o
     out.update(run_io16(torch, q, P, timer, gen, dev, args, x, keys4))
     out.update(run_attention(torch, q, P, O, timer, gen, dev, args))
+    out.update(run_key_bias(torch, q, P, timer, gen, dev, args))
+    return out
+
+
+def run_key_bias(torch, q, P, timer, gen, dev, args) -> dict:
+    """Config 4 (Qwen2.5-1.5B: 28 layers x 2 KV heads x 16384 tokens x d=128, TurboQuant b=4), one call per layer
+    as a model makes them, with and without the RoPE'd key-bias removal (Qwen's key projection has a bias).
+    Algorithmic bytes count the vectors, codes and scales (the bias and RoPE tables are extra reads)."""
+    out = {}
+    L, H, T, d = 28, 2, 16384, 128
+    n = H * T
+    cfg = P.QuantConfig("turboQuant", d, 4)
+    inv = 1.0 / 1e6 ** (torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)
+    ang = torch.arange(T, dtype=torch.float64, device=dev)[:, None] * inv[None, :]
+    cos = torch.cat([torch.cos(ang)] * 2, 1).float().contiguous()
+    sin = torch.cat([torch.sin(ang)] * 2, 1).float().contiguous()
+    layers = []
+    for _ in range(L):
+        x = torch.randn(n, d, generator=gen, device=dev)
+        c = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=dev)
+        s_ = torch.empty(n, device=dev)
+        kb = P.KeyBias(torch.randn(H, d, generator=gen, device=dev) * 8, cos, sin, 0, H)
+        layers.append((x, c, s_, torch.empty_like(x), kb))
+    nb = n * per_vector_bytes(d, 4)
+    steps = L * max(4, args.steps // 40)
+    for name, use in (("plain", False), ("key_bias", True)):
+        ms_e = timer.time(lambda i: q.enqueueEncode(layers[i % L][0], layers[i % L][1], layers[i % L][2], n, cfg,
+                                                    keyBias=layers[i % L][4] if use else None), steps, L)
+        ms_d = timer.time(lambda i: q.enqueueDecode(layers[i % L][1], layers[i % L][2], layers[i % L][3], n, cfg,
+                                                    keyBias=layers[i % L][4] if use else None), steps, L)
+        out[f"cfg4_qwen_layer_tq_d128_b4_{name}"] = {"vectors_per_call": n, "encode_us": round(ms_e * 1e3, 2),
+                                                     "decode_us": round(ms_d * 1e3, 2),
+                                                     "encode_gbps": round(nb / ms_e / 1e6, 1),
+                                                     "decode_gbps": round(nb / ms_d / 1e6, 1)}
+    del layers
+    torch.cuda.empty_cache()
     return out
 
 

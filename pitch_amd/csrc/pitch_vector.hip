@@ -111,17 +111,47 @@ __device__ __forceinline__ double div_sqrt_d(double y) {
 // as the reference's float32 torch expression rounds them (the library is built with -ffp-contract=off).
 template <int D, int N>
 __device__ __forceinline__ void key_bias_offset(const VecArgs& p, uint64_t v, int c, float (&o)[N]) {
-  const uint64_t tok = v / p.kb_heads;
-  const uint32_t h = (uint32_t)(v - tok * p.kb_heads);
+  uint64_t tok;
+  uint32_t h;
+  if (p.count <= 0xFFFFFFFFull) {  // 32-bit division whenever the call allows it
+    const uint32_t v32 = (uint32_t)v, t32 = v32 / p.kb_heads;
+    tok = t32;
+    h = v32 - t32 * p.kb_heads;
+  } else {
+    tok = v / p.kb_heads;
+    h = (uint32_t)(v - tok * p.kb_heads);
+  }
   const float* b = p.kb_bias + (uint64_t)h * D;
-  const uint64_t row = (p.kb_first + tok) * D;
+  const float* cs = p.kb_cos + (p.kb_first + tok) * D;
+  const float* sn = p.kb_sin + (p.kb_first + tok) * D;
+  if constexpr (N % 4 == 0 && D >= 8) {
+    // four coordinates at a time; a 4-aligned group never straddles the halves
 #pragma unroll
-  for (int r = 0; r < N; ++r) {
-    const int j = c + r;
-    const float rh = j < D / 2 ? -b[j + D / 2] : b[j - D / 2];
-    const float t1 = b[j] * p.kb_cos[row + j];
-    const float t2 = rh * p.kb_sin[row + j];
-    o[r] = t1 + t2;
+    for (int r = 0; r < N; r += 4) {
+      const int j = c + r;
+      const bool lo = j < D / 2;
+      const f32x4 bv = *(const f32x4*)(b + j);
+      const f32x4 pv = *(const f32x4*)(b + (lo ? j + D / 2 : j - D / 2));
+      const f32x4 cv = *(const f32x4*)(cs + j);
+      const f32x4 sv = *(const f32x4*)(sn + j);
+      const float bs[4] = {bv.x, bv.y, bv.z, bv.w}, ps[4] = {pv.x, pv.y, pv.z, pv.w};
+      const float cc[4] = {cv.x, cv.y, cv.z, cv.w}, ss[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float t1 = bs[k] * cc[k];
+        const float t2 = (lo ? -ps[k] : ps[k]) * ss[k];
+        o[r + k] = t1 + t2;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+      const int j = c + r;
+      const float rh = j < D / 2 ? -b[j + D / 2] : b[j - D / 2];
+      const float t1 = b[j] * cs[j];
+      const float t2 = rh * sn[j];
+      o[r] = t1 + t2;
+    }
   }
 }
 
