@@ -450,6 +450,54 @@ def run_attention(torch, q, P, O, timer, gen, dev, args) -> dict:
                       "parity_max_rel_l2_head0": rel}
         del kc, vc, ks, vs, Kd, Vd, ws
         torch.cuda.empty_cache()
+    # per-channel keys (KIVI b=4, G=64) with TurboQuant b=4 values: the reference's recommended configuration
+    kv, nq, d, T, G = 8, 4, 128, 32768, 64
+    kcfg, vcfg = P.ChannelQuantConfig(d, 4, G), P.QuantConfig("turboQuant", d, 4)
+    K = biased_keys(torch, gen, dev, kv, T, d)
+    V = torch.randn(kv * T, d, generator=gen, device=dev)
+    kc = torch.empty(kv * T * kcfg.codeStride, dtype=torch.uint8, device=dev)
+    kr = torch.empty(kv * (T // G) * 2 * d, dtype=torch.float16, device=dev)
+    vc = torch.empty(kv * T * vcfg.codeStride, dtype=torch.uint8, device=dev)
+    vs = torch.empty(kv * T, device=dev)
+    for h in range(kv):
+        q.enqueuePerChannelEncode(K[h], kc, kr, T, kcfg, codesOffset=h * T * kcfg.codeStride,
+                                  rangesOffset=h * (T // G) * kcfg.rangeStride)
+    q.enqueueEncode(V, vc, vs, kv * T, vcfg)
+    Q = torch.randn(kv, nq, d, generator=gen, device=dev)
+    o = torch.empty(kv, nq, d, device=dev)
+    ws = torch.empty(P.attention_workspace_bytes(vcfg, vcfg, T, nq, kv), dtype=torch.uint8, device=dev)
+    ms = timer.time(lambda i: q.enqueueAttentionDecode(Q, kc, kr, vc, vs, o, T, kcfg, vcfg, qPerKv=nq, kvHeads=kv,
+                                                       headStride=T, workspace=ws), steps, warm)
+    Kd = torch.empty(kv * T, d, device=dev)
+    Vd = torch.empty(kv * T, d, device=dev)
+
+    def decode_then_attend_kivi(i):
+        for h in range(kv):
+            q.enqueuePerChannelDecode(kc, kr, Kd, T, kcfg, codesOffset=h * T * kcfg.codeStride,
+                                      rangesOffset=h * (T // G) * kcfg.rangeStride, outputOffset=h * T * d * 4)
+        q.enqueueDecode(vc, vs, Vd, kv * T, vcfg)
+        S = torch.bmm(Q, Kd.view(kv, T, d).transpose(1, 2).contiguous()) / math.sqrt(d)
+        return torch.bmm(torch.softmax(S, -1), Vd.view(kv, T, d))
+
+    ms_b = timer.time(decode_then_attend_kivi, max(5, steps // 4), 2)
+    torch.cuda.synchronize()
+    ck = O.unpack_codes(kc[:T * kcfg.codeStride].cpu().numpy().tobytes(), T, d, 4)
+    rk = kr[:(T // G) * 2 * d].cpu().numpy().reshape(T // G, 2, d)
+    cv = O.unpack_codes(vc[:T * vcfg.codeStride].cpu().numpy().tobytes(), T, d, 4)
+    ro, _ = O.attention_decode_channel_keys(Q[0].cpu().numpy().astype(np.float64), ck, rk, 4, G, cv,
+                                            vs[:T].cpu().numpy(), "turboQuant", 4, 1 / math.sqrt(d))
+    got = o[0].cpu().numpy().astype(np.float64)
+    rel = float(max(np.linalg.norm(got[i] - ro[i]) / np.linalg.norm(ro[i]) for i in range(nq)))
+    if rel > 1e-5:
+        raise SystemExit(f"attention parity failed for per-channel keys: rel L2 {rel}")
+    nb = kv * T * (kcfg.codeStride + vcfg.codeStride + 4) + kv * (T // G) * 4 * d
+    out["cfg5_llama3_8b_layer_attention_kivi_keys_T32768"] = {
+        "kv_heads": kv, "q_per_kv": nq, "dim": d, "tokens": T, "key_group": G, "ms": round(ms, 5),
+        "cache_tokens_per_s": round(kv * T / ms * 1e3, 1), "codes_gbps": round(nb / ms / 1e6, 1),
+        "decode_then_attend_ms": round(ms_b, 4), "speedup_vs_decode_then_attend": round(ms_b / ms, 2),
+        "parity_max_rel_l2_head0": rel}
+    del K, V, kc, kr, vc, vs, Kd, Vd, ws
+    torch.cuda.empty_cache()
     return out
 
 

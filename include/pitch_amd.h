@@ -233,6 +233,26 @@ int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch
                                    uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes,
                                    uint64_t lse_offset, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* pitch_enqueue_attention_decode with per-channel (KIVI) keys and per-vector values: the configuration the
+ * reference recommends for models whose key projection has a bias (README.md:30) and evaluates as
+ * "kivi_K{b}_turboV{b}" (reference/attention_extra.py:57-59). Keys decode as f32(c) * step + lo per group and
+ * channel (reference/pitch_reference.py:165-174). The key cache is head-major, as per-head
+ * pitch_enqueue_channel_encode calls write it: codes of (head h, token t) at row h * head_stride + t, fp16 ranges
+ * of (h, group g) at group h * head_stride / group_size + g; desc->token_stride must be 1 and, with more than one
+ * KV head, head_stride a multiple of the group size holding the tokens (one head: head_stride is ignored). The
+ * values use the same rows. The group size must be a multiple of 64. */
+int pitch_attention_channel_keys_workspace_size(const pitch_channel_config_t* key_config,
+                                                const pitch_config_t* value_config, const pitch_attention_desc_t* desc,
+                                                uint64_t* bytes);
+int pitch_enqueue_attention_decode_channel_keys(
+    const pitch_channel_config_t* key_config, const pitch_config_t* value_config, const pitch_attention_desc_t* desc,
+    const void* q, uint64_t q_bytes, uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,
+    uint64_t key_codes_offset, const void* key_ranges, uint64_t key_ranges_bytes, uint64_t key_ranges_offset,
+    const void* value_codes, uint64_t value_codes_bytes, uint64_t value_codes_offset, const void* value_scales,
+    uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output, uint64_t output_bytes,
+    uint64_t output_offset, void* lse, uint64_t lse_bytes, uint64_t lse_offset, void* workspace,
+    uint64_t workspace_bytes, void* stream);
+
 /* Packs count rows of dim unpacked codes (one uint8 per code, each < 2^bits) into count * code_stride
  * bytes, code i at bits [i * bits, i * bits + bits) of the row's little-endian 32-bit words.
  * Replaces pack_codes (reference/pitch_reference.py:68-78). */

@@ -360,6 +360,16 @@ def attention_decode(Q, k_codes, k_scales, v_codes, v_scales, k_method: str, k_b
     return attend(Q, K, V, scale)
 
 
+def attention_decode_channel_keys(Q, k_codes, k_ranges, k_bits: int, G: int, v_codes, v_scales, v_method: str,
+                                  v_bits: int, scale: float, v_seed: int = DEFAULT_SEED):
+    """Attention with per-channel keys and per-vector values ("kivi_K{b}_turboV{b}",
+    reference/attention_extra.py:57-59): K = channel_decode(k_codes, k_ranges) in float32
+    (pitch_reference.py:165-174), V = decode(v_codes, v_scales), then attend."""
+    K = channel_decode(k_codes, k_ranges, k_bits, G)
+    V = DECODERS[v_method](v_codes, np.asarray(v_scales, np.float32).astype(np.float64), v_bits, v_seed)
+    return attend(Q, K, V, scale)
+
+
 # ----------------------------------------------------------------------------- boundary classification
 # The parity bar for per-vector codes: a code may differ from the oracle's only at a coordinate whose
 # rotated value lies within REL_BAND of a decision boundary, relative to max(|boundary|, floor). The floor

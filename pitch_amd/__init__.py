@@ -11,7 +11,7 @@ from .api import (  # noqa: F401
     CHANNEL_DEFAULT_GROUP, DECODERS, DEFAULT_SEED, ENCODERS, FP16_MAX, PITCH, SUPPORTED_BITS, SUPPORTED_DIMS,
     ChannelCompressedBlock, ChannelQuantConfig, CompressedBatch, ConfigurationMismatch, DecodingFailed,
     DeviceUnavailable, EncodingFailed, InvalidBitWidth, InvalidDimension, InvalidInput, KeyBias, PITCHError,
-    QuantConfig, QuantMethod, attention_decode, attention_workspace_bytes, bits_per_coordinate, channel_bits_per_coordinate, channel_decode, channel_encode,
+    QuantConfig, QuantMethod, attention_decode, attention_decode_channel_keys, attention_workspace_bytes, bits_per_coordinate, channel_bits_per_coordinate, channel_decode, channel_encode,
     channel_group_count, code_stride_bytes, half_to_float, pack_codes, polar_decode, polar_encode, rand_signs,
     turbo_decode, turbo_encode, unpack_codes,
 )

@@ -83,6 +83,13 @@ SIGNATURES = {
     "pitch_enqueue_attention_decode": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
                                               ctypes.POINTER(PitchAttentionDescC)] + [_vp, _u64, _u64] * 7
                                        + [_vp, _u64, _vp]),
+    "pitch_attention_channel_keys_workspace_size": (_int, [ctypes.POINTER(PitchChannelConfigC),
+                                                           ctypes.POINTER(PitchConfigC),
+                                                           ctypes.POINTER(PitchAttentionDescC), ctypes.POINTER(_u64)]),
+    "pitch_enqueue_attention_decode_channel_keys": (_int, [ctypes.POINTER(PitchChannelConfigC),
+                                                           ctypes.POINTER(PitchConfigC),
+                                                           ctypes.POINTER(PitchAttentionDescC)] + [_vp, _u64, _u64] * 7
+                                                    + [_vp, _u64, _vp]),
     "pitch_enqueue_pack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_unpack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
 }

@@ -682,14 +682,22 @@ class PITCH:
         """out = softmax(scale * q K^T) V over caches held as codes: q and output are fp32
         [kvHeads][qPerKv][dim]; the vector of (head h, token t) is t * tokenStride + h * headStride (default
         headStride = tokens, a head-major cache). scale defaults to 1 / sqrt(dim). lse, when given, receives the
-        natural-log sum of exp of the scaled scores per query. Without a workspace one is allocated."""
+        natural-log sum of exp of the scaled scores per query. Without a workspace one is allocated.
+        With a ChannelQuantConfig as keyConfig the keys are per-channel: keyScales is their fp16 ranges tensor, the
+        caches are head-major (tokenStride 1) and headStride, in tokens, a multiple of the group size (default:
+        tokens rounded up to it)."""
         torch = _torch()
+        channel_keys = isinstance(keyConfig, ChannelQuantConfig)
+        if channel_keys and valueConfig is None:
+            raise InvalidInput("per-channel keys need a per-vector valueConfig")
         valueConfig = valueConfig or keyConfig
         scale = 1.0 / math.sqrt(keyConfig.dim) if scale is None else scale
-        headStride = int(tokens) if headStride is None else headStride
+        if headStride is None:
+            headStride = int(tokens) if not channel_keys else -(-int(tokens) // keyConfig.groupSize) * keyConfig.groupSize
         desc = _attention_desc(qPerKv, kvHeads, tokens, tokenStride, headStride, scale)
         if workspace is None:
-            nbytes = attention_workspace_bytes(keyConfig, valueConfig, tokens, qPerKv, kvHeads)
+            nbytes = attention_workspace_bytes(valueConfig if channel_keys else keyConfig, valueConfig, tokens,
+                                               qPerKv, kvHeads)
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         args = []
         for t, name in ((q, "query"), (keyCodes, "key codes"), (keyScales, "key scales"), (valueCodes, "value codes"),
@@ -702,9 +710,10 @@ class PITCH:
         else:
             args += [None, 0, 0]
         wp, wb = _buf(workspace, "workspace")
-        rc = self._lib.pitch_enqueue_attention_decode(ctypes.byref(keyConfig._c()), ctypes.byref(valueConfig._c()),
-                                                      ctypes.byref(desc), *args, wp, wb,
-                                                      _stream_handle(stream, self.device))
+        fn = (self._lib.pitch_enqueue_attention_decode_channel_keys if channel_keys
+              else self._lib.pitch_enqueue_attention_decode)
+        rc = fn(ctypes.byref(keyConfig._c()), ctypes.byref(valueConfig._c()), ctypes.byref(desc), *args, wp, wb,
+                _stream_handle(stream, self.device))
         _raise_for(rc)
 
     # ---- per-channel (PerChannel.swift:182-290)
@@ -971,6 +980,29 @@ def attention_decode(q, k_codes, k_scales, v_codes, v_scales, b: int, method: st
     with torch.cuda.device(q.device):
         _pitch_for(q).enqueueAttentionDecode(q.to(torch.float32).contiguous(), k_codes.contiguous(),
                                              k_scales.to(torch.float32).contiguous(), v_codes.contiguous(),
+                                             v_scales.to(torch.float32).contiguous(), out, T, kc, vc, qPerKv=nq,
+                                             kvHeads=H, tokenStride=1, headStride=T, scale=scale, lse=lse)
+    return out, lse
+
+
+def attention_decode_channel_keys(q, k_codes, k_ranges, v_codes, v_scales, k_bits: int, v_bits: int,
+                                  group: int = CHANNEL_DEFAULT_GROUP, v_method: str = "turboQuant",
+                                  v_seed: int = DEFAULT_SEED, scale: float | None = None):
+    """attention_decode with per-channel keys: k_codes (kv_heads, T_pad, codeStride) uint8 and k_ranges
+    (kv_heads, T_pad / group, 2, d) fp16 as per-head channel_encode calls write them, with T_pad the tokens
+    rounded up to the group size; v_codes / v_scales per-vector over the same rows."""
+    torch = _torch()
+    if q.dim() == 2:
+        q = q.unsqueeze(0)
+    H, nq, d = q.shape
+    T = k_codes.shape[1]
+    kc = ChannelQuantConfig(d, k_bits, group)
+    vc = QuantConfig(v_method, d, v_bits, v_seed)
+    out = torch.empty((H, nq, d), dtype=torch.float32, device=q.device)
+    lse = torch.empty((H, nq), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _pitch_for(q).enqueueAttentionDecode(q.to(torch.float32).contiguous(), k_codes.contiguous(),
+                                             k_ranges.contiguous(), v_codes.contiguous(),
                                              v_scales.to(torch.float32).contiguous(), out, T, kc, vc, qPerKv=nq,
                                              kvHeads=H, tokenStride=1, headStride=T, scale=scale, lse=lse)
     return out, lse

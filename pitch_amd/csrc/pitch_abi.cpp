@@ -610,6 +610,92 @@ int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch
   return ok();
 }
 
+int pitch_attention_channel_keys_workspace_size(const pitch_channel_config_t* key_config,
+                                                const pitch_config_t* value_config, const pitch_attention_desc_t* desc,
+                                                uint64_t* bytes) {
+  PITCH_TRY(validate_channel_config(key_config));
+  if (!value_config) return fail(PITCH_ERR_INVALID_INPUT, "value config is null");
+  const pitch_config_t k{PITCH_METHOD_TURBO, key_config->dim, key_config->bits, 0u};
+  return pitch_attention_workspace_size(&k, value_config, desc, bytes);
+}
+
+int pitch_enqueue_attention_decode_channel_keys(
+    const pitch_channel_config_t* key_config, const pitch_config_t* value_config, const pitch_attention_desc_t* desc,
+    const void* q, uint64_t q_bytes, uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,
+    uint64_t key_codes_offset, const void* key_ranges, uint64_t key_ranges_bytes, uint64_t key_ranges_offset,
+    const void* value_codes, uint64_t value_codes_bytes, uint64_t value_codes_offset, const void* value_scales,
+    uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output, uint64_t output_bytes,
+    uint64_t output_offset, void* lse, uint64_t lse_bytes, uint64_t lse_offset, void* workspace,
+    uint64_t workspace_bytes, void* stream) {
+  PITCH_TRY(validate_channel_config(key_config));
+  const pitch_config_t kvec{PITCH_METHOD_TURBO, key_config->dim, key_config->bits, 0u};
+  PITCH_TRY(validate_attention(&kvec, value_config, desc));
+  const uint32_t dim = key_config->dim, G = key_config->group_size, nq = desc->q_per_kv, nqp = padded_queries(nq);
+  if (G % 64 != 0)
+    return fail(PITCH_ERR_INVALID_INPUT, "attention over per-channel keys needs a group size that is a multiple of 64, "
+                "got %u", G);
+  if (desc->token_stride != 1)
+    return fail(PITCH_ERR_INVALID_INPUT, "per-channel key caches are head-major: token_stride must be 1");
+  if (desc->kv_heads > 1 && (desc->head_stride < desc->tokens || desc->head_stride % G != 0))
+    return fail(PITCH_ERR_INVALID_INPUT, "head_stride %llu must hold the tokens and be a multiple of the group size %u",
+                (unsigned long long)desc->head_stride, G);
+  const uint64_t head_stride = desc->kv_heads > 1 ? desc->head_stride : (desc->tokens + G - 1) / G * G;
+  const uint32_t kcs = code_stride_of(dim, key_config->bits), vcs = code_stride_of(dim, value_config->bits);
+  uint64_t vectors = 0;
+  PITCH_TRY(attention_extent(desc, &vectors));
+  const uint64_t queries = (uint64_t)desc->kv_heads * nq;
+  const uint64_t kgroups = ((uint64_t)(desc->kv_heads - 1) * head_stride + desc->tokens + G - 1) / G;
+  PITCH_TRY(check_buffer(q, q_bytes, q_offset, queries * dim * 4u, "query"));
+  PITCH_TRY(check_buffer(key_codes, key_codes_bytes, key_codes_offset, vectors * kcs, "key codes"));
+  PITCH_TRY(check_buffer(key_ranges, key_ranges_bytes, key_ranges_offset, kgroups * 4u * dim, "key ranges"));
+  PITCH_TRY(check_buffer(value_codes, value_codes_bytes, value_codes_offset, vectors * vcs, "value codes"));
+  PITCH_TRY(check_buffer(value_scales, value_scales_bytes, value_scales_offset, vectors * 4u, "value scales"));
+  PITCH_TRY(check_buffer(output, output_bytes, output_offset, queries * dim * 4u, "output"));
+  if (lse) PITCH_TRY(check_buffer(lse, lse_bytes, lse_offset, queries * 4u, "lse"));
+  const uint32_t chunk = pitch::attention_chunk_tokens(desc->tokens, desc->kv_heads);
+  const uint64_t ws_need = 4u * pitch::attention_workspace_floats(dim, nqp, desc->kv_heads, desc->tokens, chunk);
+  PITCH_TRY(check_buffer(workspace, workspace_bytes, 0, ws_need, "workspace"));
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  PITCH_TRY(check_device(q, dev, "query"));
+  PITCH_TRY(check_device(key_codes, dev, "key codes"));
+  PITCH_TRY(check_device(key_ranges, dev, "key ranges"));
+  PITCH_TRY(check_device(value_codes, dev, "value codes"));
+  PITCH_TRY(check_device(value_scales, dev, "value scales"));
+  PITCH_TRY(check_device(output, dev, "output"));
+  if (lse) PITCH_TRY(check_device(lse, dev, "lse"));
+  PITCH_TRY(check_device(workspace, dev, "workspace"));
+  pitch::AttnArgs a{};
+  a.q = at<const float>(q, q_offset);
+  a.k_codes = at<const uint32_t>(key_codes, key_codes_offset);
+  a.k_ranges = at<const uint16_t>(key_ranges, key_ranges_offset);
+  a.k_group = G;
+  a.v_codes = at<const uint32_t>(value_codes, value_codes_offset);
+  a.v_scales = at<const float>(value_scales, value_scales_offset);
+  a.out = at<float>(output, output_offset);
+  a.lse = lse ? at<float>(lse, lse_offset) : nullptr;
+  a.ws = (float*)workspace;
+  a.tokens = desc->tokens;
+  a.token_stride = 1;
+  a.head_stride = head_stride;
+  a.dim = dim;
+  a.nq = nq;
+  a.nqp = nqp;
+  a.kv_heads = desc->kv_heads;
+  a.kbits = key_config->bits;
+  a.vbits = value_config->bits;
+  a.vpolar = value_config->method == PITCH_METHOD_POLAR;
+  a.vseed = value_config->seed;
+  a.chunk = chunk;
+  a.chunks = (uint32_t)((desc->tokens + chunk - 1) / chunk);
+  a.kscale = (float)((double)desc->scale * 1.4426950408889634);
+  a.oscale = (float)(1.0 / __builtin_sqrt((double)dim));
+  const hipError_t e = dim == 64 ? pitch::launch_attention_d64(a, (hipStream_t)stream)
+                                 : pitch::launch_attention_d128(a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Attention failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 static int pack_common(bool pack, uint32_t dim, uint32_t bits, const void* src, uint64_t src_bytes,
                        uint64_t src_off, void* dst, uint64_t dst_bytes, uint64_t dst_off, uint64_t count,
                        void* stream) {

@@ -251,6 +251,136 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
   }
 }
 
+// ---------------------------------------------------------------------------------------------- scores, KIVI keys
+// Per-channel keys decode as k_j = f32(c_j) * step_j + lo_j per group (reference/pitch_reference.py:165-174), so
+// q . k_t = sum_j (q_j step_j) c_tj + sum_j q_j lo_j. Workgroup (chunk, KV head); thread = token; a wave's 64
+// tokens lie in one group (the group size is a multiple of 64), so the wave builds that group's query products
+// qs_j = q_j * step_j (times scale * log2 e) in its LDS slice and the per-query constant q . lo, then each lane
+// reads its token's codes and sums qs_j * c_j with broadcast LDS reads. Chunk max, weights and sums as attn_scores.
+template <int D, int B, int NQ>
+__global__ __launch_bounds__(kBlock) void attn_scores_chan(AttnArgs a) {
+  constexpr int NW = D * B / 32;
+  constexpr int E = D / 64;                 // coordinates per lane when the wave builds the query products
+  constexpr uint32_t kMask = (1u << B) - 1u;
+  const float levels = (float)((1 << B) - 1);
+  __shared__ float s_s[kMaxChunk * NQ];
+  __shared__ float s_red[4 * NQ];
+  __shared__ __attribute__((aligned(16))) float s_qs[4][D * NQ];   // per wave: [coordinate][query]
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const uint32_t kv = blockIdx.y, c = blockIdx.x;
+  const uint64_t t0 = (uint64_t)c * a.chunk;
+  const uint32_t n = (uint32_t)min((uint64_t)a.chunk, a.tokens - t0);
+  const uint64_t groups_per_head = a.head_stride / a.k_group;
+  // this lane's query coordinates j = E * lane + e, scaled by scale * log2(e)
+  float qv[NQ][E];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h)
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      qv[h][e] = h < (int)a.nq ? a.q[((uint64_t)kv * a.nq + h) * D + E * lane + e] * a.kscale : 0.f;
+  float* qs = s_qs[wid];
+  uint64_t cur_group = ~0ull;
+  float beta[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) beta[h] = 0.f;
+
+  for (uint32_t i0 = 0; i0 < n; i0 += kBlock) {
+    const uint32_t wfirst = i0 + 64u * wid;   // this wave's first token in the chunk
+    if (wfirst < n) {                          // uniform per wave
+      const uint64_t g = (t0 + wfirst) / a.k_group;
+      if (g != cur_group) {
+        cur_group = g;
+        const uint16_t* rg = a.k_ranges + ((uint64_t)kv * groups_per_head + g) * 2u * D;
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) beta[h] = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int j = E * lane + e;
+          const float lo = widen1<1>(rg[j]), hi = widen1<1>(rg[D + j]);
+          float step = (hi - lo) / levels;
+          step = step == 0.f ? 1.f : step;
+#pragma unroll
+          for (int h = 0; h < NQ; ++h) {
+            qs[j * NQ + h] = qv[h][e] * step;
+            beta[h] = __builtin_fmaf(qv[h][e], lo, beta[h]);
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < NQ; ++h)
+#pragma unroll
+          for (int off = 1; off < 64; off <<= 1) beta[h] += __shfl_xor(beta[h], off);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      const uint32_t i = wfirst + lane;
+      const bool valid = i < n;
+      const uint64_t row = (uint64_t)kv * a.head_stride + t0 + (valid ? i : wfirst);
+      uint32_t w[NW];
+      load_row<NW>(a.k_codes + row * NW, w);
+      float acc[NQ];
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) acc[h] = beta[h];
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        const int pos = B * j, wi = pos >> 5, sh = pos & 31;
+        const uint32_t bits = (sh + B <= 32) ? (w[wi] >> sh) : __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh);
+        const float cf = (float)(bits & kMask);
+        float qj[NQ];
+        if constexpr (NQ % 4 == 0) {
+#pragma unroll
+          for (int h = 0; h < NQ; h += 4) {
+            const float4 v4 = *(const float4*)(qs + j * NQ + h);
+            qj[h] = v4.x; qj[h + 1] = v4.y; qj[h + 2] = v4.z; qj[h + 3] = v4.w;
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < NQ; ++h) qj[h] = qs[j * NQ + h];
+        }
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) acc[h] = __builtin_fmaf(qj[h], cf, acc[h]);
+      }
+      if (valid) {
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) s_s[i * NQ + h] = acc[h];
+      }
+    }
+  }
+  __syncthreads();
+
+  float m[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) m[h] = -__builtin_inff();
+  for (uint32_t i = tid; i < n; i += kBlock) {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) m[h] = fmaxf(m[h], s_s[i * NQ + h]);
+  }
+  block_reduce<NQ, true>(m, s_red);
+  const WsLayout L(a);
+  float* pw = a.ws + L.p + ((uint64_t)kv * a.tokens + t0) * NQ;
+  float l[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) l[h] = 0.f;
+  for (uint32_t i = tid; i < n; i += kBlock) {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const float e = exp2f(s_s[i * NQ + h] - m[h]);
+      l[h] += e;
+      pw[(uint64_t)i * NQ + h] = e;
+    }
+  }
+  block_reduce<NQ, false>(l, s_red);
+  if (tid == 0) {
+    float* ml = a.ws + L.ml;
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const uint64_t k = (((uint64_t)kv * NQ + h) * a.chunks + c) * 2;
+      ml[k] = m[h];
+      ml[k + 1] = l[h];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------- values
 // Workgroup (chunk, KV head). Per block of 256 tokens, each thread stages one token's code row and weights
 // p * n in LDS; then lane (r, g) of wave w takes token 16 * step + 4 * w + r and the g-th 16th of its code pairs,
@@ -437,12 +567,23 @@ hipError_t launch_nq(const AttnArgs& a, hipStream_t s) {
   constexpr int D = PITCH_DIM;
   const dim3 grid(a.chunks, a.kv_heads);
   const float* qp = a.ws;
-  switch (a.kbits) {
+  if (a.k_ranges) {
+    switch (a.kbits) {
+#define PITCH_SCORES_CHAN(B) \
+  case B: hipLaunchKernelGGL((attn_scores_chan<D, B, NQ>), grid, dim3(kBlock), 0, s, a); break;
+      PITCH_SCORES_CHAN(2) PITCH_SCORES_CHAN(3) PITCH_SCORES_CHAN(4) PITCH_SCORES_CHAN(5) PITCH_SCORES_CHAN(6)
+      PITCH_SCORES_CHAN(7) PITCH_SCORES_CHAN(8)
+#undef PITCH_SCORES_CHAN
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (a.kbits) {
 #define PITCH_SCORES(B) \
   case B: hipLaunchKernelGGL((attn_scores<D, B, NQ>), grid, dim3(kBlock), 0, s, a, qp); break;
-    PITCH_SCORES(2) PITCH_SCORES(3) PITCH_SCORES(4) PITCH_SCORES(5) PITCH_SCORES(6) PITCH_SCORES(7) PITCH_SCORES(8)
+      PITCH_SCORES(2) PITCH_SCORES(3) PITCH_SCORES(4) PITCH_SCORES(5) PITCH_SCORES(6) PITCH_SCORES(7) PITCH_SCORES(8)
 #undef PITCH_SCORES
-    default: return hipErrorInvalidValue;
+      default: return hipErrorInvalidValue;
+    }
   }
   switch (a.vbits) {
 #define PITCH_VALUES(B) \
@@ -463,7 +604,9 @@ hipError_t PITCH_CAT(launch_attention_d, PITCH_DIM)(const AttnArgs& a, hipStream
   constexpr int D = PITCH_DIM;
   static_assert(D == 64 || D == 128, "attention dimensions");
   if (a.dim != (uint32_t)D || a.chunk < 64 || a.chunk > (uint32_t)kMaxChunk || a.chunks == 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
+  if (a.k_ranges && (a.k_group == 0 || a.k_group % 64 != 0 || a.head_stride % a.k_group != 0 || a.token_stride != 1))
+    return hipErrorInvalidValue;
+  if (!a.k_ranges) hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
   hipError_t e;
   switch (a.nqp) {
     case 1: e = launch_nq<1>(a, s); break;

@@ -73,6 +73,11 @@ struct AttnArgs {
   uint32_t chunk, chunks;    // tokens per workgroup and chunks per KV head
   float qscale;              // softmax scale * log2(e) / sqrt(dim), folded into the rotated queries
   float oscale;              // 1 / sqrt(dim) of the value decode
+  // Per-channel (KIVI) keys instead of per-vector ones (k_ranges non-null): codes [h][token] at
+  // (t + h * head_stride) rows, fp16 ranges [h][group][2][dim] with head_stride / k_group groups per head.
+  const uint16_t* k_ranges;
+  uint32_t k_group;          // tokens per key group (a multiple of 64)
+  float kscale;              // softmax scale * log2(e), folded into the per-group query products
 };
 
 // Chunk length (tokens per workgroup) the attention kernels use for a call, and the workspace it needs.

@@ -364,3 +364,33 @@ def test_channel_append_validation(lib):
     assert app(T, 1, io=1, i=Host(T * 128)) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
     assert "needs" not in _lib.last_error()
     assert app(T, 1) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+
+
+def test_attention_channel_keys_validation(lib):
+    kc = _lib.PitchChannelConfigC(64, 4, 64, 0)
+    vc = _lib.PitchConfigC(0, 64, 4, 0)
+    desc = _lib.PitchAttentionDescC(2, 2, 100, 1, 128, 0.125, 0)
+    n = ctypes.c_uint64(0)
+    assert lib.pitch_attention_channel_keys_workspace_size(ctypes.byref(kc), ctypes.byref(vc), ctypes.byref(desc),
+                                                           ctypes.byref(n)) == 0 and n.value > 0
+    vecs = 128 + 100
+    sizes = dict(q=2 * 2 * 64 * 4, kcodes=vecs * 32, kranges=4 * 256, vcodes=vecs * 32, vscales=vecs * 4,
+                 out=2 * 2 * 64 * 4, lse=2 * 2 * 4)
+
+    def call(kcfg=kc, d=desc, **over):
+        sz = dict(sizes, **over)
+        b = {k: Host(v) for k, v in sz.items()}
+        w = Host(n.value)
+        args = []
+        for k in ("q", "kcodes", "kranges", "vcodes", "vscales", "out", "lse"):
+            args += [b[k].p, b[k].nbytes, 0]
+        return lib.pitch_enqueue_attention_decode_channel_keys(ctypes.byref(kcfg), ctypes.byref(vc), ctypes.byref(d),
+                                                               *args, w.p, w.nbytes, None)
+
+    assert call() in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE) and "needs" not in _lib.last_error()
+    assert call(kcfg=_lib.PitchChannelConfigC(64, 4, 32, 0)) == _lib.ERR_INVALID_INPUT     # G not a multiple of 64
+    assert "multiple of 64" in _lib.last_error()
+    assert call(d=_lib.PitchAttentionDescC(2, 2, 100, 2, 128, 0.125, 0)) == _lib.ERR_INVALID_INPUT  # token stride
+    assert call(d=_lib.PitchAttentionDescC(2, 2, 100, 1, 96, 0.125, 0)) == _lib.ERR_INVALID_INPUT   # head stride
+    assert call(kranges=4 * 256 - 4) == _lib.ERR_INVALID_INPUT and "key ranges" in _lib.last_error()
+    assert call(kcfg=_lib.PitchChannelConfigC(128, 4, 64, 0)) == _lib.ERR_CONFIGURATION_MISMATCH

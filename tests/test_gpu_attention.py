@@ -180,3 +180,61 @@ def test_attention_function_mirror(q):
         ro, rl = O.attention_decode(Q[h].astype(np.float64), kc[h], ks[h], vc[h], vs[h], "turboQuant", b,
                                     "turboQuant", b, 1 / math.sqrt(d))
         _check(out[h], lse[h], ro, rl, OUT_REL_L2, LSE_TOL, f"mirror head {h}")
+
+
+CHANNEL_CASES = [
+    # (kb, vb, d, G, nq, kv, T)
+    (4, 4, 128, 64, 4, 2, 1000),
+    (2, 2, 64, 64, 1, 3, 777),
+    (3, 4, 128, 128, 6, 1, 5000),
+    (8, 2, 64, 64, 4, 2, 300),
+    (4, 3, 128, 64, 8, 1, 65),
+    (5, 4, 64, 128, 2, 2, 1),
+    (4, 4, 128, 64, 4, 1, 70000),
+]
+
+
+@pytest.mark.parametrize("kb,vb,d,G,nq,kv,T", CHANNEL_CASES)
+def test_attention_channel_keys(q, kb, vb, d, G, nq, kv, T):
+    """Per-channel (KIVI) keys with TurboQuant values: the reference's recommended configuration for biased key
+    projections (README.md:30; "kivi_K{b}_turboV{b}", attention_extra.py:57-59). Caches are built by the
+    library's own per-head encoders into head-major buffers with the head stride rounded up to the group."""
+    import torch
+    import pitch_amd as P
+    dev = q.device
+    label = f"KIVI K b{kb} G{G} / TQ V b{vb} d={d} nq={nq} kv={kv} T={T}"
+    print(label, flush=True)
+    Tp = -(-T // G) * G
+    g = torch.Generator(device=dev).manual_seed(kb * 100 + vb * 10 + d + T)
+    K = (torch.randn(kv, Tp, d, generator=g, device=dev) * torch.exp(torch.randn(kv, 1, d, generator=g, device=dev))
+         + 3 * torch.randn(kv, 1, d, generator=g, device=dev))
+    V = torch.randn(kv, Tp, d, generator=g, device=dev)
+    kc_cfg = P.ChannelQuantConfig(d, kb, G)
+    vc_cfg = P.QuantConfig("turboQuant", d, vb, 77)
+    kcodes = torch.zeros(kv * Tp * kc_cfg.codeStride, dtype=torch.uint8, device=dev)
+    kranges = torch.zeros(kv * (Tp // G) * 2 * d, dtype=torch.float16, device=dev)
+    vcodes = torch.zeros(kv * Tp * vc_cfg.codeStride, dtype=torch.uint8, device=dev)
+    vscales = torch.zeros(kv * Tp, device=dev)
+    for h in range(kv):
+        q.enqueuePerChannelEncode(K[h].contiguous(), kcodes, kranges, T, kc_cfg, codesOffset=h * Tp * kc_cfg.codeStride,
+                                  rangesOffset=h * (Tp // G) * kc_cfg.rangeStride)
+    q.enqueueEncode(V.reshape(-1, d).contiguous(), vcodes, vscales, kv * Tp, vc_cfg)
+    Q = torch.randn(kv, nq, d, generator=g, device=dev)
+    out = torch.empty(kv, nq, d, device=dev)
+    lse = torch.empty(kv, nq, device=dev)
+    q.enqueueAttentionDecode(Q, kcodes, kranges, vcodes, vscales, out, T, kc_cfg, vc_cfg, qPerKv=nq, kvHeads=kv,
+                             headStride=Tp, lse=lse)
+    torch.cuda.synchronize()
+    out, lse = out.cpu().numpy(), lse.cpu().numpy()
+    kcn = kcodes.cpu().numpy().tobytes()
+    krn = kranges.cpu().numpy().view(np.uint16).reshape(kv, Tp // G, 2, d)
+    vcn = vcodes.cpu().numpy().tobytes()
+    vsn = vscales.cpu().numpy().reshape(kv, Tp)
+    Qn = Q.cpu().numpy().astype(np.float64)
+    for h in range(kv):
+        ck = O.unpack_codes(kcn[h * Tp * kc_cfg.codeStride:(h * Tp + T) * kc_cfg.codeStride], T, d, kb)
+        rk = krn[h, :-(-T // G)].view(np.float16)
+        cv = O.unpack_codes(vcn[h * Tp * vc_cfg.codeStride:(h * Tp + T) * vc_cfg.codeStride], T, d, vb)
+        ro, rl = O.attention_decode_channel_keys(Qn[h], ck, rk, kb, G, cv, vsn[h, :T], "turboQuant", vb,
+                                                 1 / math.sqrt(d), 77)
+        _check(out[h], lse[h], ro, rl, OUT_REL_L2, LSE_TOL, f"{label} head {h}")
