@@ -192,19 +192,26 @@ constexpr float kKiviGuard = 1e-4f;
 #ifndef PITCH_KIVI_WAVES
 #define PITCH_KIVI_WAVES 3  // waves per SIMD the per-channel encoder's register budget allows
 #endif
-constexpr int kSlab = 64;        // channels per wave
-constexpr int kGroupMaxW = 64;   // largest group this kernel takes (16 tokens per lane)
+constexpr int kSlab = 64;        // channels per wave of the decoder
+constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
+#ifndef PITCH_KIVI_SLAB
+#define PITCH_KIVI_SLAB 0        // encoder slab width: 0 = chosen per call, else 32 or 64 channels
+#endif
 
-template <int B, int IO>
+// SW = 64: lane (r, c) = (lane / 16, lane % 16), tokens r, r + 4, ... (16 per lane); SW = 32: lane
+// (lane / 8, lane % 8), tokens r, r + 8, ... (8 per lane), twice the work items and half the registers.
+template <int B, int IO, int SW>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KIVI_WAVES))) void chan_encode_w(ChanArgs p) {
-  constexpr int TPL = kGroupMaxW / 4;  // tokens per lane
+  constexpr int QW = SW / 4;           // lanes per token row
+  constexpr int RPI = 64 / QW;         // token rows per load instruction
+  constexpr int TPL = kGroupMaxW / RPI;  // tokens per lane
   const float levels = (float)((1 << B) - 1);
-  __shared__ __attribute__((aligned(16))) uint8_t s_stage_all[kBlock / 64][kGroupMaxW * kSlab];
+  __shared__ __attribute__((aligned(16))) uint8_t s_stage_all[kBlock / 64][kGroupMaxW * SW];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   uint8_t* s_stage = s_stage_all[wid];
-  const int r = lane >> 4, c = lane & 15;
+  const int r = lane / QW, c = lane % QW;
   const uint32_t dim = p.dim, G = p.group;
-  const uint32_t slabs = (dim + kSlab - 1) / kSlab;
+  const uint32_t slabs = (dim + SW - 1) / SW;
   const uint32_t groups = (p.count + G - 1) / G;
   const uint64_t items = (uint64_t)groups * slabs;
   const uint64_t waves = (uint64_t)gridDim.x * (kBlock / 64);
@@ -212,7 +219,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
   for (uint64_t it = (uint64_t)blockIdx.x * (kBlock / 64) + wid; it < items; it += waves) {
     const uint32_t g = (uint32_t)(it / slabs), sl = (uint32_t)(it - (uint64_t)g * slabs);
     const uint32_t first = g * G, n = min(G, p.count - first);
-    const uint32_t ch0 = sl * kSlab, cw = min((uint32_t)kSlab, dim - ch0);  // cw is a multiple of 4
+    const uint32_t ch0 = sl * SW, cw = min((uint32_t)SW, dim - ch0);  // cw is a multiple of 4
     const bool cact = 4u * c < cw;
     const uint64_t src = (uint64_t)first * dim + ch0 + (cact ? 4u * c : 0u);  // element index
 
@@ -220,7 +227,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
     float4 x[TPL];
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
-      const uint32_t tk = r + 4u * i;
+      const uint32_t tk = r + (uint32_t)RPI * i;
       float v[4];
       load_elems<IO, 4>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
       x[i] = make_float4(v[0], v[1], v[2], v[3]);
@@ -234,10 +241,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
     float l[4] = {lo.x, lo.y, lo.z, lo.w}, h[4] = {hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      l[k] = fminf(l[k], __shfl_xor(l[k], 16));
-      h[k] = fmaxf(h[k], __shfl_xor(h[k], 16));
-      l[k] = fminf(l[k], __shfl_xor(l[k], 32));
-      h[k] = fmaxf(h[k], __shfl_xor(h[k], 32));
+#pragma unroll
+      for (int off = QW; off < 64; off <<= 1) {
+        l[k] = fminf(l[k], __shfl_xor(l[k], off));
+        h[k] = fmaxf(h[k], __shfl_xor(h[k], off));
+      }
     }
     uint16_t l16[4], h16[4];
     float bs[4], st[4], inv[4];
@@ -258,7 +266,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
     // codes clip(floor((x - lo) / step + 0.5), 0, 2^B - 1) (pitch_reference.py:157-158), one byte each in LDS
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
-      const uint32_t tk = r + 4u * i;
+      const uint32_t tk = r + (uint32_t)RPI * i;
       if (tk < n && cact) {
         const float xv[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
         uint32_t word = 0u;
@@ -270,7 +278,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
           if (!(f > kKiviGuard && f < 1.0f - kKiviGuard)) q = floorf(a / st[k] + 0.5f);  // exact division
           word |= (uint32_t)fminf(fmaxf(q, 0.0f), levels) << (8 * k);
         }
-        *(uint32_t*)(s_stage + tk * kSlab + 4u * c) = word;
+        *(uint32_t*)(s_stage + tk * SW + 4u * c) = word;
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -282,7 +290,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
       const uint32_t gpr = cw >> 5, ng = n * gpr;  // 32-code groups per row, then in all
       for (uint32_t q = lane; q < ng; q += 64) {
         const uint32_t tok = q / gpr, gi = q - tok * gpr;
-        const uint4* s4 = (const uint4*)(s_stage + tok * kSlab + 32u * gi);
+        const uint4* s4 = (const uint4*)(s_stage + tok * SW + 32u * gi);
         const uint4 q0 = s4[0], q1 = s4[1];
         const uint32_t bytes[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         uint32_t w[B];
@@ -294,7 +302,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
       const uint32_t wpr = p.nwords - ch0 * B / 32u, nw = n * wpr;
       for (uint32_t q = lane; q < nw; q += 64) {
         const uint32_t tok = q / wpr, wi = q - tok * wpr;
-        const uint8_t* row = s_stage + tok * kSlab;
+        const uint8_t* row = s_stage + tok * SW;
         uint32_t word = 0u;
         for (uint32_t i = (32u * wi) / B; i < cw; ++i) {
           const int sh = (int)(i * B) - (int)(32u * wi);
@@ -487,9 +495,21 @@ template <int B, int IO>
 hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
   const bool vec4 = (a.dim & 3u) == 0u;
   if (encode && vec4 && a.group <= (uint32_t)kGroupMaxW) {
-    const uint64_t items = (((uint64_t)a.count + a.group - 1) / a.group) * ((a.dim + kSlab - 1) / kSlab);
-    const uint64_t grid = persistent_grid((const void*)&chan_encode_w<B, IO>, (items + 3) / 4);
-    hipLaunchKernelGGL((chan_encode_w<B, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;
+    // 32-channel slabs double the work items and halve each lane's registers, which balances calls with few
+    // (group, 64-channel) items over the resident waves (+5-10 % at 4096-8192 items); long calls keep
+    // 64-channel slabs, whose loads read whole 256-byte rows (+4 % at 131072 items)
+    const uint64_t items64 = groups * ((a.dim + 63) / 64);
+    const int sw = PITCH_KIVI_SLAB ? PITCH_KIVI_SLAB : (items64 <= 32768 ? 32 : 64);
+    if (sw == 32) {
+      const uint64_t items = groups * ((a.dim + 31) / 32);
+      const uint64_t grid = persistent_grid((const void*)&chan_encode_w<B, IO, 32>, (items + 3) / 4);
+      hipLaunchKernelGGL((chan_encode_w<B, IO, 32>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    } else {
+      const uint64_t items = groups * ((a.dim + 63) / 64);
+      const uint64_t grid = persistent_grid((const void*)&chan_encode_w<B, IO, 64>, (items + 3) / 4);
+      hipLaunchKernelGGL((chan_encode_w<B, IO, 64>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    }
   } else if (encode) {
     const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;
     const void* k = vec4 ? (const void*)&chan_encode4<B, IO> : (const void*)&chan_encode1<B, IO>;

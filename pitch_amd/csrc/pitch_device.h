@@ -201,11 +201,22 @@ __device__ __forceinline__ void widen2(uint32_t w, float& a, float& b) {
 }
 
 // (a, b) rounded to the 16-bit type and packed, a in the low half.
+#ifndef PITCH_F16_PACKED_CVT
+#define PITCH_F16_PACKED_CVT 1  // float16: one v_cvt_pk_f16_f32 per pair (0: two v_cvt_f16_f32)
+#endif
 template <int IO>
 __device__ __forceinline__ uint32_t narrow2(float a, float b) {
   const f32x2 v{a, b};
-  if constexpr (IO == 1) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
-  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  if constexpr (IO == 1) {
+    if constexpr (PITCH_F16_PACKED_CVT) {
+      return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+    } else {
+      const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)a), hi = __builtin_bit_cast(uint16_t, (_Float16)b);
+      return lo | (hi << 16);
+    }
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  }
 }
 
 template <int IO>

@@ -246,8 +246,11 @@ struct TqQuant {
 #endif
 
 // ----------------------------------------------------------------------------------------------------
+#ifndef PITCH_POLAR_WAVES
+#define PITCH_POLAR_WAVES 1  // minimum waves per SIMD requested for the team encoder (caps its VGPRs)
+#endif
 template <int D, int B, bool POLAR, int IO, bool KBIAS>
-__global__ __launch_bounds__(kBlock) void vec_encode(VecArgs p) {
+__global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode(VecArgs p) {
   using G = Geom<D>;
   constexpr int L = 1 << B;
   constexpr int NW = (D * B + 31) / 32;  // 32-bit words of codes per vector

@@ -110,7 +110,7 @@ def test_more_than_2_32_floats_in_one_call(q):
     per_vector_full(q, "turboQuant", (1 << 22) + 100, 1024, 4, 6000, "gauss")
 
 
-def channel_full(q, heads, tokens, d, bits, G, seed):
+def channel_full(q, heads, tokens, d, bits, G, seed, one_call=False):
     import torch
     import pitch_amd as P
     dev = q.device
@@ -121,7 +121,11 @@ def channel_full(q, heads, tokens, d, bits, G, seed):
     codes = torch.empty(heads * tokens * cfg.codeStride, dtype=torch.uint8, device=dev)
     ranges = torch.empty(heads * groups * cfg.rangeStride // 2, dtype=torch.float16, device=dev)
     out = torch.empty(heads * tokens, d, dtype=torch.float32, device=dev)
-    for h in range(heads):           # one call per head, at its offsets in the whole cache
+    if one_call:                     # all heads in one call: groups never cross a head (tokens % G == 0)
+        assert tokens % G == 0
+        q.enqueuePerChannelEncode(x, codes, ranges, heads * tokens, cfg)
+        q.enqueuePerChannelDecode(codes, ranges, out, heads * tokens, cfg)
+    for h in range(0 if one_call else heads):   # one call per head, at its offsets in the whole cache
         q.enqueuePerChannelEncode(x, codes, ranges, tokens, cfg, inputOffset=h * tokens * d * 4,
                                   codesOffset=h * tokens * cfg.codeStride, rangesOffset=h * groups * cfg.rangeStride)
         q.enqueuePerChannelDecode(codes, ranges, out, tokens, cfg, codesOffset=h * tokens * cfg.codeStride,
@@ -152,3 +156,9 @@ def test_config3_kivi_keys(q):
 
 def test_config5_k_share(q):
     channel_full(q, 32, 131072, 128, 4, 64, 5001)
+
+
+def test_config5_k_share_one_call(q):
+    """16 heads x 131072 tokens in one call: 65,536 (group, 64-channel) items, so the encoder takes its
+    64-channel-slab variant (fewer items take the 32-channel one, covered above)."""
+    channel_full(q, 16, 131072, 128, 4, 64, 5002, one_call=True)
