@@ -129,6 +129,86 @@ __device__ __forceinline__ void fwht(F (&v)[Geom<D>::E], int t) {
   });
 }
 
+// ---------------------------------------------------------------------------------------------------
+// Cross-lane butterflies as one instruction per element. v_fmac_f32 with a DPP quad permute on its first
+// operand computes v = partner * sg + v: with sg = +1 on the low lane of a pair and -1 on the high lane, the
+// low lane gets a + b and the high lane b - a = -(a - b), each with the single rounding of a + b or a - b.
+// The compiler does not form this instruction from mov_dpp + fma, hence the inline assembly. A DPP read
+// needs two wait states after a VALU write of its source register: the leading s_nop covers the block's
+// inputs, the trailing one a compiler-emitted DPP read of its outputs.
+#ifndef PITCH_DPP_FMAC
+#define PITCH_DPP_FMAC 1
+#endif
+#define PITCH_FMAC_DPP(I, PERM) "v_fmac_f32_dpp %" #I ", %" #I ", %16 " PERM " row_mask:0xf bank_mask:0xf\n"
+#define PITCH_FMAC_DPP16(PERM)                                                                              \
+  "s_nop 1\n" PITCH_FMAC_DPP(0, PERM) PITCH_FMAC_DPP(1, PERM) PITCH_FMAC_DPP(2, PERM) PITCH_FMAC_DPP(3, PERM) \
+      PITCH_FMAC_DPP(4, PERM) PITCH_FMAC_DPP(5, PERM) PITCH_FMAC_DPP(6, PERM) PITCH_FMAC_DPP(7, PERM)          \
+          PITCH_FMAC_DPP(8, PERM) PITCH_FMAC_DPP(9, PERM) PITCH_FMAC_DPP(10, PERM) PITCH_FMAC_DPP(11, PERM)   \
+              PITCH_FMAC_DPP(12, PERM) PITCH_FMAC_DPP(13, PERM) PITCH_FMAC_DPP(14, PERM)                      \
+                  PITCH_FMAC_DPP(15, PERM) "s_nop 1\n"
+
+template <int LM, int O, int E>
+__device__ __forceinline__ void fmac_dpp16(float (&v)[E], float sg) {
+  static_assert((LM == 1 || LM == 2) && O + 16 <= E, "quad permutes over 16 elements");
+#define PITCH_FMAC_DPP_OPS                                                                                  \
+  : "+v"(v[O]), "+v"(v[O + 1]), "+v"(v[O + 2]), "+v"(v[O + 3]), "+v"(v[O + 4]), "+v"(v[O + 5]),             \
+    "+v"(v[O + 6]), "+v"(v[O + 7]), "+v"(v[O + 8]), "+v"(v[O + 9]), "+v"(v[O + 10]), "+v"(v[O + 11]),       \
+    "+v"(v[O + 12]), "+v"(v[O + 13]), "+v"(v[O + 14]), "+v"(v[O + 15])                                      \
+  : "v"(sg)
+  if constexpr (LM == 1)
+    asm(PITCH_FMAC_DPP16("quad_perm:[1,0,3,2]") PITCH_FMAC_DPP_OPS);
+  else
+    asm(PITCH_FMAC_DPP16("quad_perm:[2,3,0,1]") PITCH_FMAC_DPP_OPS);
+#undef PITCH_FMAC_DPP_OPS
+}
+
+// Lanes of the team whose cross-lane stages fwht_f32_lane_signed runs as v_fmac_f32_dpp (distances 1 and 2,
+// when E is a multiple of 16).
+template <int D>
+__host__ __device__ constexpr int dpp_lane_bits() {
+  return (PITCH_DPP_FMAC && Geom<D>::E % 16 == 0) ? (3 & (Geom<D>::T - 1)) : 0;
+}
+// Sign bit that lane t's results of fwht_f32_lane_signed carry: (-1)^popcount(t & dpp_lane_bits).
+template <int D>
+__device__ __forceinline__ uint32_t dpp_lane_sign_bit(int t) {
+  return (uint32_t)(__builtin_popcount((unsigned)(t & dpp_lane_bits<D>())) & 1) << 31;
+}
+
+// fwht<D, float> with the cross-lane stages at distances 1 and 2 done by fmac_dpp16. The high lane of each
+// such pair comes out negated, and every later butterfly pairs lanes that carry the same sign (they differ
+// only in higher lane bits or are the same lane), so the factor passes through unchanged: lane t's results
+// equal the transform times (-1)^popcount(t & dpp_lane_bits<D>()), bit for bit up to that sign (b - a
+// and -(a - b) round alike; only a zero may come out with the other sign). The first PRE stages (bits
+// below PRE <= log2 W, inside a chunk) are taken as already applied by the caller.
+template <int D, int PRE = 0>
+__device__ __forceinline__ void fwht_f32_lane_signed(float (&v)[Geom<D>::E], int t) {
+  using G = Geom<D>;
+  static_assert(PRE >= 0 && PRE <= G::LGW, "pre-applied stages lie inside a chunk");
+  static_for<PRE, G::LGD>([&](auto bit_c) {
+    constexpr int bit = decltype(bit_c)::value;
+    if constexpr (bit >= G::LGW && bit < G::LGW + G::LGT) {
+      constexpr int lm = 1 << (bit - G::LGW);
+      const float sg = (t & lm) ? -1.0f : 1.0f;
+      if constexpr ((dpp_lane_bits<D>() & lm) != 0) {
+        static_for<0, G::E / 16>([&](auto o_c) { fmac_dpp16<lm, 16 * decltype(o_c)::value>(v, sg); });
+      } else {
+#pragma unroll
+        for (int e = 0; e < G::E; ++e) v[e] = fma_t(v[e], sg, xchg<lm>(v[e]));
+      }
+    } else {
+      constexpr int m = bit < G::LGW ? (1 << bit) : (G::W << (bit - G::LGW - G::LGT));
+#pragma unroll
+      for (int e = 0; e < G::E; ++e) {
+        if (!(e & m)) {
+          const float a = v[e], b = v[e | m];
+          v[e] = a + b;
+          v[e | m] = a - b;
+        }
+      }
+    }
+  });
+}
+
 // Unnormalised Walsh-Hadamard transform of E contiguous coordinates per lane across a team of T lanes:
 // coordinate c = t * E + e; stages in the reference's order, bits >= log2 E cross lanes.
 template <int E, int T, typename F>

@@ -422,6 +422,9 @@ struct DecTab {
   static constexpr int G = W < 4 ? (B <= 5 ? 2 : 1) : (POLAR ? (B <= 5 ? 2 : 1) : (B == 2 ? 4 : (B <= 5 ? 2 : 1)));
   static constexpr int ENTRIES = G == 4 ? 256 : (G == 2 ? (1 << (2 * B)) : L);
   static constexpr int FLOATS = G == 1 ? (POLAR ? 3 * L : L) : ENTRIES * G;
+  // transform stages folded into the table: an entry of G consecutive coordinates holds their values after
+  // the butterflies on coordinate bits 0 .. log2(G) - 1, the first stages of the transform
+  static constexpr int PRE = G == 4 ? 2 : (G == 2 ? 1 : 0);
 };
 
 template <int D, int B, bool POLAR>
@@ -436,8 +439,9 @@ __device__ __forceinline__ void build_dec_table(float* s_tab) {
     if constexpr (TB::G == 2) {
       for (int i = threadIdx.x; i < TB::ENTRIES; i += kBlock) {
         const float r = rad[i & (L - 1)];
-        s_tab[2 * i] = r * cs[i >> B];
-        s_tab[2 * i + 1] = r * sn[i >> B];
+        const float x = r * cs[i >> B], y = r * sn[i >> B];
+        s_tab[2 * i] = x + y;
+        s_tab[2 * i + 1] = x - y;
       }
     } else {
       for (int i = threadIdx.x; i < L; i += kBlock) {
@@ -450,13 +454,18 @@ __device__ __forceinline__ void build_dec_table(float* s_tab) {
     const float* cb = pitch_codebook_tab + pitch_codebook_offset(ilog2(D), B);
     if constexpr (TB::G == 4) {
       for (int i = threadIdx.x; i < 256; i += kBlock) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s_tab[4 * i + r] = cb[(i >> (2 * r)) & 3];
+        const float q0 = cb[i & 3], q1 = cb[(i >> 2) & 3], q2 = cb[(i >> 4) & 3], q3 = cb[i >> 6];
+        const float a0 = q0 + q1, a1 = q0 - q1, a2 = q2 + q3, a3 = q2 - q3;
+        s_tab[4 * i] = a0 + a2;
+        s_tab[4 * i + 1] = a1 + a3;
+        s_tab[4 * i + 2] = a0 - a2;
+        s_tab[4 * i + 3] = a1 - a3;
       }
     } else if constexpr (TB::G == 2) {
       for (int i = threadIdx.x; i < TB::ENTRIES; i += kBlock) {
-        s_tab[2 * i] = cb[i & (L - 1)];
-        s_tab[2 * i + 1] = cb[i >> B];
+        const float x = cb[i & (L - 1)], y = cb[i >> B];
+        s_tab[2 * i] = x + y;
+        s_tab[2 * i + 1] = x - y;
       }
     } else {
       for (int i = threadIdx.x; i < L; i += kBlock) s_tab[i] = cb[i];
@@ -464,7 +473,8 @@ __device__ __forceinline__ void build_dec_table(float* s_tab) {
   }
 }
 
-// Unpacks the W codes of one chunk (bits [0, W*B) of `bits`) into W rotated-domain values.
+// Unpacks the W codes of one chunk (bits [0, W*B) of `bits`) into W rotated-domain values, with the first
+// DecTab::PRE transform stages already applied.
 template <int D, int B, bool POLAR>
 __device__ __forceinline__ void decode_chunk(uint32_t bits, const float* s_tab, float* y) {
   using TB = DecTab<B, POLAR, Geom<D>::W>;
@@ -527,9 +537,11 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
 
   build_dec_table<D, B, POLAR>(s_tab);
   const uint32_t fbits = p.lane_flips[t];
+  // the transform's lane sign (fwht_f32_lane_signed) is folded into the random sign flips
+  const uint32_t lane_sign = dpp_lane_sign_bit<D>(t);
   uint32_t flip[G::E];
 #pragma unroll
-  for (int e = 0; e < G::E; ++e) flip[e] = ((fbits >> e) & 1u) << 31;
+  for (int e = 0; e < G::E; ++e) flip[e] = (((fbits >> e) & 1u) << 31) ^ lane_sign;
   // word index and bit offset of each of this lane's chunks (the next word is read when a chunk straddles)
   int wlo[G::CH], whi[G::CH];
   uint32_t wsh[G::CH];
@@ -562,17 +574,17 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
     }
     return b;
   };
-  auto body = [&](const Batch& b, uint64_t base, auto tail_c) {
-    constexpr bool TAIL = decltype(tail_c)::value;
-    const uint64_t v = base + slot;
-    const bool valid = !TAIL || v < p.count;
-    float y[G::E];
+  // table lookups and the transform, shared by the full and the tail iteration
+  auto transform = [&](const Batch& b, float (&y)[G::E]) {
 #pragma unroll
     for (int k = 0; k < G::CH; ++k)
       decode_chunk<D, B, POLAR>(__builtin_amdgcn_alignbit(b.hi[k], b.lo[k], wsh[k]), s_tab, y + k * G::W);
-
-    fwht<D, float>(y, t);
-
+    fwht_f32_lane_signed<D, TB::PRE>(y, t);
+  };
+  auto body = [&](const Batch& b, float (&y)[G::E], uint64_t base, auto tail_c) {
+    constexpr bool TAIL = decltype(tail_c)::value;
+    const uint64_t v = base + slot;
+    const bool valid = !TAIL || v < p.count;
     const float f = b.scale * DimConst<D>::kInvSqrtF;
     if constexpr (kLdsStore) {
       // stage the wave's vectors in LDS, then write them back as contiguous 1 KB wave stores
@@ -636,8 +648,10 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   for (;;) {
     const uint64_t nbase = base + stride;
     const Batch nxt = fetch(nbase < p.count ? nbase : base);
-    if (base + G::VPB <= p.count) body(cur, base, std::false_type{});
-    else body(cur, base, std::true_type{});
+    float y[G::E];
+    transform(cur, y);
+    if (base + G::VPB <= p.count) body(cur, y, base, std::false_type{});
+    else body(cur, y, base, std::true_type{});
     if (nbase >= p.count) break;
     cur = nxt;
     base = nbase;
