@@ -156,60 +156,83 @@ __device__ __forceinline__ void key_bias_offset(const VecArgs& p, uint64_t v, in
 }
 
 // TurboQuant quantiser: code = #{edges < u}, searchsorted(edges, u, 'left') (pitch_reference.py:99-101).
-// With a bucket table (gen_tables.py lut_for): j = clamp(floor(u * 2^m + off)), code = c_j + [u > e_j], one
-// 8-byte LDS read per coordinate (e_j as float32 bits, c_j). Lookups are issued in batches of up to 15 (what
-// the LDS wait counter tracks) before any result is used, so a wave pays one LDS round trip per batch, not per
-// coordinate. Tables too large for LDS use a binary search over the float64 edges.
+// With a bucket table (gen_tables.py lut_for): bucket j = floor(u * 2^m + off), clamped to [0, n), holds at
+// most one edge e_j, and code = c_j + [u > e_j]. The comparison is made in the bucket domain: one fma gives
+// t = u * 2^m + off + 2^16 + 2^15 in float64, which lies in [2^16, 2^17) for every |u| <= 1, so the top 20
+// mantissa bits (the high word's low 20 bits) are floor(16 * (t - 2^16)) and bits 4 .. 19 of the high word
+// hold the bucket index plus 2^15. A med3 clamp of the high word and a mask give the byte offset 16 * j of
+// the entry directly. Each entry holds E_j = e_j * 2^m + off + 2^16 + 2^15 (exact in float64: 2^m is a
+// power of two) and c_j, and t > E_j decides the code: it equals u > e_j except where u lies within the
+// rounding of t (2^-37 bucket units) of the edge, far inside the near-boundary band. Lookups are issued in
+// batches of up to 15 (what the LDS wait counter tracks) before any result is used, so a wave pays one LDS
+// round trip per batch, not per coordinate. Tables too large for LDS use a binary search over the float64
+// edges.
 template <int D, int B>
 struct TqQuant {
   static constexpr int L = 1 << B;
   static constexpr PitchLutInfo LI = pitch_lut_info(ilog2(D), B);
   static constexpr bool kLut = LI.offset >= 0;
   static constexpr int kBatch = PITCH_QBATCH;
+  static constexpr double kMagic = 98304.0 + LI.off;  // 2^16 + 2^15 + off
+  static constexpr int kIdxBits = kLut ? ilog2(2 * LI.entries - 1) : 1;  // 2^kIdxBits >= entries
+  static constexpr uint32_t kHiLo = 0x40F80000u;                          // high word of t at j = 0
+  static constexpr uint32_t kHiHi = kHiLo + 16u * (uint32_t)((kLut ? LI.entries : 1) - 1) + 15u;
+  static constexpr uint32_t kMask = ((1u << kIdxBits) - 1u) << 4;
+  static_assert(!kLut || (kIdxBits <= 15 && LI.scale + LI.off < 32768.0), "bucket index inside the high word");
 
+  struct alignas(16) Ent {
+    double e;    // E_j, the edge in the bucket domain (+inf past the last edge)
+    uint32_t c;  // c_j
+    uint32_t pad;
+  };
   struct Smem {
-    uint2 lut[kLut ? LI.entries : 1];  // (float32 bits of e_j, c_j)
+    Ent lut[kLut ? LI.entries : 1];
     double edge64[kLut ? 1 : L];
   };
 
   __device__ static void load(Smem& sm, int tid, int nthreads) {
     if constexpr (kLut) {
-      for (int i = tid; i < LI.entries; i += nthreads)
-        sm.lut[i] = make_uint2(pitch_lut_tab[2 * (LI.offset + i)], pitch_lut_tab[2 * (LI.offset + i) + 1]);
+      for (int i = tid; i < LI.entries; i += nthreads) {
+        const float e = __uint_as_float(pitch_lut_tab[2 * (LI.offset + i)]);
+        sm.lut[i].e = __builtin_fma((double)e, LI.scale, kMagic);  // exact; inf stays inf
+        sm.lut[i].c = pitch_lut_tab[2 * (LI.offset + i) + 1];
+        sm.lut[i].pad = 0u;
+      }
     } else {
       constexpr int off = pitch_codebook_offset(ilog2(D), B);
       for (int i = tid; i < L; i += nthreads) sm.edge64[i] = (double)pitch_edge_tab[off + i];
     }
   }
 
-  // Bucket of u = x * us: |u| <= 1 for the coordinates of a rotated unit vector, so the index fits an int.
-  __device__ static int bucket(double x, double us_m) {
-    const int j = (int)__builtin_fma(x, us_m, LI.off);
-    return min(max(j, 0), LI.entries - 1);
-  }
-
   // Applies f(e, code) to the codes of x[0..N) in order, with u = x * us.
   template <int N, typename F>
   __device__ static void for_codes(const Smem& sm, const double (&x)[N], double us, F&& f) {
     if constexpr (kLut) {
-      const double us_m = us * LI.scale;
+      const double us_m = us * LI.scale;  // exact: LI.scale is a power of two
+      typedef uint32_t u32x4n __attribute__((ext_vector_type(4)));  // naturally (16-byte) aligned
+      typedef __attribute__((address_space(3))) const u32x4n lds_u32x4;
+      typedef __attribute__((address_space(3))) const char lds_byte;
+      lds_byte* tab = (lds_byte*)(sm.lut);
 #pragma unroll
       for (int b0 = 0; b0 < N; b0 += kBatch) {
-        // one 8-byte read per entry through a 32-bit LDS address
-        struct W2 { uint32_t e, c; };
-        typedef __attribute__((address_space(3))) const W2 lds_w2;
-        lds_w2* tab = (lds_w2*)(sm.lut);
-        W2 ent[kBatch];
+        double tt[kBatch];
+        double ee[kBatch];
+        uint32_t cc[kBatch];
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
           if (b0 + i < N) {
-            const int j = bucket(x[b0 + i], us_m);
-            ent[i] = W2{tab[j].e, tab[j].c};
+            tt[i] = __builtin_fma(x[b0 + i], us_m, kMagic);
+            const uint32_t hi = (uint32_t)((uint64_t)__double_as_longlong(tt[i]) >> 32);
+            const uint32_t hc = min(max(hi, kHiLo), kHiHi);  // NaN and out-of-table u land on an end bucket
+            // one 16-byte read per entry (the offset is a multiple of 16)
+            const u32x4n w = *(lds_u32x4*)(tab + (hc & kMask));
+            ee[i] = __longlong_as_double((long long)(((uint64_t)w.y << 32) | w.x));
+            cc[i] = w.z;
           }
         }
 #pragma unroll
         for (int i = 0; i < kBatch; ++i)
-          if (b0 + i < N) f(b0 + i, ent[i].c + (x[b0 + i] * us > (double)__uint_as_float(ent[i].e) ? 1u : 0u));
+          if (b0 + i < N) f(b0 + i, cc[i] + (tt[i] > ee[i] ? 1u : 0u));
       }
     } else {
 #pragma unroll
