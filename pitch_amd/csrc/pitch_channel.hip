@@ -184,11 +184,14 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
 // are reduced across the four token phases with two lane exchanges; every lane then knows the fp16 range of
 // its channels. Codes are staged as bytes in the wave's LDS slice and packed 32 at a time.
 //
-// Quantiser: the reference's t = RN(RN((x - lo) / step) + 0.5) (pitch_reference.py:157, float32) is first
-// taken as RN(RN((x - lo) * RN(1 / step)) + 0.5), which is within 3 float32 ulps of t (under 5e-5 for
-// t < 256). floor(t) is kept when t is at least kKiviGuard from an integer; otherwise the correctly rounded
-// division decides (the library is built with -fhip-fp32-correctly-rounded-divide-sqrt).
-constexpr float kKiviGuard = 1e-4f;
+// Quantiser: the reference's t = RN(RN((x - lo) / step) + 0.5) (pitch_reference.py:157, float32) exactly,
+// without a division per element. With inv = RN(1 / step) (one correctly rounded division per channel),
+// q0 = RN(a * inv) is within one ulp of a / step, the residual r = a - q0 * step is exact in one fma, and
+// q0 + r * inv rounded once is RN(a / step) (Markstein's theorem for a correctly rounded reciprocal). The
+// step itself, RN((hi - lo) / (2^B - 1)), is obtained the same way with the constant RN(1 / (2^B - 1)).
+// Outside the theorem's range nothing decides a code: a step of +inf (a range end beyond fp16) is clamped to
+// FLT_MAX in the residual so that a finite a gives q = 0 as a / inf does, and only a subnormal quotient
+// (|a / step| < 2^-126, whose code is 0 either way) may differ from RN(a / step).
 #ifndef PITCH_KIVI_WAVES
 #define PITCH_KIVI_WAVES 3  // waves per SIMD the per-channel encoder's register budget allows
 #endif
@@ -248,14 +251,19 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
       }
     }
     uint16_t l16[4], h16[4];
-    float bs[4], st[4], inv[4];
+    float bs[4], stc[4], inv[4];
+    constexpr float kInvLevels = 1.0f / (float)((1 << B) - 1);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       l16[k] = f2h_bits(l[k]);
       h16[k] = f2h_bits(h[k]);
       bs[k] = h2f(l16[k]);
-      st[k] = kivi_step(bs[k], h2f(h16[k]), levels);
-      inv[k] = 1.0f / st[k];
+      const float d = h2f(h16[k]) - bs[k];
+      const float s0 = d * kInvLevels;
+      const float sq = __builtin_fmaf(__builtin_fmaf(-s0, levels, d), kInvLevels, s0);  // RN(d / levels)
+      const float st = sq == 0.0f ? 1.0f : sq;                                            // kivi_step
+      inv[k] = 1.0f / st;
+      stc[k] = __builtin_fminf(st, 0x1.fffffep127f);
     }
     if (r == 0 && cact) {
       uint16_t* rg = p.ranges_out + (uint64_t)g * 2u * dim + ch0 + 4u * c;
@@ -263,23 +271,23 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
       *(u32x2*)(rg + dim) =
           u32x2{(uint32_t)h16[0] | ((uint32_t)h16[1] << 16), (uint32_t)h16[2] | ((uint32_t)h16[3] << 16)};
     }
-    // codes clip(floor((x - lo) / step + 0.5), 0, 2^B - 1) (pitch_reference.py:157-158), one byte each in LDS
+    // codes clip(floor((x - lo) / step + 0.5), 0, 2^B - 1) (pitch_reference.py:157-158), one byte each in LDS.
+    // Rows past the group's end and channels past the slab's end are quantised and staged too (their slots
+    // exist and are never packed), so the loop has no branches.
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
       const uint32_t tk = r + (uint32_t)RPI * i;
-      if (tk < n && cact) {
-        const float xv[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
-        uint32_t word = 0u;
+      const float xv[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+      uint32_t word = 0u;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float a = xv[k] - bs[k];
-          float q = floorf(a * inv[k] + 0.5f);
-          const float f = (a * inv[k] + 0.5f) - q;
-          if (!(f > kKiviGuard && f < 1.0f - kKiviGuard)) q = floorf(a / st[k] + 0.5f);  // exact division
-          word |= (uint32_t)fminf(fmaxf(q, 0.0f), levels) << (8 * k);
-        }
-        *(uint32_t*)(s_stage + tk * SW + 4u * c) = word;
+      for (int k = 0; k < 4; ++k) {
+        const float a = xv[k] - bs[k];
+        const float q0 = a * inv[k];
+        const float q = __builtin_fmaf(__builtin_fmaf(-q0, stc[k], a), inv[k], q0);  // RN(a / step)
+        const float t = __builtin_floorf(q + 0.5f);
+        word |= (uint32_t)__builtin_fminf(__builtin_fmaxf(t, 0.0f), levels) << (8 * k);
       }
+      *(uint32_t*)(s_stage + tk * SW + 4u * c) = word;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
