@@ -125,3 +125,19 @@ def test_uncorrected_product_is_not_enough():
         misses += f32(a * inv) != f32(a / step)
         assert quotient(float(a), float(step)) == float(f32(a / step))
     assert misses > 0
+
+
+def test_native_sweep(tmp_path):
+    """The same arithmetic in C with hardware fmaf over 1.5M ranges x 8 values (tests/division_sweep.c)."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    exe = tmp_path / "division_sweep"
+    src = Path(__file__).with_name("division_sweep.c")
+    subprocess.run([cc, "-O2", "-ffp-contract=off", str(src), "-o", str(exe), "-lm"], check=True)
+    out = subprocess.run([str(exe), "1500000"], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "code_diff 0" in out.stdout
