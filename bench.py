@@ -230,7 +230,7 @@ def main() -> int:
         "pct_of_hbm_peak": round(100 * gbps / PEAK_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": f"pitch::vec_decode<64, {b}, false>",
+                     "kernel": f"pitch::vec_decode<64, {b}, false, 0, false>",
                      "kernel_us_per_launch": round(ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": nbytes,
                      "traffic_source": ("profiles/vec_decode_d64_b4_config2_hbm_traffic.md (rocprofv3 FETCH_SIZE x2 "
