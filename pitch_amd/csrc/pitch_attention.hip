@@ -15,6 +15,8 @@
 //   attn_scores   one thread per token: scores in log2 units into LDS, chunk max m_c, p = 2^(s - m_c), l_c
 //   attn_values   16 lanes per token: a_c = sum_t p_t n_t t[c_t] in the rotated domain
 //   attn_combine  merges the chunks, divides by the softmax sum, inverse rotation, output and log-sum-exp
+// With equal key and value bit widths attn_chunk runs the scores and values phases in one kernel and keeps the
+// weights p in LDS (attn_scores and attn_values remain for unequal widths and for per-channel keys).
 // Query heads of one KV head (grouped-query attention) share every table read; their count is padded to
 // 1, 2, 4 or 8 (padded queries are zero and never written out).
 #include "pitch_device.h"
@@ -27,6 +29,9 @@ namespace pitch {
 namespace {
 
 constexpr int kMaxChunk = 1024;          // tokens per workgroup; a chunk's scores stay in LDS
+#ifndef PITCH_ATTN_FUSED
+#define PITCH_ATTN_FUSED 1  // keys and values of equal bit width: scores and values in one kernel (attn_chunk)
+#endif
 constexpr float kLn2 = 0x1.62e430p-1f;   // ln(2)
 
 // Workspace regions (floats): rotated queries [kv][D/2][nqp][2], weights p [kv][T][nqp],
@@ -155,21 +160,19 @@ __global__ __launch_bounds__(64) void attn_prep(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------- scores
-// Workgroup (chunk, KV head); thread = token. qp (the rotated queries of this KV head, read-only here) is
-// passed separately so its wave-uniform reads can be scalar loads.
-template <int D, int B, int NQ>
-__global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* __restrict__ qp_all) {
+// Scores of chunk c of KV head kv, one thread per token, into s_s in log2 units; then the chunk maximum m, the
+// weights p = 2^(s - m) and their sum l. (m, l) go to the workspace; the weights overwrite s_s, or with
+// WRITE_P go to the workspace for a separate values kernel. The table s_tab holds the key codes' pair values.
+// qp (the rotated queries of this KV head, read-only here) is passed separately so its wave-uniform reads can
+// be scalar loads.
+template <int D, int B, int NQ, bool WRITE_P>
+__device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __restrict__ qp_all, const float2* s_tab,
+                                             float* s_s, float* s_red, uint32_t kv, uint32_t c) {
   using P = PairLut<D, B>;
   constexpr int NW = D * B / 32;
-  __shared__ float2 s_tab[P::N];
-  __shared__ float s_s[kMaxChunk * NQ];
-  __shared__ float s_red[4 * NQ];
   const int tid = threadIdx.x;
-  const uint32_t kv = blockIdx.y, c = blockIdx.x;
   const uint64_t t0 = (uint64_t)c * a.chunk;
   const uint32_t n = (uint32_t)min((uint64_t)a.chunk, a.tokens - t0);
-  P::build(s_tab, a.kpolar != 0);
-  __syncthreads();
   const float* __restrict__ qp = qp_all + (uint64_t)kv * D * NQ;
 
   // software pipeline: the next token's code row and scale are loaded before this token's scores are computed
@@ -231,15 +234,16 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
       e[h] = exp2f(s_s[i * NQ + h] - m[h]);
       l[h] += e[h];
     }
+    float* dst = WRITE_P ? pw : s_s;  // each thread rewrites only the scores it read
     if constexpr (NQ % 4 == 0) {
 #pragma unroll
-      for (int h = 0; h < NQ; h += 4) *(f32x4*)(pw + (uint64_t)i * NQ + h) = f32x4{e[h], e[h + 1], e[h + 2], e[h + 3]};
+      for (int h = 0; h < NQ; h += 4) *(f32x4*)(dst + (uint64_t)i * NQ + h) = f32x4{e[h], e[h + 1], e[h + 2], e[h + 3]};
     } else {
 #pragma unroll
-      for (int h = 0; h < NQ; ++h) pw[(uint64_t)i * NQ + h] = e[h];
+      for (int h = 0; h < NQ; ++h) dst[(uint64_t)i * NQ + h] = e[h];
     }
   }
-  block_reduce<NQ, false>(l, s_red);
+  block_reduce<NQ, false>(l, s_red);  // its barriers also publish the weights in s_s
   if (tid == 0) {
     float* ml = a.ws + L.ml;
 #pragma unroll
@@ -249,6 +253,18 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
       ml[k + 1] = l[h];
     }
   }
+}
+
+// Workgroup (chunk, KV head); thread = token.
+template <int D, int B, int NQ>
+__global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* __restrict__ qp_all) {
+  using P = PairLut<D, B>;
+  __shared__ float2 s_tab[P::N];
+  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ];
+  __shared__ float s_red[4 * NQ];
+  P::build(s_tab, a.kpolar != 0);
+  __syncthreads();
+  scores_phase<D, B, NQ, true>(a, qp_all, s_tab, s_s, s_red, blockIdx.y, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------------------------- scores, KIVI keys
@@ -382,28 +398,31 @@ __global__ __launch_bounds__(kBlock) void attn_scores_chan(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------- values
-// Workgroup (chunk, KV head). Per block of 256 tokens, each thread stages one token's code row and weights
-// p * n in LDS; then lane (r, g) of wave w takes token 16 * step + 4 * w + r and the g-th 16th of its code pairs,
-// accumulating sum_t p_t n_t t[c_t] for its 2 * PPL coordinates and every query head.
-template <int D, int B, int NQ>
-__global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
+// a_c = sum_t p_t n_t t[c_t] over chunk c of KV head kv into the workspace. Per block of 256 tokens, each thread
+// stages one token's code row and weights p * n in LDS; then lane (r, g) of wave w takes token
+// 16 * step + 4 * w + r and the g-th 16th of its code pairs, accumulating its 2 * PPL coordinates for every
+// query head. The weights p come from s_p (P_LDS, the fused kernel) or from the workspace. s_acc may alias
+// s_code: it is written only after a barrier that ends the staging.
+template <int D, int B>
+struct ValuesLayout {
+  static constexpr int NW = D * B / 32;
+  static constexpr int RS = NW + 1;  // staged row stride in words (odd: consecutive rows start on other banks)
+  static constexpr int kCodeWords = kBlock * RS + 4;
+};
+template <int D, int B, int NQ, bool P_LDS>
+__device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_tab, const float* s_p,
+                                             uint32_t* s_code, float* s_w, float* s_acc, uint32_t kv, uint32_t c) {
   using P = PairLut<D, B>;
-  constexpr int NW = D * B / 32;
-  constexpr int RS = NW + 1;         // staged row stride in words (odd: consecutive rows start on other banks)
+  constexpr int NW = ValuesLayout<D, B>::NW;
+  constexpr int RS = ValuesLayout<D, B>::RS;
   constexpr int PPL = D / 32;        // code pairs per lane
   constexpr int LB = PPL * 2 * B;    // code bits per lane
   static_assert(LB <= 64, "a lane's codes fit two words after alignment");
-  __shared__ float2 s_tab[P::N];
-  __shared__ uint32_t s_code[kBlock * RS + 4];
-  __shared__ __attribute__((aligned(16))) float s_w[kBlock * NQ];
-  __shared__ float s_acc[4 * NQ * D];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, r = lane >> 4, g = lane & 15;
-  const uint32_t kv = blockIdx.y, c = blockIdx.x;
   const uint64_t t0 = (uint64_t)c * a.chunk;
   const uint32_t n = (uint32_t)min((uint64_t)a.chunk, a.tokens - t0);
-  P::build(s_tab, a.vpolar != 0);
   const WsLayout L(a);
-  const float* pw = a.ws + L.p + ((uint64_t)kv * a.tokens + t0) * NQ;
+  const float* pw = P_LDS ? s_p : a.ws + L.p + ((uint64_t)kv * a.tokens + t0) * NQ;
   const int bit0 = g * LB, wlo = bit0 >> 5;
   const uint32_t sh = (uint32_t)(bit0 & 31);
 
@@ -479,6 +498,7 @@ __global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
       acc[h][e] += __shfl_xor(acc[h][e], 16);
       acc[h][e] += __shfl_xor(acc[h][e], 32);
     }
+  __syncthreads();  // staging reads are done (s_acc may alias s_code)
   if (r == 0) {
 #pragma unroll
     for (int h = 0; h < NQ; ++h)
@@ -492,6 +512,49 @@ __global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
     const float v = (s_acc[h * D + j] + s_acc[(NQ + h) * D + j]) + (s_acc[(2 * NQ + h) * D + j] + s_acc[(3 * NQ + h) * D + j]);
     A[(((uint64_t)kv * NQ + h) * a.chunks + c) * D + j] = v;
   }
+}
+
+// Workgroup (chunk, KV head), weights from the workspace.
+template <int D, int B, int NQ>
+__global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
+  using P = PairLut<D, B>;
+  __shared__ float2 s_tab[P::N];
+  __shared__ uint32_t s_code[ValuesLayout<D, B>::kCodeWords];
+  __shared__ __attribute__((aligned(16))) float s_w[kBlock * NQ];
+  __shared__ float s_acc[4 * NQ * D];
+  P::build(s_tab, a.vpolar != 0);
+  values_phase<D, B, NQ, false>(a, s_tab, nullptr, s_code, s_w, s_acc, blockIdx.y, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------------------------- scores + values
+// One workgroup per (chunk, KV head) for keys and values of the same bit width: the scores phase leaves the
+// chunk's weights p in LDS and the values phase reads them there, so p never goes through HBM and the call
+// has one launch fewer. Dynamic LDS: [chunk * NQ] weights, then the values staging (codes and weights), whose
+// space also holds the four waves' partial accumulators at the end.
+template <int D, int B, int NQ>
+struct FusedLds {
+  static constexpr int kStageBytes = ValuesLayout<D, B>::kCodeWords * 4 + kBlock * NQ * 4;
+  static constexpr int kAccBytes = 4 * NQ * D * 4;
+  static constexpr int kRegionBytes = kStageBytes > kAccBytes ? kStageBytes : kAccBytes;
+  static constexpr int kStaticBytes = PairLut<D, B>::N * 8 + 4 * NQ * 4;
+  static uint32_t dynamic_bytes(uint32_t chunk) { return chunk * NQ * 4u + (uint32_t)kRegionBytes; }
+};
+template <int D, int B, int NQ>
+__global__ __launch_bounds__(kBlock) void attn_chunk(AttnArgs a, const float* __restrict__ qp_all) {
+  using P = PairLut<D, B>;
+  __shared__ float2 s_tab[P::N];
+  __shared__ float s_red[4 * NQ];
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
+  float* s_s = s_dyn;                                       // a.chunk * NQ floats (a multiple of 16 bytes)
+  uint32_t* s_code = (uint32_t*)(s_dyn + (size_t)a.chunk * NQ);
+  float* s_w = (float*)(s_code + ValuesLayout<D, B>::kCodeWords);  // 16-byte aligned: kCodeWords % 4 == 0
+  static_assert(ValuesLayout<D, B>::kCodeWords % 4 == 0, "weights staging stays 16-byte aligned");
+  P::build(s_tab, a.kpolar != 0);
+  __syncthreads();
+  scores_phase<D, B, NQ, false>(a, qp_all, s_tab, s_s, s_red, blockIdx.y, blockIdx.x);
+  // the scores phase ended with a barrier after its last table read; the values phase begins with one
+  if (a.vpolar != a.kpolar) P::build(s_tab, a.vpolar != 0);
+  values_phase<D, B, NQ, true>(a, s_tab, s_s, s_code, s_w, (float*)s_code, blockIdx.y, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------------------------- combine
@@ -562,11 +625,32 @@ __global__ __launch_bounds__(kBlock) void attn_combine(AttnArgs a) {
   if (lane == 0 && a.lse) a.lse[(uint64_t)kv * a.nq + h] = (M + log2f(lsum)) * kLn2;
 }
 
+template <int NQ, int B>
+bool launch_fused(const AttnArgs& a, hipStream_t s) {
+  using F = FusedLds<PITCH_DIM, B, NQ>;
+  const uint32_t bytes = F::dynamic_bytes(a.chunk);
+  if (bytes + (uint32_t)F::kStaticBytes > 65536u) return false;  // stay within 64 KB of LDS per workgroup
+  hipLaunchKernelGGL((attn_chunk<PITCH_DIM, B, NQ>), dim3(a.chunks, a.kv_heads), dim3(kBlock), bytes, s, a,
+                     (const float*)a.ws);
+  return true;
+}
+
 template <int NQ>
 hipError_t launch_nq(const AttnArgs& a, hipStream_t s) {
   constexpr int D = PITCH_DIM;
   const dim3 grid(a.chunks, a.kv_heads);
   const float* qp = a.ws;
+  if (!a.k_ranges && a.kbits == a.vbits && PITCH_ATTN_FUSED) {
+    bool done = false;
+    switch (a.kbits) {
+#define PITCH_FUSED(B) \
+  case B: done = launch_fused<NQ, B>(a, s); break;
+      PITCH_FUSED(2) PITCH_FUSED(3) PITCH_FUSED(4) PITCH_FUSED(5) PITCH_FUSED(6) PITCH_FUSED(7) PITCH_FUSED(8)
+#undef PITCH_FUSED
+      default: return hipErrorInvalidValue;
+    }
+    if (done) return hipSuccess;
+  }
   if (a.k_ranges) {
     switch (a.kbits) {
 #define PITCH_SCORES_CHAN(B) \

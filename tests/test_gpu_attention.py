@@ -12,7 +12,9 @@ relative, so those cases use 1e-4.
 Cases cover every kernel instantiation family: d = 64 and 128; key and value bit widths 2..8 (pair tables for
 b <= 5, two-level tables above), both methods on either side, different seeds for K and V, query heads per KV
 head 1..8 (padded to 1, 2, 4, 8), one to three KV heads, token counts from 1 to 70,000 (one to many chunks,
-chunk lengths 256 / 512 / 1024), head-major and token-major caches, and end-to-end encoded caches.
+chunk lengths 256 / 512 / 1024), head-major and token-major caches, and end-to-end encoded caches. Equal key
+and value widths run the fused scores-and-values kernel (attn_chunk), including equal widths with different
+methods, where it rebuilds its table between the phases; unequal widths run the separate kernels.
 """
 import math
 
@@ -63,6 +65,8 @@ CASES = [
     ("polarQuant", "polarQuant", 6, 6, 64, 2, 1, 255),
     ("polarQuant", "polarQuant", 8, 8, 128, 7, 1, 200),
     ("turboQuant", "polarQuant", 4, 3, 128, 4, 1, 600),
+    ("turboQuant", "polarQuant", 4, 4, 128, 4, 1, 600),    # equal widths, other tables: the fused kernel rebuilds
+    ("polarQuant", "turboQuant", 3, 3, 64, 2, 2, 1300),
     ("polarQuant", "turboQuant", 5, 2, 64, 1, 1, 600),
     ("turboQuant", "turboQuant", 8, 2, 128, 4, 2, 2000),   # the reference's mixed (key, value) bits
     ("turboQuant", "turboQuant", 4, 2, 64, 4, 1, 1),
