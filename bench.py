@@ -6,7 +6,7 @@
 A step is one full-cache decode of the GPT-2-small-shaped value cache (32768 tokens x 12 heads x d=64,
 393,216 vectors, TurboQuant b=4, fp32 token-major) with codes, norms and the output already resident in
 HBM. Steps rotate over --sets independent buffer sets (default 8, ~0.9 GB) so the 256 MB Infinity Cache
-cannot serve them. value = algorithmic bytes per step / time per step, with algorithmic bytes
+cannot serve them. Every timed measurement follows at least W warm-up calls and at least 0.25 s of calls. value = algorithmic bytes per step / time per step, with algorithmic bytes
 n * (4d + codeStride + 4). One JSON line is printed; --extras adds the other BASELINE configs
 (bulk encode, append-encode latency, KIVI, d=128 TurboQuant/PolarQuant), float16/bfloat16 caches and
 decode-step attention over compressed caches under "extra", and --full adds config 5 (Llama-3-8B long
@@ -47,6 +47,9 @@ def kivi_bytes(n: int, d: int, b: int, G: int, heads: int = 1, elem: int = 4) ->
     return heads * (n * (elem * d + cs) + ((n + G - 1) // G) * 4 * d)
 
 
+WARMUP_S = 0.25  # minimum warm-up per timed measurement, as the reference's benchmarks (BenchmarkSuite.swift:150-185)
+
+
 class Timer:
     """HIP events on the stream the codec launches on (torch's current stream)."""
 
@@ -55,11 +58,18 @@ class Timer:
         self.stream = torch.cuda.current_stream()
 
     def time(self, fn, steps: int, warmup: int) -> float:
-        """Average milliseconds per call of fn(i) over `steps` calls after `warmup` calls."""
+        """Average milliseconds per call of fn(i) over `steps` calls, after at least `warmup` calls and at least
+        WARMUP_S seconds of calls: the GPU's clocks take milliseconds to ramp up, so a warm-up of a few short
+        calls under-reports sustained throughput by up to 20 %."""
         torch = self.torch
-        for i in range(warmup):
+        i, t0 = 0, time.perf_counter()
+        while i < warmup or time.perf_counter() - t0 < WARMUP_S:
             fn(i)
+            i += 1
+            if i % 64 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
+        warmup = i
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record(self.stream)

@@ -145,6 +145,18 @@ def main(src: str, dst: str) -> None:
                 info.append("{-1, 0, 0.0, 0.0}")
                 continue
             scale, off, ent = lut
+            # The staged-stage TurboQuant encoder compares in the bucket domain t = u * 2^m + off + 2^k + 2^(k-1)
+            # (k = 13 or 17, t in [2^k, 2^(k+1))) and keeps each entry's code in the low 8 mantissa bits of its
+            # mapped edge: the mapping must be exact and leave those bits zero.
+            for k in (13, 17):
+                magic = 2.0 ** k + 2.0 ** (k - 1) + off
+                for e_bits, c in ent:
+                    e = float(np.uint32(e_bits).view(np.float32))
+                    if np.isinf(e):
+                        continue
+                    E = np.float64(e * scale + magic)
+                    assert float(E) - magic == e * scale and 2.0 ** k <= E < 2.0 ** (k + 1), (d, b, k, e)
+                    assert int(E.view(np.uint64)) & 0xFF == 0, (d, b, k, e)
             info.append(f"{{{len(lut_words) // 2}, {len(ent)}, {scale.hex()}, {off.hex()}}}")
             for e_bits, c in ent:
                 lut_words.extend([e_bits, c])

@@ -375,6 +375,17 @@ __device__ __forceinline__ void store_elems(void* base, uint64_t i, const float 
   }
 }
 
+// store_words with non-temporal stores (streamed out, not kept in the caches).
+template <int N>
+__device__ __forceinline__ void store_words_nt(uint32_t* dst, const uint32_t (&w)[N]) {
+  int i = 0;
+#pragma unroll
+  for (; i + 4 <= N; i += 4) __builtin_nontemporal_store(u32x4{w[i], w[i + 1], w[i + 2], w[i + 3]}, (u32x4*)(dst + i));
+  if constexpr (N % 4 == 3) __builtin_nontemporal_store(u32x3{w[i], w[i + 1], w[i + 2]}, (u32x3*)(dst + i));
+  if constexpr (N % 4 == 2) __builtin_nontemporal_store(u32x2{w[i], w[i + 1]}, (u32x2*)(dst + i));
+  if constexpr (N % 4 == 1) __builtin_nontemporal_store(w[i], dst + i);
+}
+
 template <int N>
 __device__ __forceinline__ void store_words(uint32_t* dst, const uint32_t (&w)[N]) {
   int i = 0;

@@ -11,6 +11,8 @@
 // rotated coordinates agree with the float64 specification to a few ulps (PolarQuant: bit for bit, with
 // correctly rounded divisions) and codes can differ only for values within ~1e-15 of a decision edge. The
 // decoders run in float32 (relative L2 error ~1e-7 against the float64 specification).
+#include <cstddef>
+
 #include "pitch_device.h"
 
 #ifndef PITCH_DIM
@@ -261,6 +263,131 @@ struct TqQuant {
   template <int N>
   __device__ static void codes(const Smem& sm, const double (&x)[N], double us, uint32_t (&out)[N]) {
     for_codes(sm, x, us, [&](int e, uint32_t cd) { out[e] = cd; });
+  }
+};
+
+// TurboQuant quantiser with 8-byte bucket-table entries, for the staged-stage encoder. The bucket domain is
+// t = u * 2^m + off + 2^k + 2^(k-1) in [2^k, 2^(k+1)) with k = 20 - log2(R), R the bytes per table row, so
+// bits 20 - k .. 19 of t's high word hold the bucket index plus 2^(k-1) and masking them gives the row's byte
+// offset directly. An entry is one float64: the bucket's edge E_j mapped to that domain (exact; gen_tables.py
+// checks that its low 8 mantissa bits are zero) with c_j stored in those 8 bits, or, past the last edge, the
+// largest such value below 2^(k+1). code = c_j + [t > E'_j] comes out of one compare and one add with carry
+// of the entry's low word; its bits above B are cleared by the packing. E'_j exceeds E_j by c_j ulps
+// (2^-31 bucket units at most), which moves the decision by less than 2^-36 in u, far inside the
+// near-boundary band. Small tables are replicated once per lane of a 16-lane LDS access phase (row = 16
+// copies, R = 128 bytes), so the random lookups of a wave never conflict on a bank; larger ones have one copy
+// (R = 8).
+#ifndef PITCH_LUT8_REP_MAX
+#define PITCH_LUT8_REP_MAX 20480  // largest replicated table in bytes
+#endif
+// (a & m) | b in one v_and_or_b32 (the compiler otherwise splits it into an and and an add).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(b));
+  return r;
+}
+
+template <int D, int B>
+struct TqLut8 {
+  static constexpr int L = 1 << B;
+  static constexpr PitchLutInfo LI = pitch_lut_info(ilog2(D), B);
+  static constexpr bool kLut = LI.offset >= 0;
+  static constexpr int N = kLut ? LI.entries : 1;
+  static constexpr int REP = (kLut && N * 128 <= PITCH_LUT8_REP_MAX) ? 16 : 1;
+  static constexpr int R = 8 * REP;                     // bytes per row
+  static constexpr int K = 20 - ilog2(R);               // t in [2^K, 2^(K+1))
+  static constexpr double kMagic = double(1 << K) + double(1 << (K - 1)) + LI.off;
+  static constexpr int kIdxBits = kLut ? ilog2(2 * N - 1) : 1;  // 2^kIdxBits >= N
+  static constexpr uint32_t kHiLo = (uint32_t)(1023 + K) << 20 | 0x80000u;  // high word of 2^K + 2^(K-1)
+  static constexpr uint32_t kHiHi = kHiLo + (uint32_t)R * (uint32_t)(N - 1) + (uint32_t)(R - 1);
+  static constexpr uint32_t kMask = ((1u << kIdxBits) - 1u) * (uint32_t)R;
+  static constexpr uint64_t kTop = ((uint64_t)(1023 + K) << 52) | 0xFFFFFFFFFFF00ull;  // below 2^(K+1), low byte 0
+  static_assert(!kLut || (kIdxBits <= K - 1 && LI.scale + LI.off < double(1 << (K - 1))), "index in the high word");
+  static_assert(kLut || B >= 7, "every table of B <= 6 fits");
+
+  struct Smem {
+    uint64_t tab[kLut ? N * REP : 1];
+    double edge64[kLut ? 1 : L];
+  };
+
+  __device__ static void load(Smem& sm, int tid, int nthreads) {
+    if constexpr (kLut) {
+      for (int i = tid; i < N * REP; i += nthreads) {
+        const int j = i / REP;
+        const float e = __uint_as_float(pitch_lut_tab[2 * (LI.offset + j)]);
+        const uint32_t c = pitch_lut_tab[2 * (LI.offset + j) + 1];
+        const uint64_t bits = __builtin_isinf(e) ? kTop : (uint64_t)__double_as_longlong(__builtin_fma((double)e, LI.scale, kMagic));
+        sm.tab[i] = bits | c;
+      }
+    } else {
+      constexpr int off = pitch_codebook_offset(ilog2(D), B);
+      for (int i = tid; i < L; i += nthreads) sm.edge64[i] = (double)pitch_edge_tab[off + i];
+    }
+  }
+
+  // Applies f(e, raw) to x[0..NX) in order, with u = x * us; the low B bits of raw are the code of x[e].
+  // Lookups are issued in batches of QB (at most 15, what the LDS wait counter tracks) before any is used.
+  template <int QB, int NX, typename F>
+  __device__ static void for_codes(const Smem& sm, const double (&x)[NX], double us, int lane, F&& f) {
+    if constexpr (kLut) {
+      const double us_m = us * LI.scale;  // exact: LI.scale is a power of two
+      typedef __attribute__((address_space(3))) const uint64_t lds_u64;
+      typedef __attribute__((address_space(3))) const char lds_byte;
+      lds_byte* tab = (lds_byte*)(sm.tab);
+      const uint32_t loff = REP > 1 ? (uint32_t)(lane % REP) * 8u : 0u;
+      constexpr int kB = QB;
+#pragma unroll
+      for (int b0 = 0; b0 < NX; b0 += kB) {
+        double tt[kB];
+        uint64_t ee[kB];
+#pragma unroll
+        for (int i = 0; i < kB; ++i) {
+          if (b0 + i < NX) {
+            tt[i] = __builtin_fma(x[b0 + i], us_m, kMagic);
+            const uint32_t hi = (uint32_t)((uint64_t)__double_as_longlong(tt[i]) >> 32);
+            const uint32_t hc = min(max(hi, kHiLo), kHiHi);  // NaN and out-of-table u land on an end bucket
+            ee[i] = *(lds_u64*)(tab + and_or(hc, kMask, loff));
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kB; ++i)
+          if (b0 + i < NX) f(b0 + i, (uint32_t)ee[i] + (tt[i] > __longlong_as_double((long long)ee[i]) ? 1u : 0u));
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < NX; ++e) {
+        const double u = x[e] * us;
+        uint32_t cd = 0;
+#pragma unroll
+        for (int s = L / 2; s >= 1; s >>= 1) cd = (u > sm.edge64[cd + s - 1]) ? cd + s : cd;
+        f(e, cd);
+      }
+    }
+  }
+
+  // Codes of x[0..NX) packed into words as they are produced: code e at bits [e*B, e*B + B) of w. When B
+  // divides 32 each code is shifted in from the top of its word (v_alignbit), which also drops the raw
+  // value's bits above B; otherwise the code is masked and or-ed in.
+  template <int QB, int NX, int NWORDS>
+  __device__ static void codes_packed(const Smem& sm, const double (&x)[NX], double us, int lane,
+                                      uint32_t (&w)[NWORDS]) {
+    if constexpr (32 % B == 0) {
+#pragma unroll
+      for (int i = 0; i < NWORDS; ++i) w[i] = 0u;
+      for_codes<QB>(sm, x, us, lane, [&](int e, uint32_t raw) {
+        const int wi = (e * B) >> 5;
+        w[wi] = __builtin_amdgcn_alignbit(raw, w[wi], B);
+      });
+    } else {
+#pragma unroll
+      for (int i = 0; i < NWORDS; ++i) w[i] = 0u;
+      for_codes<QB>(sm, x, us, lane, [&](int e, uint32_t raw) {
+        const uint32_t cd = raw & (uint32_t)(L - 1);
+        const int pos = e * B, wi = pos >> 5, sh = pos & 31;
+        w[wi] |= cd << sh;
+        if (sh + B > 32) w[wi + 1] |= cd >> (32 - sh);
+      });
+    }
   }
 };
 
@@ -870,6 +997,352 @@ void tq_encode_lpv(VecArgs p) {
   }
 }
 
+// ----------------------------------------------------------------------------------------------------
+// TurboQuant encoder for float32 vectors at D = 64 and 128 with the transform's top stages applied at
+// staging. A compute team of T lanes holds one vector, E = D / T contiguous coordinates per lane
+// (c = t * E + e), so every stage left after staging runs inside a lane and each lane's codes are whole,
+// contiguous code words (or, for E * B not a multiple of 32, words shared with one neighbour). The stages on
+// the team bits (coordinate bits log2 E .. log2 D - 1) run while staging: staging lane p of a vector loads the
+// T chunks at coordinates 4p + E * i (i < T), applies the rotation signs, widens to float64, applies those
+// log2 T butterfly stages and writes the results to the LDS rows of the compute lanes that own them. The SL =
+// E / 4 staging lanes of a vector read 4E contiguous bytes per load instruction, so the loads stay coalesced,
+// and no cross-lane butterfly (two DPP moves and an add per float64 coordinate) is left.
+template <int D, int T>
+struct Hs {
+  static constexpr int E = D / T;        // coordinates per compute lane
+  static constexpr int V = 64 / T;       // vectors per wave iteration
+  static constexpr int SL = E / 4;       // staging lanes per vector
+  static constexpr int VPS = 64 / SL;    // vectors per load set (one load instruction per chunk i)
+  static constexpr int NSET = V / VPS;   // load sets per wave iteration
+  static constexpr int QPL = T * NSET;   // 16-byte chunks each lane loads per iteration
+  // The sets are staged one at a time through LDS rows for VPS vectors: the compute lanes of set s read
+  // their rows before set s + 1 is staged. Rows are padded so that the 8 lanes of each 128-byte access phase
+  // hit distinct banks, for the staging writes (consecutive positions 4 pp, and vectors) and for the compute
+  // reads (team lanes, and vectors): elements 16 apart are 36 banks apart when E > 16 (eoff), lane rows are
+  // 8 banks apart (LS = 4 mod 16) and vectors 4 banks apart modulo 8 (VS = 2 mod 4).
+  static constexpr int LS = E > 16 ? E + 4 : E + 4;  // float64 per compute lane row (E = 16: 20, E = 32: 36)
+  static constexpr int VS = T * LS + 2;              // float64 per vector
+  static constexpr int ROWS = VPS * VS;              // float64 of LDS rows per wave
+  static constexpr int WAVES = kBlock / 64;  // independent waves per workgroup (they share the bucket table)
+  __host__ __device__ static constexpr int eoff(int e) { return E > 16 ? e + 2 * (e / 16) : e; }
+  static_assert(T >= 2 && E % 4 == 0 && 64 % SL == 0 && V % VPS == 0, "staging geometry");
+  static_assert(eoff(E - 1) < LS && (2 * LS) % 32 == 8 && VS % 4 == 2, "row padding");
+};
+
+#ifndef PITCH_HS_T64
+#define PITCH_HS_T64 4  // team lanes per vector of the staged-stage TurboQuant encoder at D = 64 (2 or 4)
+#endif
+
+template <int D>
+constexpr int hs_team() { return D == 64 ? PITCH_HS_T64 : 4; }
+
+#ifndef PITCH_HS_NT
+#define PITCH_HS_NT 1  // the staged-stage encoder streams its input in and its codes and scales out non-temporally
+#endif
+
+// One 16-byte load of the staged-stage encoder's input. Non-temporal: an encode reads each input byte once,
+// and keeping the stream out of the caches lets the few writes interleave with it better (measured: +5 % at
+// the same instruction count).
+__device__ __forceinline__ u32x4 hs_load(const float* p) {
+  if constexpr (PITCH_HS_NT) return __builtin_nontemporal_load((const u32x4*)p);
+  else return *(const u32x4*)p;
+}
+
+// Coalesced loads of a wave's block of V vectors: set s, chunk i of lane l is vector base + s * VPS + l / SL
+// at coordinates 4 * (l % SL) + E * i (vectors past the end re-read the last one).
+template <int D, int T>
+__device__ __forceinline__ void hs_fetch(const float* in, uint64_t base, uint64_t count, int lane,
+                                        u32x4 (&pf)[Hs<D, T>::QPL]) {
+  using H = Hs<D, T>;
+  const int vl = lane / H::SL, pp = lane % H::SL;
+  if (base + H::V <= count) {
+    const float* blk = in + (base + vl) * D + 4 * pp;
+#pragma unroll
+    for (int s = 0; s < H::NSET; ++s)
+#pragma unroll
+      for (int i = 0; i < T; ++i) pf[s * T + i] = hs_load(blk + (uint64_t)s * H::VPS * D + H::E * i);
+  } else {
+#pragma unroll
+    for (int s = 0; s < H::NSET; ++s) {
+      const uint64_t v = base + s * H::VPS + vl;
+      const float* row = in + (v < count ? v : count - 1) * D + 4 * pp;
+#pragma unroll
+      for (int i = 0; i < T; ++i) pf[s * T + i] = hs_load(row + H::E * i);
+    }
+  }
+}
+
+// sqrt(n2) rounded as the library's float64 sqrt and h ~ 1 / (2 sqrt(n2)) to about an ulp, for n2 > 0 in
+// the range of sums of squares of finite float32 values (2^-300 .. 2^264), which needs none of the range
+// scaling of the general routine: the reciprocal square root estimate refined by one Goldschmidt step,
+// two Newton corrections of the root and one more step of h.
+__device__ __forceinline__ double sqrt_and_half_rsqrt(double n2, double& h) {
+  const double y = __builtin_amdgcn_rsq(n2);
+  double g = n2 * y;
+  h = 0.5 * y;
+  double r = __builtin_fma(-h, g, 0.5);
+  g = __builtin_fma(g, r, g);
+  h = __builtin_fma(h, r, h);
+  double dd = __builtin_fma(-g, g, n2);
+  g = __builtin_fma(dd, h, g);
+  dd = __builtin_fma(-g, g, n2);
+  g = __builtin_fma(dd, h, g);
+  r = __builtin_fma(-h, g, 0.5);
+  h = __builtin_fma(h, r, h);
+  return g;
+}
+
+#ifndef PITCH_HS_PFD64
+#define PITCH_HS_PFD64 1  // blocks of loads the staged-stage encoder keeps in flight per wave at D = 64 (1, 2)
+#endif
+#ifndef PITCH_HS_PFD128
+#define PITCH_HS_PFD128 1  // the same at D = 128
+#endif
+// (one block where the key-bias variant's or the shared-word packing's extra registers leave no room for two)
+template <int D, int B, bool KBIAS>
+constexpr int hs_pfd() { return (KBIAS || B == 5 || B == 7) ? 1 : (D == 64 ? PITCH_HS_PFD64 : PITCH_HS_PFD128); }
+
+// f, negated in the lanes whose bit of the wave-uniform mask is set: one v_cndmask with a negated operand and
+// the mask as its lane-select scalar register pair.
+__device__ __forceinline__ float neg_lanes(float f, uint64_t lanes) {
+  float r;
+  asm("v_cndmask_b32_e64 %0, %1, -%1, %2" : "=v"(r) : "v"(f), "s"(lanes));
+  return r;
+}
+
+// Lane masks of the rotation signs for the staged-stage encoder (host side): bit l of mask i * 4 + k is set when
+// coordinate 4 (l % SL) + E i + k, the one lane l stages as element k of chunk i, has sign -1.
+static_assert(offsetof(VecArgs, lane_flips) % 8 == 0, "lane_flips is read as 64-bit lane masks");
+template <int D, int T>
+void fill_hs_flips(uint32_t seed, uint32_t* out) {
+  using H = Hs<D, T>;
+  static_assert(T * 4 * 2 <= 32, "masks fit in VecArgs::lane_flips");
+  thread_local uint32_t cached_seed = 0;
+  thread_local bool have = false;
+  thread_local uint32_t cached[32];
+  if (!have || cached_seed != seed) {
+    for (int j = 0; j < 32; ++j) cached[j] = 0u;
+    for (int i = 0; i < T; ++i)
+      for (int k = 0; k < 4; ++k)
+        for (int l = 0; l < 64; ++l)
+          if (sign_is_negative(seed, (uint32_t)(4 * (l % H::SL) + H::E * i + k)))
+            cached[2 * (i * 4 + k) + (l >> 5)] |= 1u << (l & 31);
+    cached_seed = seed;
+    have = true;
+  }
+  for (int j = 0; j < 32; ++j) out[j] = cached[j];
+}
+
+// Staging of one block (see Hs), one load set at a time: signs, float64, the butterfly stages on the team
+// bits, the LDS rows of the set's compute lanes, which then read their coordinates into x. neg[i * 4 + k] is
+// the lane mask of the sign of element k of chunk i (fill_hs_flips).
+template <int D, int T, bool KBIAS>
+__device__ __forceinline__ void hs_stage(const VecArgs& p, const u32x4 (&pf)[Hs<D, T>::QPL], uint64_t base, int lane,
+                                         const uint64_t* neg, double* sx, double (&x)[Hs<D, T>::E]) {
+  using H = Hs<D, T>;
+  constexpr int E = H::E;
+  const int pp = lane % H::SL, vs = lane / H::SL;
+  const int t = lane % T, vw = lane / T;
+#pragma unroll
+  for (int s = 0; s < H::NSET; ++s) {
+    double y[T][4];
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      const u32x4 c = pf[s * T + i];
+      float f[4] = {__uint_as_float(c.x), __uint_as_float(c.y), __uint_as_float(c.z), __uint_as_float(c.w)};
+      if constexpr (KBIAS) {  // key-bias removal: encode x - o (mechanism_eval.py:113-116)
+        float o[4];
+        const uint64_t v = base + s * H::VPS + vs;
+        key_bias_offset<D, 4>(p, v < p.count ? v : p.count - 1, 4 * pp + E * i, o);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f[k] = f[k] - o[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) y[i][k] = (double)neg_lanes(f[k], neg[i * 4 + k]);
+    }
+#pragma unroll
+    for (int h = 1; h < T; h <<= 1)
+#pragma unroll
+      for (int i = 0; i < T; ++i)
+        if (!(i & h))
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const double a = y[i][k], b = y[i | h][k];
+            y[i][k] = a + b;
+            y[i | h][k] = a - b;
+          }
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      double* row = sx + vs * H::VS + i * H::LS + H::eoff(4 * pp);
+      *(double2*)row = double2{y[i][0], y[i][1]};
+      *(double2*)(row + 2) = double2{y[i][2], y[i][3]};
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (H::NSET == 1 || vw / H::VPS == s) {
+      const double* row = sx + (vw % H::VPS) * H::VS + t * H::LS;
+#pragma unroll
+      for (int k = 0; k < E / 2; ++k) {
+        const double2 v2 = *(const double2*)(row + H::eoff(2 * k));
+        x[2 * k] = v2.x;
+        x[2 * k + 1] = v2.y;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+// Compute phase of one block: the in-lane stages, the norm, quantisation and the stores.
+template <int D, int T, int B>
+__device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLut8<D, B>::Smem& sq, uint64_t base,
+                                           int lane, double* sx, double (&x)[Hs<D, T>::E]) {
+  using H = Hs<D, T>;
+  using Q = TqLut8<D, B>;
+  constexpr int E = H::E, V = H::V;
+  constexpr int NW = (D * B + 31) / 32;            // code words per vector
+  constexpr bool kWhole = (E * B) % 32 == 0;       // each lane owns whole code words
+  constexpr int NWL = (E * B + 31) / 32;           // code words a lane packs (first one shared when !kWhole)
+  static_assert(kWhole || (T == 4 && E == 16 && B % 2 == 1), "shared code words: D = 64, T = 4, odd B");
+  const int t = lane % T, vw = lane / T;
+  // ||x||^2 = sum of squares after the team-bit stages / T (each stage doubles it exactly)
+  double ss[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int e = 0; e < E; ++e) ss[e & 3] = __builtin_fma(x[e], x[e], ss[e & 3]);
+  double n2 = (ss[0] + ss[1]) + (ss[2] + ss[3]);
+  n2 = team_reduce<T>(n2, [](double a, double b) { return a + b; }) * (1.0 / T);
+  fwht_contig<E, 1, double>(x, 0);
+  double h;
+  const double g = sqrt_and_half_rsqrt(n2, h);
+  const bool zero = !(n2 > 0.0);
+  const float nrm = zero ? 0.f : (float)g;
+  // u = H(s * x) / (||x|| sqrt(d)) (pitch_reference.py:96-98); a zero vector is divided by 1
+  const double us = zero ? DimConst<D>::kInvSqrt : (2.0 * h) * DimConst<D>::kInvSqrt;
+
+  uint32_t w[NWL];
+  Q::template codes_packed<(E > 16 ? 8 : PITCH_QBATCH)>(sq, x, us, lane, w);
+  // Every store is unconditional, so the compiler can count the vector-memory operations of an iteration and
+  // wait for the next block's loads without waiting for these stores (gfx9 counts loads and stores together,
+  // in order). A vector past the end was loaded from the last vector (hs_fetch), so its codes and scale equal
+  // the last vector's and are written to that vector's place: the same bytes to the same address.
+  const uint64_t vst = base + vw < p.count ? base + vw : p.count - 1;
+  // the T lanes of a team write the same scale
+  if constexpr (PITCH_HS_NT) __builtin_nontemporal_store(nrm, p.scales_out + vst);
+  else p.scales_out[vst] = nrm;
+  if constexpr (kWhole) {
+    // lane (vw, t) owns words t * NWL .. of its vector: the wave's stores are one contiguous run
+    if constexpr (PITCH_HS_NT) store_words_nt(p.codes_out + vst * NW + t * NWL, w);
+    else store_words(p.codes_out + vst * NW + t * NWL, w);
+  } else {
+    // E * B = 16 B bits per lane: odd lanes start half-way into a word. Shift their bits up by 16, then
+    // the even lane of each pair takes the odd lane's first (shared) word into its last one.
+    if (t & 1) {
+#pragma unroll
+      for (int j = NWL - 1; j > 0; --j) w[j] = __builtin_amdgcn_alignbit(w[j], w[j - 1], 16);
+      w[0] <<= 16;
+    }
+    const uint32_t shared = xchg_u32<1>(w[0]);
+    if (!(t & 1)) w[NWL - 1] |= shared;
+    __builtin_amdgcn_wave_barrier();
+    uint32_t* sc = (uint32_t*)sx;  // the LDS rows were read into registers while staging
+    static_assert(V * NW <= 2 * H::ROWS, "codes fit in the rows");
+    const int w0 = (E * B * t) / 32;
+#pragma unroll
+    for (int j = 0; j < NWL; ++j)
+      if (j > 0 || !(t & 1)) sc[vw * NW + w0 + j] = w[j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // V * NW / CW chunks of CW words, contiguous; lanes past the last chunk repeat it, and chunks of vectors
+    // past the end go to the last vector's place (their words are the same)
+    constexpr int CW = NW % 4 == 0 ? 4 : (NW % 2 == 0 ? 2 : 1);
+    constexpr int NCH = V * NW / CW, CPV = NW / CW;
+#pragma unroll
+    for (int i = 0; i < (NCH + 63) / 64; ++i) {
+      const int q = min(lane + 64 * i, NCH - 1);
+      const int vq = q / CPV;
+      const uint64_t vd = base + vq < p.count ? base + vq : p.count - 1;
+      uint32_t* dst = p.codes_out + vd * NW + CW * (q - vq * CPV);
+      if constexpr (CW == 4) store_v((u32x4*)dst, *(const u32x4*)(sc + 4 * q), PITCH_HS_NT);
+      else if constexpr (CW == 2) store_v((u32x2*)dst, *(const u32x2*)(sc + 2 * q), PITCH_HS_NT);
+      else store_v(dst, sc[q], PITCH_HS_NT);
+    }
+  }
+}
+
+// Waves per SIMD the staged-stage encoder's registers must allow (its LDS allows 3; the key-bias variant's
+// extra registers would spill at 3).
+#ifndef PITCH_HS_WAVES64
+#define PITCH_HS_WAVES64 3
+#endif
+#ifndef PITCH_HS_WAVES128
+#define PITCH_HS_WAVES128 3
+#endif
+template <int D, bool KBIAS>
+constexpr int hs_waves() { return KBIAS ? 2 : (D == 64 ? PITCH_HS_WAVES64 : PITCH_HS_WAVES128); }
+
+template <int D, int B, bool KBIAS>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hs_waves<D, KBIAS>())))
+void tq_encode_hs(VecArgs p) {
+  constexpr int T = hs_team<D>();
+  using H = Hs<D, T>;
+  constexpr int E = H::E, V = H::V;
+  using Q = TqLut8<D, B>;
+  __shared__ __attribute__((aligned(16))) double s_x[H::WAVES][H::ROWS];
+  __shared__ __attribute__((aligned(16))) typename Q::Smem s_q;
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const float* in = (const float*)p.in;
+  const uint64_t stride = (uint64_t)gridDim.x * H::WAVES * V;
+  uint64_t base = ((uint64_t)blockIdx.x * H::WAVES + wave) * V;
+  // Software pipeline with PFD blocks of loads in flight. The loop is rotated so that each block's loads are
+  // waited for in straight-line code after exactly the stores of the block before (two or so operations):
+  // an iteration issues the loads of block k + PFD, computes and stores block k, then stages block k + 1.
+  // The waves' first loads are issued after the table set-up, so no other load is pending at that point.
+  constexpr int PFD = hs_pfd<D, B, KBIAS>();
+  static_assert(PFD == 1 || PFD == 2, "prefetch depth");
+  Q::load(s_q, threadIdx.x, 64 * H::WAVES);
+  const uint64_t* neg = (const uint64_t*)p.lane_flips;  // fill_hs_flips; kernel arguments, read as scalars
+  __syncthreads();
+  if (base >= p.count) return;
+  double* sx = s_x[wave];
+  u32x4 pfa[H::QPL];
+  u32x4 pfb[PFD > 1 ? H::QPL : 1];
+  double x[E];
+  // every fetch is unconditional, like the stores: a block past the end re-reads the last vector (a cache hit)
+  hs_fetch<D, T>(in, base, p.count, lane, pfa);
+  if constexpr (PFD > 1) hs_fetch<D, T>(in, base + stride, p.count, lane, pfb);
+  hs_stage<D, T, KBIAS>(p, pfa, base, lane, neg, sx, x);
+  auto step = [&](u32x4 (&refill)[H::QPL], u32x4 (&next)[H::QPL]) {
+    hs_fetch<D, T>(in, base + (uint64_t)PFD * stride, p.count, lane, refill);
+    __builtin_amdgcn_sched_barrier(0);  // the loads go out before the compute, not interleaved into it
+    hs_compute<D, T, B>(p, s_q, base, lane, sx, x);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the next block's staging waits for its loads: keep all of it after the compute
+    __builtin_amdgcn_sched_barrier(0);
+    base += stride;
+    hs_stage<D, T, KBIAS>(p, next, base, lane, neg, sx, x);  // past the end: staged, never computed
+  };
+  if constexpr (PFD > 1) {
+    while (true) {
+      step(pfa, pfb);
+      if (base >= p.count) break;
+      step(pfb, pfa);
+      if (base >= p.count) break;
+    }
+  } else {
+    while (base < p.count) step(pfa, pfa);
+  }
+}
+
+#ifndef PITCH_HS_ENCODER
+#define PITCH_HS_ENCODER 1  // 1: float32 TurboQuant encode at D = 64 / 128 uses tq_encode_hs
+#endif
+
 template <int D>
 constexpr bool use_lpv_encoder() { return D >= 8 && D <= 128; }
 
@@ -877,6 +1350,17 @@ template <int D, int B, bool POLAR, int IO, bool KBIAS>
 hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   using G = Geom<D>;
   VecArgs a = args;
+  if constexpr (!POLAR && IO == 0 && PITCH_HS_ENCODER && (D == 64 || D == 128)) {
+    if (encode) {
+      using H = Hs<D, hs_team<D>()>;
+      fill_hs_flips<D, hs_team<D>()>(a.seed, a.lane_flips);
+      const uint64_t need = (a.count + H::WAVES * H::V - 1) / (H::WAVES * H::V);
+      const void* k = (const void*)&tq_encode_hs<D, B, KBIAS>;
+      const uint64_t grid = persistent_grid(k, need, 64 * H::WAVES);
+      hipLaunchKernelGGL((tq_encode_hs<D, B, KBIAS>), dim3((uint32_t)grid), dim3(64 * H::WAVES), 0, s, a);
+      return hipGetLastError();
+    }
+  }
   if constexpr (!POLAR && use_lpv_encoder<D>()) {
     if (encode) {
       constexpr int V = Lpv<D, IO>::V;
