@@ -197,6 +197,9 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
 #endif
 constexpr int kSlab = 64;        // channels per wave of the decoder
 constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
+#ifndef PITCH_KIVI_NT
+#define PITCH_KIVI_NT 1  // the wave encoder streams keys in and codes and ranges out non-temporally
+#endif
 #ifndef PITCH_KIVI_SLAB
 #define PITCH_KIVI_SLAB 0        // encoder slab width: 0 = chosen per call, else 32 or 64 channels
 #endif
@@ -232,7 +235,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
     for (int i = 0; i < TPL; ++i) {
       const uint32_t tk = r + (uint32_t)RPI * i;
       float v[4];
-      load_elems<IO, 4>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
+      if constexpr (PITCH_KIVI_NT) load4_nt<IO>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
+      else load_elems<IO, 4>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
       x[i] = make_float4(v[0], v[1], v[2], v[3]);
     }
     float4 lo = x[0], hi = x[0];
@@ -267,9 +271,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
     }
     if (r == 0 && cact) {
       uint16_t* rg = p.ranges_out + (uint64_t)g * 2u * dim + ch0 + 4u * c;
-      *(u32x2*)rg = u32x2{(uint32_t)l16[0] | ((uint32_t)l16[1] << 16), (uint32_t)l16[2] | ((uint32_t)l16[3] << 16)};
-      *(u32x2*)(rg + dim) =
-          u32x2{(uint32_t)h16[0] | ((uint32_t)h16[1] << 16), (uint32_t)h16[2] | ((uint32_t)h16[3] << 16)};
+      store_v((u32x2*)rg, u32x2{(uint32_t)l16[0] | ((uint32_t)l16[1] << 16), (uint32_t)l16[2] | ((uint32_t)l16[3] << 16)},
+              PITCH_KIVI_NT);
+      store_v((u32x2*)(rg + dim),
+              u32x2{(uint32_t)h16[0] | ((uint32_t)h16[1] << 16), (uint32_t)h16[2] | ((uint32_t)h16[3] << 16)},
+              PITCH_KIVI_NT);
     }
     // codes clip(floor((x - lo) / step + 0.5), 0, 2^B - 1) (pitch_reference.py:157-158), one byte each in LDS.
     // Rows past the group's end and channels past the slab's end are quantised and staged too (their slots
@@ -303,7 +309,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
         const uint32_t bytes[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         uint32_t w[B];
         pack32<B>(bytes, w);
-        store_words<B>(dst + (uint64_t)tok * p.nwords + gi * B, w);
+        if constexpr (PITCH_KIVI_NT) store_words_nt<B>(dst + (uint64_t)tok * p.nwords + gi * B, w);
+        else store_words<B>(dst + (uint64_t)tok * p.nwords + gi * B, w);
       }
     } else {
       // last, partial slab of a row whose width is not a multiple of 32: it ends the row

@@ -340,6 +340,19 @@ __device__ __forceinline__ void load_elems(const void* base, uint64_t i, float (
   }
 }
 
+// load_elems of 4 elements with a non-temporal load (an input streamed through once).
+template <int IO>
+__device__ __forceinline__ void load4_nt(const void* base, uint64_t i, float (&f)[4]) {
+  if constexpr (IO == 0) {
+    const f32x4 a = __builtin_nontemporal_load((const f32x4*)((const float*)base + i));
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  } else {
+    const u32x2 w = __builtin_nontemporal_load((const u32x2*)((const uint16_t*)base + i));
+    widen2<IO>(w.x, f[0], f[1]);
+    widen2<IO>(w.y, f[2], f[3]);
+  }
+}
+
 // Stores f[0, N) at elements [i, i + N) of an IO-typed array in one access, non-temporal when NT.
 template <typename V>
 __device__ __forceinline__ void store_v(V* p, V v, bool nt) {

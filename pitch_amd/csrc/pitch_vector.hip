@@ -396,6 +396,9 @@ struct TqLut8 {
 #endif
 
 // ----------------------------------------------------------------------------------------------------
+#ifndef PITCH_VEC_ENC_NT
+#define PITCH_VEC_ENC_NT 1  // the team encoder reads its input with non-temporal loads
+#endif
 #ifndef PITCH_POLAR_WAVES
 #define PITCH_POLAR_WAVES 1  // minimum waves per SIMD requested for the team encoder (caps its VGPRs)
 #endif
@@ -435,8 +438,12 @@ __global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode(VecArgs 
     // load every chunk before converting (all loads in flight together), then apply the signs (exact)
     float f[G::E];
 #pragma unroll
-    for (int k = 0; k < G::CH; ++k)
-      load_elems<IO, G::W>(p.in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
+    for (int k = 0; k < G::CH; ++k) {
+      if constexpr (PITCH_VEC_ENC_NT && G::W == 4)  // read-once input: streamed past the caches
+        load4_nt<IO>(p.in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
+      else
+        load_elems<IO, G::W>(p.in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
+    }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (KBIAS) {  // key-bias removal: encode x - o (mechanism_eval.py:113-116)
 #pragma unroll
@@ -998,8 +1005,8 @@ void tq_encode_lpv(VecArgs p) {
 }
 
 // ----------------------------------------------------------------------------------------------------
-// TurboQuant encoder for float32 vectors at D = 64 and 128 with the transform's top stages applied at
-// staging. A compute team of T lanes holds one vector, E = D / T contiguous coordinates per lane
+// Per-vector encoder (TurboQuant and PolarQuant) for float32 vectors at D = 64 and 128 with the transform's
+// top stages applied at staging. A compute team of T lanes holds one vector, E = D / T contiguous coordinates per lane
 // (c = t * E + e), so every stage left after staging runs inside a lane and each lane's codes are whole,
 // contiguous code words (or, for E * B not a multiple of 32, words shared with one neighbour). The stages on
 // the team bits (coordinate bits log2 E .. log2 D - 1) run while staging: staging lane p of a vector loads the
@@ -1195,8 +1202,62 @@ __device__ __forceinline__ void hs_stage(const VecArgs& p, const u32x4 (&pf)[Hs<
   }
 }
 
-// Compute phase of one block: the in-lane stages, the norm, quantisation and the stores.
-template <int D, int T, int B>
+// PolarQuant codes of the lane's E contiguous coordinates after the in-lane stages (pitch_reference.py:109-121):
+// pairs (y_2p, y_2p+1) -> radius code floor(r / rmax * (2^B - 1) + 0.5) clipped and angle code
+// floor(theta / 2 pi * 2^B + 0.5) mod 2^B, rmax = the largest radius of the vector (team-reduced). The codes
+// depend only on the directions and on the radii relative to rmax, which the division by sqrt(d) of rotate()
+// leaves unchanged (up to float64 rounding, far inside the near-boundary band): the pairs come from the
+// unnormalised transform and only rmax is scaled. Each pair is decided in float32 on the unscaled pair (the
+// angle is scale-invariant; the radius is multiplied by (2^B - 1) / rmax) when its t values are at least
+// kPolarGuard from an integer; otherwise, for a pair at the origin, or for a vector whose rmax lies outside
+// [1e-30, 1e30] (where the unscaled float32 pair could lose precision), the float64 path in the reference's
+// order decides. A NaN or an overflow in the float32 path fails the guard as well.
+template <int D, int T, int B, int NWL>
+__device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w)[NWL]) {
+  constexpr int E = Hs<D, T>::E, NP = E / 2, L = 1 << B;
+  fwht_contig<E, 1, double>(x, 0);
+  double m = 0.0;
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const double r2 = __builtin_fma(x[2 * q], x[2 * q], x[2 * q + 1] * x[2 * q + 1]);
+    m = r2 > m ? r2 : m;
+  }
+  m = team_reduce<T>(m, [](double a, double b) { return a > b ? a : b; });
+  const double rmax = __builtin_sqrt(m);  // = the largest radius: sqrt is monotone
+  const double safe = rmax > 0.0 ? rmax : 1.0;
+  const bool inrange = rmax > 1e-30 && rmax < 1e30;
+  const float sr = (float)(double(L - 1) / safe);
+#pragma unroll
+  for (int i = 0; i < NWL; ++i) w[i] = 0u;
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const float af = (float)x[2 * q], cf = (float)x[2 * q + 1];
+    const float rf = __builtin_amdgcn_sqrtf(__builtin_fmaf(af, af, cf * cf));
+    bool ok = inrange && (af != 0.f || cf != 0.f);
+    const float kr = guarded_floor(__builtin_fmaf(rf, sr, 0.5f), ok);
+    const float ka = guarded_floor(__builtin_fmaf(angle_turns<B>(cf, af), float(L), 0.5f), ok);
+    uint32_t cr = (uint32_t)__builtin_fminf(kr, float(L - 1));
+    uint32_t ca = (uint32_t)ka & (uint32_t)(L - 1);
+    if (!ok) {  // rare: one shared out-of-line copy
+      const double a = x[2 * q], c = x[2 * q + 1];
+      const uint2 cc = polar_codes_exact<B>(a, c, __builtin_fma(a, a, c * c), safe);
+      cr = cc.x;
+      ca = cc.y;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t cd = h ? ca : cr;
+      const int pos = (2 * q + h) * B, wi = pos >> 5, sh = pos & 31;
+      w[wi] |= cd << sh;
+      if (sh + B > 32) w[wi + 1] |= cd >> (32 - sh);
+    }
+  }
+  return (float)div_sqrt_d<D>(rmax);
+}
+
+// Compute phase of one block: the in-lane stages, the quantisation (TurboQuant: norm and bucket table;
+// PolarQuant: hs_polar_codes) and the stores.
+template <int D, int T, int B, bool POLAR>
 __device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLut8<D, B>::Smem& sq, uint64_t base,
                                            int lane, double* sx, double (&x)[Hs<D, T>::E]) {
   using H = Hs<D, T>;
@@ -1207,22 +1268,26 @@ __device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLu
   constexpr int NWL = (E * B + 31) / 32;           // code words a lane packs (first one shared when !kWhole)
   static_assert(kWhole || (T == 4 && E == 16 && B % 2 == 1), "shared code words: D = 64, T = 4, odd B");
   const int t = lane % T, vw = lane / T;
-  // ||x||^2 = sum of squares after the team-bit stages / T (each stage doubles it exactly)
-  double ss[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-  for (int e = 0; e < E; ++e) ss[e & 3] = __builtin_fma(x[e], x[e], ss[e & 3]);
-  double n2 = (ss[0] + ss[1]) + (ss[2] + ss[3]);
-  n2 = team_reduce<T>(n2, [](double a, double b) { return a + b; }) * (1.0 / T);
-  fwht_contig<E, 1, double>(x, 0);
-  double h;
-  const double g = sqrt_and_half_rsqrt(n2, h);
-  const bool zero = !(n2 > 0.0);
-  const float nrm = zero ? 0.f : (float)g;
-  // u = H(s * x) / (||x|| sqrt(d)) (pitch_reference.py:96-98); a zero vector is divided by 1
-  const double us = zero ? DimConst<D>::kInvSqrt : (2.0 * h) * DimConst<D>::kInvSqrt;
-
   uint32_t w[NWL];
-  Q::template codes_packed<(E > 16 ? 8 : PITCH_QBATCH)>(sq, x, us, lane, w);
+  float nrm;
+  if constexpr (POLAR) {
+    nrm = hs_polar_codes<D, T, B, NWL>(x, w);
+  } else {
+    // ||x||^2 = sum of squares after the team-bit stages / T (each stage doubles it exactly)
+    double ss[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int e = 0; e < E; ++e) ss[e & 3] = __builtin_fma(x[e], x[e], ss[e & 3]);
+    double n2 = (ss[0] + ss[1]) + (ss[2] + ss[3]);
+    n2 = team_reduce<T>(n2, [](double a, double b) { return a + b; }) * (1.0 / T);
+    fwht_contig<E, 1, double>(x, 0);
+    double h;
+    const double g = sqrt_and_half_rsqrt(n2, h);
+    const bool zero = !(n2 > 0.0);
+    nrm = zero ? 0.f : (float)g;
+    // u = H(s * x) / (||x|| sqrt(d)) (pitch_reference.py:96-98); a zero vector is divided by 1
+    const double us = zero ? DimConst<D>::kInvSqrt : (2.0 * h) * DimConst<D>::kInvSqrt;
+    Q::template codes_packed<(E > 16 ? 8 : PITCH_QBATCH)>(sq, x, us, lane, w);
+  }
   // Every store is unconditional, so the compiler can count the vector-memory operations of an iteration and
   // wait for the next block's loads without waiting for these stores (gfx9 counts loads and stores together,
   // in order). A vector past the end was loaded from the last vector (hs_fetch), so its codes and scale equal
@@ -1280,18 +1345,23 @@ __device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLu
 #ifndef PITCH_HS_WAVES128
 #define PITCH_HS_WAVES128 3
 #endif
-template <int D, bool KBIAS>
-constexpr int hs_waves() { return KBIAS ? 2 : (D == 64 ? PITCH_HS_WAVES64 : PITCH_HS_WAVES128); }
+#ifndef PITCH_HS_WAVES_POLAR
+#define PITCH_HS_WAVES_POLAR 2  // PolarQuant is bound by its arithmetic, not by latency
+#endif
+template <int D, bool POLAR, bool KBIAS>
+constexpr int hs_waves() {
+  return POLAR ? PITCH_HS_WAVES_POLAR : (KBIAS ? 2 : (D == 64 ? PITCH_HS_WAVES64 : PITCH_HS_WAVES128));
+}
 
-template <int D, int B, bool KBIAS>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hs_waves<D, KBIAS>())))
-void tq_encode_hs(VecArgs p) {
+template <int D, int B, bool POLAR, bool KBIAS>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hs_waves<D, POLAR, KBIAS>())))
+void vec_encode_hs(VecArgs p) {
   constexpr int T = hs_team<D>();
   using H = Hs<D, T>;
   constexpr int E = H::E, V = H::V;
   using Q = TqLut8<D, B>;
   __shared__ __attribute__((aligned(16))) double s_x[H::WAVES][H::ROWS];
-  __shared__ __attribute__((aligned(16))) typename Q::Smem s_q;
+  __shared__ __attribute__((aligned(16))) typename Q::Smem s_q;  // (unused by PolarQuant)
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float* in = (const float*)p.in;
@@ -1303,7 +1373,7 @@ void tq_encode_hs(VecArgs p) {
   // The waves' first loads are issued after the table set-up, so no other load is pending at that point.
   constexpr int PFD = hs_pfd<D, B, KBIAS>();
   static_assert(PFD == 1 || PFD == 2, "prefetch depth");
-  Q::load(s_q, threadIdx.x, 64 * H::WAVES);
+  if constexpr (!POLAR) Q::load(s_q, threadIdx.x, 64 * H::WAVES);
   const uint64_t* neg = (const uint64_t*)p.lane_flips;  // fill_hs_flips; kernel arguments, read as scalars
   __syncthreads();
   if (base >= p.count) return;
@@ -1318,7 +1388,7 @@ void tq_encode_hs(VecArgs p) {
   auto step = [&](u32x4 (&refill)[H::QPL], u32x4 (&next)[H::QPL]) {
     hs_fetch<D, T>(in, base + (uint64_t)PFD * stride, p.count, lane, refill);
     __builtin_amdgcn_sched_barrier(0);  // the loads go out before the compute, not interleaved into it
-    hs_compute<D, T, B>(p, s_q, base, lane, sx, x);
+    hs_compute<D, T, B, POLAR>(p, s_q, base, lane, sx, x);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1340,7 +1410,10 @@ void tq_encode_hs(VecArgs p) {
 }
 
 #ifndef PITCH_HS_ENCODER
-#define PITCH_HS_ENCODER 1  // 1: float32 TurboQuant encode at D = 64 / 128 uses tq_encode_hs
+#define PITCH_HS_ENCODER 1  // 1: float32 TurboQuant encode at D = 64 / 128 uses vec_encode_hs
+#endif
+#ifndef PITCH_HS_POLAR
+#define PITCH_HS_POLAR 1  // 1: float32 PolarQuant encode at D = 64 / 128 uses vec_encode_hs
 #endif
 
 template <int D>
@@ -1350,14 +1423,14 @@ template <int D, int B, bool POLAR, int IO, bool KBIAS>
 hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   using G = Geom<D>;
   VecArgs a = args;
-  if constexpr (!POLAR && IO == 0 && PITCH_HS_ENCODER && (D == 64 || D == 128)) {
+  if constexpr (IO == 0 && (POLAR ? PITCH_HS_POLAR : PITCH_HS_ENCODER) && (D == 64 || D == 128)) {
     if (encode) {
       using H = Hs<D, hs_team<D>()>;
       fill_hs_flips<D, hs_team<D>()>(a.seed, a.lane_flips);
       const uint64_t need = (a.count + H::WAVES * H::V - 1) / (H::WAVES * H::V);
-      const void* k = (const void*)&tq_encode_hs<D, B, KBIAS>;
+      const void* k = (const void*)&vec_encode_hs<D, B, POLAR, KBIAS>;
       const uint64_t grid = persistent_grid(k, need, 64 * H::WAVES);
-      hipLaunchKernelGGL((tq_encode_hs<D, B, KBIAS>), dim3((uint32_t)grid), dim3(64 * H::WAVES), 0, s, a);
+      hipLaunchKernelGGL((vec_encode_hs<D, B, POLAR, KBIAS>), dim3((uint32_t)grid), dim3(64 * H::WAVES), 0, s, a);
       return hipGetLastError();
     }
   }
