@@ -100,6 +100,35 @@ __device__ __forceinline__ float guarded_floor(float t, bool& ok) {
   return k;
 }
 
+// The staged-stage PolarQuant encoder's angle in sector units, w = (atan2(c, a) mod 2 pi) * 2^B / (2 pi) in
+// [0, 2^B]: angle_turns with the factor 2^B / (2 pi) folded into the polynomial's coefficients (each product
+// rounded once to float32) and the octant fix-ups taken in sector units (2^B / 4, 2^B / 2, 2^B are exact).
+template <int B>
+__device__ __forceinline__ float angle_sectors(float c, float a) {
+  constexpr int DEG = pitch_atan_degree(B);
+  constexpr float L = float(1 << B);
+  constexpr float kS = float(double(1 << B) / 6.283185307179586);  // 2^B / (2 pi)
+  const float ax = __builtin_fabsf(a), ay = __builtin_fabsf(c);
+  const float mx = __builtin_fmaxf(ax, ay), mn = __builtin_fminf(ax, ay);
+  const float z = mn * __builtin_amdgcn_rcpf(mx);
+  const float s = z * z;
+  float poly = pitch_atan_coef[DEG][DEG] * kS;
+#pragma unroll
+  for (int i = DEG - 1; i >= 0; --i) poly = __builtin_fmaf(poly, s, pitch_atan_coef[DEG][i] * kS);
+  float w = poly * z;                  // atan(mn / mx) in sector units, [0, 2^B / 8]
+  if (ay > ax) w = 0.25f * L - w;
+  if (a < 0.f) w = 0.5f * L - w;
+  return c < 0.f ? L - w : w;
+}
+
+// floor(t) for t >= 0 (a truncating convert) when t is at least kPolarGuard from an integer (then ok is left
+// alone), else ok = false; a NaN t fails the guard.
+__device__ __forceinline__ uint32_t guarded_code(float t, bool& ok) {
+  const float f = __builtin_amdgcn_fractf(t);
+  ok = ok && f > kPolarGuard && f < 1.f - kPolarGuard;
+  return (uint32_t)t;
+}
+
 // y / sqrt(D) rounded as the reference's division (pitch_reference.py:33).
 template <int D>
 __device__ __forceinline__ double div_sqrt_d(double y) {
@@ -1233,11 +1262,11 @@ __device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w
   for (int q = 0; q < NP; ++q) {
     const float af = (float)x[2 * q], cf = (float)x[2 * q + 1];
     const float rf = __builtin_amdgcn_sqrtf(__builtin_fmaf(af, af, cf * cf));
-    bool ok = inrange && (af != 0.f || cf != 0.f);
-    const float kr = guarded_floor(__builtin_fmaf(rf, sr, 0.5f), ok);
-    const float ka = guarded_floor(__builtin_fmaf(angle_turns<B>(cf, af), float(L), 0.5f), ok);
-    uint32_t cr = (uint32_t)__builtin_fminf(kr, float(L - 1));
-    uint32_t ca = (uint32_t)ka & (uint32_t)(L - 1);
+    // rf <= rmax up to rounding, so t_r < 2^B - 1/2 + 1e-5 and its floor needs no clip; a pair at the origin
+    // gives a NaN angle (0 * 1/0), which fails the guard
+    bool ok = inrange;
+    uint32_t cr = guarded_code(__builtin_fmaf(rf, sr, 0.5f), ok);
+    uint32_t ca = guarded_code(angle_sectors<B>(cf, af) + 0.5f, ok) & (uint32_t)(L - 1);
     if (!ok) {  // rare: one shared out-of-line copy
       const double a = x[2 * q], c = x[2 * q + 1];
       const uint2 cc = polar_codes_exact<B>(a, c, __builtin_fma(a, a, c * c), safe);

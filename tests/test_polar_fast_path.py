@@ -1,10 +1,16 @@
-"""The PolarQuant encoder's float32 fast path, emulated on the CPU (CPU only).
+"""The PolarQuant encoders' float32 fast paths, emulated on the CPU (CPU only).
 
-pitch_vector.hip decides each radius and angle code from t = value * levels + 0.5 evaluated in float32
-(angle_turns: octant reduction and the fitted atan polynomial) and keeps floor(t) only when t lies at least
-kPolarGuard = 3e-4 from an integer; otherwise the float64 path decides. This test evaluates the same float32
-steps in numpy (fused multiply-adds as one rounding, the reciprocal correctly rounded, which the hardware's
-1-ulp reciprocal can differ from by one ulp) on rotated K/V-like vectors and checks that
+pitch_vector.hip decides each radius and angle code from t = value * levels + 0.5 evaluated in float32 and
+keeps floor(t) only when t lies at least kPolarGuard = 3e-4 from an integer; otherwise the float64 path
+decides. There are two formulations:
+* the team encoder (vec_encode; 16-bit inputs and dimensions other than 64 and 128) scales each pair by
+  1 / rmax in float64 before rounding it to float32, and takes the angle in turns (angle_turns);
+* the staged-stage encoder (vec_encode_hs; float32 inputs at d = 64 and 128) rounds the unscaled pair of the
+  unnormalised transform to float32, multiplies the radius by RN((2^b - 1) / rmax), and takes the angle in
+  sector units (angle_sectors: the factor 2^b / (2 pi) folded into the polynomial's coefficients).
+This test evaluates the same float32 steps in numpy (fused multiply-adds as one rounding, the reciprocal and
+square root correctly rounded, which the hardware's 1-ulp versions can differ from by one ulp) on rotated
+K/V-like vectors and checks, for both, that
 * the float32 t stays within a third of the guard of the float64 t of the oracle at every bit width,
 * every code the guard accepts equals the oracle's code (pitch_reference.py:109-121),
 * the guard sends only a small fraction of pairs to the float64 path.
@@ -44,6 +50,74 @@ def angle_turns(c, a, coef):
     at = np.where(a < 0, (f32(np.pi) - at).astype(f32), at)
     turns = (at * f32(1 / (2 * np.pi))).astype(f32)
     return np.where(c < 0, (f32(1) - turns).astype(f32), turns)
+
+
+def angle_sectors(c, a, coef, b):
+    """angle_sectors of pitch_vector.hip: angle_turns * 2^b with 2^b / (2 pi) folded into the coefficients."""
+    L = f32(2 ** b)
+    kS = f32(2 ** b / (2 * np.pi))
+    cs = [f32(k) * kS for k in coef]
+    ax, ay = np.abs(a), np.abs(c)
+    mx, mn = np.maximum(ax, ay), np.minimum(ax, ay)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        z = (mn * (f32(1) / mx)).astype(f32)
+    s = (z * z).astype(f32)
+    p = np.full_like(s, cs[-1])
+    for k in cs[-2::-1]:
+        p = _fma32(p, s, np.full_like(s, k))
+    w = (p * z).astype(f32)
+    w = np.where(ay > ax, (f32(0.25) * L - w).astype(f32), w)
+    w = np.where(a < 0, (f32(0.5) * L - w).astype(f32), w)
+    return np.where(c < 0, (L - w).astype(f32), w)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_staged_fast_path_matches_oracle(d):
+    """The staged-stage encoder's formulation, on the unnormalised transform as the kernel holds it."""
+    rng = np.random.default_rng(100 + d)
+    X = rng.standard_t(5, size=(6000, d)) * np.exp(rng.uniform(-2, 3, size=(6000, 1))) + rng.normal(0, 2, (1, d))
+    X = X.astype(np.float32).astype(np.float64)
+    Yu = O.rotate(X, O.DEFAULT_SEED) * math.sqrt(d)  # the transform before the division by sqrt(d)
+    a, c = Yu[:, 0::2], Yu[:, 1::2]
+    r, theta = O.polar_parts(X)
+    ru = np.hypot(a, c)
+    rmax = ru.max(1, keepdims=True)
+    safe = np.where(rmax > 0, rmax, 1.0)
+    af, cf = a.astype(f32), c.astype(f32)
+    rf = np.sqrt(_fma32(af, af, (cf * cf).astype(f32))).astype(f32)
+    for b in range(2, 9):
+        L = 2 ** b
+        sr = ((L - 1) / safe).astype(f32)
+        tr = _fma32(rf, np.broadcast_to(sr, rf.shape), np.full_like(rf, f32(0.5)))
+        ta = (angle_sectors(cf, af, G.atan_poly(G.ATAN_DEG[b]), b) + f32(0.5)).astype(f32)
+        tr_exact = ru / safe * (L - 1) + 0.5
+        ta_exact = theta / (2 * np.pi) * L + 0.5
+        da = np.abs(ta - ta_exact)
+        da = np.minimum(da, np.abs(da - L))
+        assert np.abs(tr - tr_exact).max() < GUARD / 3, b
+        assert da.max() < GUARD / 3, b
+        assert tr.max() < L - 0.5 + 1e-4, b  # the radius code needs no clip
+        fr, fa = tr - np.floor(tr), ta - np.floor(ta)
+        ok = (r > 0) & (fr > GUARD) & (fr < 1 - GUARD) & (fa > GUARD) & (fa < 1 - GUARD)
+        codes, _ = O.polar_encode(X, b)
+        rc = np.floor(tr).astype(np.int64)
+        ac = np.floor(ta).astype(np.int64) & (L - 1)
+        assert np.array_equal(rc[ok], codes[:, 0::2][ok]), b
+        assert np.array_equal(ac[ok], codes[:, 1::2][ok]), b
+        assert ok.mean() > 0.99, (b, ok.mean())
+
+
+@pytest.mark.parametrize("b", range(2, 9))
+def test_sector_angle_error_budget(b):
+    """Full circle: the emulated sector-unit angle keeps t = w + 0.5 within 1e-4 of the exact t."""
+    coef = G.atan_poly(G.ATAN_DEG[b])
+    th = np.linspace(-math.pi, math.pi, 400001)
+    a, c = np.cos(th).astype(f32), np.sin(th).astype(f32)
+    w = angle_sectors(c, a, coef, b).astype(np.float64)
+    ref = np.mod(np.arctan2(c.astype(np.float64), a.astype(np.float64)), 2 * np.pi) / (2 * np.pi) * 2 ** b
+    err = np.abs(w - ref)
+    err = np.minimum(err, 2 ** b - err)
+    assert err.max() < 1e-4
 
 
 @pytest.mark.parametrize("d", [16, 64, 128])
