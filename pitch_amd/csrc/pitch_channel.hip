@@ -200,14 +200,21 @@ constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
 #ifndef PITCH_KIVI_NT
 #define PITCH_KIVI_NT 1  // the wave encoder streams keys in and codes and ranges out non-temporally
 #endif
+#ifndef PITCH_KIVI_DP
+#define PITCH_KIVI_DP 1  // direct packing in the wave encoder where the bit width and row width allow it
+#endif
 #ifndef PITCH_KIVI_SLAB
 #define PITCH_KIVI_SLAB 0        // encoder slab width: 0 = chosen per call, else 32 or 64 channels
 #endif
 
 // SW = 64: lane (r, c) = (lane / 16, lane % 16), tokens r, r + 4, ... (16 per lane); SW = 32: lane
 // (lane / 8, lane % 8), tokens r, r + 8, ... (8 per lane), twice the work items and half the registers.
-template <int B, int IO, int SW>
+// DP (direct packing; B = 2, 4 or 8 and a row width that is a multiple of SW): lane c's four codes of a token
+// are the byte-aligned bit-field [4 B c, 4 B c + 4 B) of the row's packed code stream, so the lane packs them
+// in registers and writes B / 2 bytes of packed row to LDS; the stores then copy packed rows.
+template <int B, int IO, int SW, bool DP>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KIVI_WAVES))) void chan_encode_w(ChanArgs p) {
+  static_assert(!DP || B == 2 || B == 4 || B == 8, "direct packing needs byte-aligned lane fields");
   constexpr int QW = SW / 4;           // lanes per token row
   constexpr int RPI = 64 / QW;         // token rows per load instruction
   constexpr int TPL = kGroupMaxW / RPI;  // tokens per lane
@@ -290,17 +297,40 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
         const float a = xv[k] - bs[k];
         const float q0 = a * inv[k];
         const float q = __builtin_fmaf(__builtin_fmaf(-q0, stc[k], a), inv[k], q0);  // RN(a / step)
-        const float t = __builtin_floorf(q + 0.5f);
-        word |= (uint32_t)__builtin_fminf(__builtin_fmaxf(t, 0.0f), levels) << (8 * k);
+        // clip(floor(q + 0.5), 0, 2^B - 1) as one med3 (exact: an integral value)
+        const float t = __builtin_amdgcn_fmed3f(__builtin_floorf(q + 0.5f), 0.0f, levels);
+        if constexpr (DP && B < 8) word |= (uint32_t)t << (B * k);                 // packed field
+        else word = __builtin_amdgcn_cvt_pk_u8_f32(t, (uint32_t)k, word);      // byte k
       }
-      *(uint32_t*)(s_stage + tk * SW + 4u * c) = word;
+      if constexpr (DP) {
+        uint8_t* row = s_stage + tk * (SW * B / 8) + c * (B / 2);
+        if constexpr (B == 2) *row = (uint8_t)word;
+        else if constexpr (B == 4) *(uint16_t*)row = (uint16_t)word;
+        else *(uint32_t*)row = word;
+      } else {
+        *(uint32_t*)(s_stage + tk * SW + 4u * c) = word;
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // pack: the slab's codes of a token start at word ch0 * B / 32 of its row (ch0 is a multiple of 64)
     uint32_t* dst = p.codes_out + (uint64_t)first * p.nwords + ch0 * B / 32u;
-    if ((cw & 31u) == 0u) {
+    if constexpr (DP) {
+      // packed rows of SW * B / 8 bytes in LDS, each the slab's part of a token row
+      constexpr int RW = SW * B / 32;                 // words per packed LDS row
+      constexpr int PW = RW >= 4 ? 4 : RW;            // words per copy
+      constexpr uint32_t pr = RW / PW;  // copies per row (every slab is full: cw = SW)
+      const uint32_t np = n * pr;
+      for (uint32_t q = lane; q < np; q += 64) {
+        const uint32_t tok = q / pr, pi = q - tok * pr;
+        const uint32_t* src = (const uint32_t*)(s_stage + tok * (SW * B / 8)) + PW * pi;
+        uint32_t* d = dst + (uint64_t)tok * p.nwords + PW * pi;
+        if constexpr (PW == 4) store_v((u32x4*)d, *(const u32x4*)src, PITCH_KIVI_NT);
+        else if constexpr (PW == 2) store_v((u32x2*)d, *(const u32x2*)src, PITCH_KIVI_NT);
+        else store_v(d, *src, PITCH_KIVI_NT);
+      }
+    } else if ((cw & 31u) == 0u) {
       const uint32_t gpr = cw >> 5, ng = n * gpr;  // 32-code groups per row, then in all
       for (uint32_t q = lane; q < ng; q += 64) {
         const uint32_t tok = q / gpr, gi = q - tok * gpr;
@@ -516,14 +546,24 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
     // 64-channel slabs, whose loads read whole 256-byte rows (+4 % at 131072 items)
     const uint64_t items64 = groups * ((a.dim + 63) / 64);
     const int sw = PITCH_KIVI_SLAB ? PITCH_KIVI_SLAB : (items64 <= 32768 ? 32 : 64);
+    const bool dp = PITCH_KIVI_DP && (B == 2 || B == 4 || B == 8) && a.dim % (uint32_t)sw == 0u;  // full slabs
+    auto go = [&](auto sw_c, auto dp_c) {
+      constexpr int SW = decltype(sw_c)::value;
+      constexpr bool DP = decltype(dp_c)::value;
+      const uint64_t items = groups * ((a.dim + SW - 1) / SW);
+      const void* k = (const void*)&chan_encode_w<B, IO, SW, DP>;
+      const uint64_t grid = persistent_grid(k, (items + 3) / 4);
+      hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    };
+    using I32 = std::integral_constant<int, 32>;
+    using I64 = std::integral_constant<int, 64>;
+    constexpr bool kDP = B == 2 || B == 4 || B == 8;
     if (sw == 32) {
-      const uint64_t items = groups * ((a.dim + 31) / 32);
-      const uint64_t grid = persistent_grid((const void*)&chan_encode_w<B, IO, 32>, (items + 3) / 4);
-      hipLaunchKernelGGL((chan_encode_w<B, IO, 32>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+      if (dp) go(I32{}, std::integral_constant<bool, kDP>{});
+      else go(I32{}, std::false_type{});
     } else {
-      const uint64_t items = groups * ((a.dim + 63) / 64);
-      const uint64_t grid = persistent_grid((const void*)&chan_encode_w<B, IO, 64>, (items + 3) / 4);
-      hipLaunchKernelGGL((chan_encode_w<B, IO, 64>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+      if (dp) go(I64{}, std::integral_constant<bool, kDP>{});
+      else go(I64{}, std::false_type{});
     }
   } else if (encode) {
     const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;

@@ -158,6 +158,14 @@ def test_config5_k_share(q):
     channel_full(q, 32, 131072, 128, 4, 64, 5001)
 
 
+@pytest.mark.parametrize("bits", [2, 3, 8])
+def test_kivi_64_channel_slabs_bit_widths(q, bits):
+    """One call of 2^21 + 192 tokens at d = 64: 32,771 (group, 64-channel) items, so the encoder takes its
+    64-channel-slab variant, here at the bit widths whose lane fields are packed directly (2, 8) and one that
+    goes through byte staging (3)."""
+    channel_full(q, 1, (1 << 21) + 192, 64, bits, 64, 5100 + bits, one_call=True)
+
+
 def test_config5_k_share_one_call(q):
     """16 heads x 131072 tokens in one call: 65,536 (group, 64-channel) items, so the encoder takes its
     64-channel-slab variant (fewer items take the 32-channel one, covered above)."""
