@@ -198,7 +198,13 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
 constexpr int kSlab = 64;        // channels per wave of the decoder
 constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
 #ifndef PITCH_KIVI_NT
-#define PITCH_KIVI_NT 1  // the wave encoder streams keys in and codes and ranges out non-temporally
+#define PITCH_KIVI_NT 1  // the wave encoder reads keys with non-temporal loads
+#endif
+#ifndef PITCH_KIVI_NTS
+// Non-temporal stores of codes and ranges. Off: a 32-channel slab writes half of each token's code row and
+// of each range row, and cached stores let L2 merge the halves of neighbouring slabs into whole lines (with
+// non-temporal stores the encoder wrote 1.5x its algorithmic bytes)
+#define PITCH_KIVI_NTS 0
 #endif
 #ifndef PITCH_KIVI_DP
 #define PITCH_KIVI_DP 1  // direct packing in the wave encoder where the bit width and row width allow it
@@ -279,10 +285,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
     if (r == 0 && cact) {
       uint16_t* rg = p.ranges_out + (uint64_t)g * 2u * dim + ch0 + 4u * c;
       store_v((u32x2*)rg, u32x2{(uint32_t)l16[0] | ((uint32_t)l16[1] << 16), (uint32_t)l16[2] | ((uint32_t)l16[3] << 16)},
-              PITCH_KIVI_NT);
+              PITCH_KIVI_NTS);
       store_v((u32x2*)(rg + dim),
               u32x2{(uint32_t)h16[0] | ((uint32_t)h16[1] << 16), (uint32_t)h16[2] | ((uint32_t)h16[3] << 16)},
-              PITCH_KIVI_NT);
+              PITCH_KIVI_NTS);
     }
     // codes clip(floor((x - lo) / step + 0.5), 0, 2^B - 1) (pitch_reference.py:157-158), one byte each in LDS.
     // Rows past the group's end and channels past the slab's end are quantised and staged too (their slots
@@ -326,9 +332,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
         const uint32_t tok = q / pr, pi = q - tok * pr;
         const uint32_t* src = (const uint32_t*)(s_stage + tok * (SW * B / 8)) + PW * pi;
         uint32_t* d = dst + (uint64_t)tok * p.nwords + PW * pi;
-        if constexpr (PW == 4) store_v((u32x4*)d, *(const u32x4*)src, PITCH_KIVI_NT);
-        else if constexpr (PW == 2) store_v((u32x2*)d, *(const u32x2*)src, PITCH_KIVI_NT);
-        else store_v(d, *src, PITCH_KIVI_NT);
+        if constexpr (PW == 4) store_v((u32x4*)d, *(const u32x4*)src, PITCH_KIVI_NTS);
+        else if constexpr (PW == 2) store_v((u32x2*)d, *(const u32x2*)src, PITCH_KIVI_NTS);
+        else store_v(d, *src, PITCH_KIVI_NTS);
       }
     } else if ((cw & 31u) == 0u) {
       const uint32_t gpr = cw >> 5, ng = n * gpr;  // 32-code groups per row, then in all
@@ -339,7 +345,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
         const uint32_t bytes[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         uint32_t w[B];
         pack32<B>(bytes, w);
-        if constexpr (PITCH_KIVI_NT) store_words_nt<B>(dst + (uint64_t)tok * p.nwords + gi * B, w);
+        if constexpr (PITCH_KIVI_NTS) store_words_nt<B>(dst + (uint64_t)tok * p.nwords + gi * B, w);
         else store_words<B>(dst + (uint64_t)tok * p.nwords + gi * B, w);
       }
     } else {

@@ -1322,9 +1322,9 @@ __device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLu
   // in order). A vector past the end was loaded from the last vector (hs_fetch), so its codes and scale equal
   // the last vector's and are written to that vector's place: the same bytes to the same address.
   const uint64_t vst = base + vw < p.count ? base + vw : p.count - 1;
-  // the T lanes of a team write the same scale
-  if constexpr (PITCH_HS_NT) __builtin_nontemporal_store(nrm, p.scales_out + vst);
-  else p.scales_out[vst] = nrm;
+  // the T lanes of a team write the same scale; cached (a wave writes 64 bytes of scales, half a line, which L2
+  // merges with the next wave's)
+  p.scales_out[vst] = nrm;
   if constexpr (kWhole) {
     // lane (vw, t) owns words t * NWL .. of its vector: the wave's stores are one contiguous run
     if constexpr (PITCH_HS_NT) store_words_nt(p.codes_out + vst * NW + t * NWL, w);
