@@ -741,8 +741,11 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   __syncthreads();
 
   // Software pipeline: the codes and scale of the next iteration are loaded before the current one is
-  // transformed, so every wave keeps a batch of loads in flight while it computes. Loads are unconditional
-  // (indices past the end are clamped to the last vector); only lanes holding a real vector store.
+  // transformed, so every wave keeps a batch of loads in flight while it computes. Loads and stores are
+  // unconditional: an index past the end is clamped to the last vector, whose decode such a lane then computes
+  // and writes to the last vector's place (the same bytes to the same address). With a fixed number of
+  // memory operations per iteration the compiler waits for the next batch's loads without waiting for the
+  // previous iteration's stores (gfx9 counts loads and stores together, in order).
   struct Batch {
     uint32_t lo[G::CH], hi[G::CH];
     float scale;
@@ -767,10 +770,8 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
       decode_chunk<D, B, POLAR>(__builtin_amdgcn_alignbit(b.hi[k], b.lo[k], wsh[k]), s_tab, y + k * G::W);
     fwht_f32_lane_signed<D, TB::PRE>(y, t);
   };
-  auto body = [&](const Batch& b, float (&y)[G::E], uint64_t base, auto tail_c) {
-    constexpr bool TAIL = decltype(tail_c)::value;
-    const uint64_t v = base + slot;
-    const bool valid = !TAIL || v < p.count;
+  auto body = [&](const Batch& b, float (&y)[G::E], uint64_t base) {
+    const uint64_t v = base + slot < p.count ? base + slot : p.count - 1;
     const float f = b.scale * DimConst<D>::kInvSqrtF;
     if constexpr (kLdsStore) {
       // stage the wave's vectors in LDS, then write them back as contiguous 1 KB wave stores
@@ -807,10 +808,11 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
 #pragma unroll
           for (int r = 0; r < K; ++r) o[r] = o[r] + ob[r];
         }
-        if (!TAIL || wbase + vq < p.count) store_elems<IO, K>(p.out, wbase * D + (uint64_t)K * q, o, PITCH_NT_STORE);
+        const uint64_t vd = wbase + vq < p.count ? wbase + vq : p.count - 1;
+        store_elems<IO, K>(p.out, vd * D + (uint64_t)K * cq, o, PITCH_NT_STORE);
       }
       __builtin_amdgcn_wave_barrier();
-    } else if (valid) {
+    } else {
 #pragma unroll
       for (int k = 0; k < G::CH; ++k) {
         float o[G::W];
@@ -827,20 +829,34 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
       }
     }
   };
+  // Two batches alternate (no register copies of batches that may still be in flight), and the loop is
+  // rotated so that each batch is waited for in straight-line code after exactly one iteration's stores and the
+  // next batch's loads: fetch A(i), fetch B(i + 1), compute A(i); then fetch A(i + 2), compute B(i + 1),
+  // fetch B(i + 3), compute A(i + 2), ...
   const uint64_t stride = (uint64_t)gridDim.x * G::VPB;
   uint64_t base = (uint64_t)blockIdx.x * G::VPB;
   if (base >= p.count) return;  // uniform per workgroup; no barrier follows
-  Batch cur = fetch(base);
-  for (;;) {
-    const uint64_t nbase = base + stride;
-    const Batch nxt = fetch(nbase < p.count ? nbase : base);
+  auto compute = [&](const Batch& b, uint64_t at) {
     float y[G::E];
-    transform(cur, y);
-    if (base + G::VPB <= p.count) body(cur, y, base, std::false_type{});
-    else body(cur, y, base, std::true_type{});
-    if (nbase >= p.count) break;
-    cur = nxt;
-    base = nbase;
+    transform(b, y);
+    body(b, y, at);
+  };
+  Batch ba = fetch(base);
+  Batch bb = fetch(base + stride);
+  compute(ba, base);
+  for (;;) {
+    base += stride;
+    if (base >= p.count) break;
+    ba = fetch(base + stride);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(bb, base);
+    __builtin_amdgcn_sched_barrier(0);
+    base += stride;
+    if (base >= p.count) break;
+    bb = fetch(base + stride);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(ba, base);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
