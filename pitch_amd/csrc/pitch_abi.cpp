@@ -366,7 +366,7 @@ uint64_t attention_workspace_floats(uint32_t dim, uint32_t nqp, uint32_t kv_head
   return (uint64_t)kv_heads * nqp * (dim + tokens + chunks * (2 + dim));
 }
 
-uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size) {
+uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size, bool balance_rounds) {
   static std::mutex mu;
   static std::unordered_map<const void*, int> occ_cache;
   // PITCH_BLOCKS_PER_CU overrides the resident 256-thread-block count per CU (tuning aid; smaller blocks
@@ -389,9 +389,23 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
       occ_cache[kernel] = occ;
     }
   }
-  const uint64_t cap = (uint64_t)device_cu_count() * (uint64_t)occ;
-  uint64_t g = blocks_needed < cap ? blocks_needed : cap;
-  return g < 1 ? 1 : g;
+  const uint64_t cus = (uint64_t)device_cu_count();
+  const uint64_t cap = cus * (uint64_t)occ;
+  if (blocks_needed <= cap) return blocks_needed < 1 ? 1 : blocks_needed;
+  if (!balance_rounds) return cap;
+  // k workgroups per CU make ceil(need / (cus k)) rounds of k each; a bandwidth-bound round takes about k
+  // times as long, so cost(k) = rounds * k counts the idle slots of a last, partly filled round. Take the
+  // largest k in [occ / 2, occ] within 5 % of the cheapest: a call whose last round would be nearly empty
+  // runs fewer, fully used rounds instead (e.g. 6144 blocks at 7 per CU on 256 CUs: 4 rounds of 6 rather than
+  // 3.43 of 7; config-2 decode +4 %), while long calls keep full occupancy. Kernels bound by their arithmetic
+  // lose more from fewer resident waves than they gain (16-bit per-channel encode -5 %), so callers opt in.
+  const uint64_t kmin = ((uint64_t)occ + 1) / 2;
+  auto cost = [&](uint64_t k) { return (blocks_needed + cus * k - 1) / (cus * k) * k; };
+  uint64_t best = cost((uint64_t)occ);
+  for (uint64_t k = kmin; k < (uint64_t)occ; ++k) best = cost(k) < best ? cost(k) : best;
+  for (uint64_t k = (uint64_t)occ; k > kmin; --k)
+    if (cost(k) * 20 <= best * 21) return cus * k;
+  return cus * kmin;
 }
 
 }  // namespace pitch

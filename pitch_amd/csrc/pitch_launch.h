@@ -90,8 +90,10 @@ hipError_t launch_attention_d128(const AttnArgs& a, hipStream_t s);
 int device_cu_count();
 
 // Grid size for a grid-stride kernel: enough workgroups to fill every CU at the kernel's occupancy,
-// but no more than the work needs.
-uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256);
+// but no more than the work needs. With balance_rounds, a call of several rounds may use fewer workgroups per
+// CU so that its last round is not left nearly empty (for bandwidth-bound kernels, whose rounds take time in
+// proportion to the workgroups they run).
+uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256, bool balance_rounds = false);
 
 // Per-vector launch for one dimension D and I/O element type IO (0 float32, 1 float16, 2 bfloat16); one
 // object file per (D, IO) defines launch_vec_d<D>_io<IO>.

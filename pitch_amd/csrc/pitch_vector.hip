@@ -1497,7 +1497,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
     hipLaunchKernelGGL((vec_encode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else {
     const void* k = (const void*)&vec_decode<D, B, POLAR, IO, KBIAS>;
-    const uint64_t grid = persistent_grid(k, need);
+    const uint64_t grid = persistent_grid(k, need, kBlock, true);
     hipLaunchKernelGGL((vec_decode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   }
   return hipGetLastError();
