@@ -252,19 +252,32 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
       else load_elems<IO, 4>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
       x[i] = make_float4(v[0], v[1], v[2], v[3]);
     }
-    float4 lo = x[0], hi = x[0];
+    // minima and maxima with the hardware's min3 / max3 / min / max (no canonicalising of the loaded and
+    // exchanged values, which fminf / fmaxf would add)
+    float l[4], h[4];
 #pragma unroll
-    for (int i = 1; i < TPL; ++i) {
-      lo = make_float4(fminf(lo.x, x[i].x), fminf(lo.y, x[i].y), fminf(lo.z, x[i].z), fminf(lo.w, x[i].w));
-      hi = make_float4(fmaxf(hi.x, x[i].x), fmaxf(hi.y, x[i].y), fmaxf(hi.z, x[i].z), fmaxf(hi.w, x[i].w));
+    for (int k = 0; k < 4; ++k) {
+      auto e = [&](int i) { return k == 0 ? x[i].x : k == 1 ? x[i].y : k == 2 ? x[i].z : x[i].w; };
+      float mn = e(0), mx = e(0);
+      int i = 1;
+#pragma unroll
+      for (; i + 1 < TPL; i += 2) {
+        mn = fmin3_hw(mn, e(i), e(i + 1));
+        mx = fmax3_hw(mx, e(i), e(i + 1));
+      }
+      if (i < TPL) {
+        mn = fmin_hw(mn, e(i));
+        mx = fmax_hw(mx, e(i));
+      }
+      l[k] = mn;
+      h[k] = mx;
     }
-    float l[4] = {lo.x, lo.y, lo.z, lo.w}, h[4] = {hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
 #pragma unroll
       for (int off = QW; off < 64; off <<= 1) {
-        l[k] = fminf(l[k], __shfl_xor(l[k], off));
-        h[k] = fmaxf(h[k], __shfl_xor(h[k], off));
+        l[k] = fmin_hw(l[k], __shfl_xor(l[k], off));
+        h[k] = fmax_hw(h[k], __shfl_xor(h[k], off));
       }
     }
     uint16_t l16[4], h16[4];
@@ -303,10 +316,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
         const float a = xv[k] - bs[k];
         const float q0 = a * inv[k];
         const float q = __builtin_fmaf(__builtin_fmaf(-q0, stc[k], a), inv[k], q0);  // RN(a / step)
-        // clip(floor(q + 0.5), 0, 2^B - 1) as one med3 (exact: an integral value)
-        const float t = __builtin_amdgcn_fmed3f(__builtin_floorf(q + 0.5f), 0.0f, levels);
-        if constexpr (DP && B < 8) word |= (uint32_t)t << (B * k);                 // packed field
-        else word = __builtin_amdgcn_cvt_pk_u8_f32(t, (uint32_t)k, word);      // byte k
+        // clip(floor(q + 0.5), 0, 2^B - 1): q + 0.5 rounded to float32 as in the reference, then one flooring
+        // convert and an integer med3
+        const uint32_t t = (uint32_t)min(max(cvt_flr_i32(q + 0.5f), 0), (1 << B) - 1);
+        if constexpr (DP && B < 8) word |= t << (B * k);           // packed field
+        else word |= t << (8 * k);                                 // byte k
       }
       if constexpr (DP) {
         uint8_t* row = s_stage + tk * (SW * B / 8) + c * (B / 2);

@@ -105,6 +105,31 @@ struct Geom {
 // exactly a + b and a - b, so a float64 transform reproduces the reference bit for bit.
 // Cross-lane butterfly: the low lane computes fma(mine, +1, partner) = a + b, the high lane
 // fma(mine, -1, partner) = a - b.
+// min / max with the hardware's semantics, as single instructions: for non-NaN operands the same as fminf /
+// fmaxf, without the canonicalising v_max_f32 x, x that the compiler puts before fminf / fmaxf (and before a
+// med3 against an infinity, which it turns into them) for operands not known to be canonical, such as loaded
+// values or values exchanged between lanes.
+__device__ __forceinline__ float fmin_hw(float a, float b) { float r; asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b)); return r; }
+__device__ __forceinline__ float fmax_hw(float a, float b) { float r; asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b)); return r; }
+__device__ __forceinline__ float fmin3_hw(float a, float b, float c) {
+  float r;
+  asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float fmax3_hw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// floor(x) converted to int32 in one instruction (exact: the floor of a float is an integer-valued float; NaN
+// gives 0 and values beyond the int32 range saturate). The compiler does not form it from (int)floorf(x).
+__device__ __forceinline__ int cvt_flr_i32(float x) {
+  int r;
+  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 template <int D, typename F>
 __device__ __forceinline__ void fwht(F (&v)[Geom<D>::E], int t) {
   using G = Geom<D>;
