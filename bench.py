@@ -92,8 +92,13 @@ def profiled_traffic(bits: int):
 
 
 def student_t(torch, shape, nu, gen, device):
-    """Student-t(nu) = N(0,1) / sqrt(chi2(nu) / nu), generated on the device."""
+    """Student-t(nu) = N(0,1) / sqrt(chi2(nu) / nu), generated on the device.
+
+    The Gamma sampler takes no generator and draws from torch's default CUDA generator, so that one is
+    seeded from gen first: the same seed gives the same values in every run."""
     z = torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+    seed = int(torch.randint(0, 2**62, (1,), generator=gen, device=device).item())
+    torch.cuda.manual_seed(seed)
     g = torch.distributions.Gamma(torch.tensor(nu / 2.0, device=device), torch.tensor(0.5, device=device))
     chi2 = g.sample(shape)
     return z / torch.sqrt(chi2 / nu)
