@@ -265,6 +265,13 @@ int pitch_enqueue_unpack_codes(uint32_t dim, uint32_t bits, const void* packed, 
                                uint64_t packed_offset, void* unpacked, uint64_t unpacked_bytes,
                                uint64_t unpacked_offset, uint64_t count, void* stream);
 
+/* Self-test of a hardware property the per-channel encoder relies on; no counterpart in the reference. The
+ * encoder forms the correctly rounded reciprocal of each channel's step as v_rcp_f32 plus one Newton step,
+ * which on gfx950 equals the correctly rounded 1 / x for every positive normal float below 2^126. This call
+ * checks all of them on the current device (synchronously, allocating 4 MB of device memory) and writes
+ * the number that differ (0 expected) to *mismatches. For tests and bring-up on new hardware. */
+int pitch_selftest_reciprocal(uint64_t* mismatches);
+
 #ifdef __cplusplus
 }
 #endif

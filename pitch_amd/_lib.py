@@ -92,6 +92,7 @@ SIGNATURES = {
                                                     + [_vp, _u64, _vp]),
     "pitch_enqueue_pack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_unpack_codes": (_int, [_u32, _u32, _vp, _u64, _u64, _vp, _u64, _u64, _u64, _vp]),
+    "pitch_selftest_reciprocal": (_int, [ctypes.POINTER(_u64)]),
 }
 
 _lock = threading.Lock()

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <mutex>
+#include <vector>
 #include <string>
 #include <unordered_map>
 
@@ -763,6 +764,26 @@ int pitch_enqueue_unpack_codes(uint32_t dim, uint32_t bits, const void* packed, 
                                uint64_t unpacked_offset, uint64_t count, void* stream) {
   return pack_common(false, dim, bits, packed, packed_bytes, packed_offset, unpacked, unpacked_bytes,
                      unpacked_offset, count, stream);
+}
+
+int pitch_selftest_reciprocal(uint64_t* mismatches) {
+  if (!mismatches) return fail(PITCH_ERR_INVALID_INPUT, "mismatches is null");
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  constexpr uint32_t kThreads = 1u << 20;
+  constexpr uint32_t kFirst = 0x00800000u, kEnd = 0x7e800000u;  // positive normals below 2^126
+  uint32_t* d = nullptr;
+  if (hipMalloc((void**)&d, kThreads * sizeof(uint32_t)) != hipSuccess)
+    return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "self-test allocation failed");
+  std::vector<uint32_t> h(kThreads);
+  hipError_t e = pitch::launch_selftest_reciprocal(d, kThreads, kFirst, kEnd, nullptr);
+  if (e == hipSuccess) e = hipMemcpy(h.data(), d, kThreads * sizeof(uint32_t), hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "self-test failed: %s", hipGetErrorString(e));
+  uint64_t total = 0;
+  for (uint32_t c : h) total += c;
+  *mismatches = total;
+  return ok();
 }
 
 }  // extern "C"

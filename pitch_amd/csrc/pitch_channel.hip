@@ -242,15 +242,31 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
     const bool cact = 4u * c < cw;
     const uint64_t src = (uint64_t)first * dim + ch0 + (cact ? 4u * c : 0u);  // element index
 
-    // loads: rows past the group's end re-read its last row (no effect on the range)
+    // loads: rows past the group's end re-read its last row (no effect on the range). In a group of all
+    // kGroupMaxW rows no row is clamped: each load is then a wave-uniform row base plus the lane's 32-bit byte
+    // offset, with no per-lane 64-bit address arithmetic.
     float4 x[TPL];
+    if (n == (uint32_t)kGroupMaxW) {
+      constexpr uint32_t ES = IO == 0 ? 4u : 2u;  // bytes per key element
+      const char* gbase = (const char*)p.in + ((uint64_t)first * dim + ch0) * ES;
+      const uint32_t loff = (r * dim + (cact ? 4u * c : 0u)) * ES;
 #pragma unroll
-    for (int i = 0; i < TPL; ++i) {
-      const uint32_t tk = r + (uint32_t)RPI * i;
-      float v[4];
-      if constexpr (PITCH_KIVI_NT) load4_nt<IO>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
-      else load_elems<IO, 4>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
-      x[i] = make_float4(v[0], v[1], v[2], v[3]);
+      for (int i = 0; i < TPL; ++i) {
+        const char* row = gbase + (uint64_t)(RPI * i) * dim * ES;
+        float v[4];
+        if constexpr (PITCH_KIVI_NT) load4_nt<IO>(row + loff, 0, v);
+        else load_elems<IO, 4>(row + loff, 0, v);
+        x[i] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        const uint32_t tk = r + (uint32_t)RPI * i;
+        float v[4];
+        if constexpr (PITCH_KIVI_NT) load4_nt<IO>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
+        else load_elems<IO, 4>(p.in, src + (uint64_t)(tk < n ? tk : n - 1) * dim, v);
+        x[i] = make_float4(v[0], v[1], v[2], v[3]);
+      }
     }
     // minima and maxima with the hardware's min3 / max3 / min / max (no canonicalising of the loaded and
     // exchanged values, which fminf / fmaxf would add)
@@ -292,7 +308,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
       const float s0 = d * kInvLevels;
       const float sq = __builtin_fmaf(__builtin_fmaf(-s0, levels, d), kInvLevels, s0);  // RN(d / levels)
       const float st = sq == 0.0f ? 1.0f : sq;                                            // kivi_step
-      inv[k] = 1.0f / st;
+      inv[k] = rcp_rn(st);
       stc[k] = __builtin_fminf(st, 0x1.fffffep127f);
     }
     if (r == 0 && cact) {
@@ -674,6 +690,30 @@ hipError_t launch_pack(bool pack, const PackArgs& a, hipStream_t s) {
         persistent_grid((const void*)&unpack_generic, (a.count * a.dim + kBlock - 1) / kBlock);
     hipLaunchKernelGGL(unpack_generic, dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   }
+  return hipGetLastError();
+}
+
+// Self-test of rcp_rn: thread t checks the positive normal floats with bit patterns first + t * per + k
+// (k < per, below 2^126), counting those whose rcp_rn differs from the correctly rounded 1 / x (the library is
+// built with -fhip-fp32-correctly-rounded-divide-sqrt). One count per thread, no atomics.
+__global__ __launch_bounds__(kBlock) void selftest_reciprocal(uint32_t* counts, uint32_t first, uint32_t end,
+                                                                 uint32_t per) {
+  const uint32_t t = blockIdx.x * kBlock + threadIdx.x;
+  uint32_t bad = 0;
+  for (uint32_t k = 0; k < per; ++k) {
+    const uint64_t bits = (uint64_t)first + (uint64_t)t * per + k;
+    if (bits >= end) break;
+    const float x = __uint_as_float((uint32_t)bits);
+    bad += __float_as_uint(rcp_rn(x)) != __float_as_uint(1.0f / x) ? 1u : 0u;
+  }
+  counts[t] = bad;
+}
+
+hipError_t launch_selftest_reciprocal(uint32_t* counts, uint32_t threads, uint32_t first, uint32_t end,
+                                      hipStream_t s) {
+  if (threads % kBlock != 0 || end <= first) return hipErrorInvalidValue;
+  const uint32_t per = (uint32_t)(((uint64_t)end - first + threads - 1) / threads);
+  hipLaunchKernelGGL(selftest_reciprocal, dim3(threads / kBlock), dim3(kBlock), 0, s, counts, first, end, per);
   return hipGetLastError();
 }
 #endif

@@ -122,6 +122,16 @@ __device__ __forceinline__ float fmax3_hw(float a, float b, float c) {
   return r;
 }
 
+// RN(1 / x) for a per-channel step: v_rcp_f32 and one Newton step. On gfx950 this equals the correctly rounded
+// reciprocal for every normal x below 2^126 (checked exhaustively by pitch_selftest_reciprocal); steps of the
+// per-channel codec are at most (65504 + 65504) / 3. An infinite step (a range end beyond float16) gives 0,
+// the reciprocal of infinity; a NaN step gives NaN.
+__device__ __forceinline__ float rcp_rn(float x) {
+  const float y0 = __builtin_amdgcn_rcpf(x);
+  const float y1 = __builtin_fmaf(__builtin_fmaf(-x, y0, 1.0f), y0, y0);
+  return __builtin_isinf(x) ? 0.0f : y1;
+}
+
 // floor(x) converted to int32 in one instruction (exact: the floor of a float is an integer-valued float; NaN
 // gives 0 and values beyond the int32 range saturate). The compiler does not form it from (int)floorf(x).
 __device__ __forceinline__ int cvt_flr_i32(float x) {

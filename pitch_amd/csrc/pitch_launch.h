@@ -119,5 +119,9 @@ hipError_t launch_channel_io0(bool encode, int bits, const ChanArgs& a, hipStrea
 hipError_t launch_channel_io1(bool encode, int bits, const ChanArgs& a, hipStream_t s);
 hipError_t launch_channel_io2(bool encode, int bits, const ChanArgs& a, hipStream_t s);
 hipError_t launch_pack(bool pack, const PackArgs& a, hipStream_t s);
+// Counts per thread (threads a multiple of 256) of the floats with bit patterns in [first, end) whose rcp_rn
+// is not the correctly rounded reciprocal.
+hipError_t launch_selftest_reciprocal(uint32_t* counts, uint32_t threads, uint32_t first, uint32_t end,
+                                      hipStream_t s);
 
 }  // namespace pitch

@@ -137,6 +137,17 @@ def test_word_aligned_offsets(q, method, d):
         assert np.all(o[:off // 4] == 7.0) and np.all(o[off // 4 + n * d:] == 7.0)
 
 
+def test_reciprocal_selftest(q):
+    """The per-channel encoder forms RN(1 / step) as v_rcp_f32 plus one Newton step; pitch_selftest_reciprocal
+    checks on this device that this equals the correctly rounded reciprocal for every positive normal float
+    below 2^126 (steps are at most 131008 / 3)."""
+    import ctypes
+    from pitch_amd import _lib
+    n = ctypes.c_uint64(12345)
+    assert _lib.load().pitch_selftest_reciprocal(ctypes.byref(n)) == 0, _lib.last_error()
+    assert n.value == 0, f"{n.value} floats whose reciprocal is not correctly rounded"
+
+
 def test_channel_word_aligned_offsets(q):
     import torch
     d, n = 36, 100
