@@ -300,10 +300,6 @@ struct Io {
   static constexpr int kPerChunk = 16 / kBytes;  // elements per 16-byte access
 };
 
-// Address of element i of an IO-typed array.
-template <int IO>
-__device__ __forceinline__ void* elem_ptr(void* base, uint64_t i) { return (char*)base + i * Io<IO>::kBytes; }
-
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 

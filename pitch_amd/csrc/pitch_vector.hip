@@ -750,26 +750,16 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
     uint32_t lo[G::CH], hi[G::CH];
     float scale;
   };
-  // Vector base + j clamped to the last one, as bc + jc: the wave-uniform bc = min(base, count - 1) and the
-  // lane's 32-bit jc = min(j, count - 1 - bc) (j < 64). Every address is then a wave-uniform 64-bit base plus a
-  // small 32-bit lane offset, with the clamp as one 32-bit min per lane instead of 64-bit compares and selects.
-  auto clamp_base = [&](uint64_t base, uint32_t& lim) {
-    const uint64_t bc = base < p.count ? base : p.count - 1;
-    const uint64_t rem = p.count - 1 - bc;
-    lim = rem < 0xFFFFull ? (uint32_t)rem : 0xFFFFu;
-    return bc;
-  };
   auto fetch = [&](uint64_t base) {
     Batch b;
-    uint32_t lim;
-    const uint64_t bc = clamp_base(base, lim);
-    const uint32_t jc = (uint32_t)slot < lim ? (uint32_t)slot : lim;
-    b.scale = (p.scales_in + bc)[jc];
-    const uint32_t* cw = p.codes_in + bc * NW;
+    const uint64_t v = base + slot;
+    const uint64_t vl = v < p.count ? v : p.count - 1;
+    b.scale = p.scales_in[vl];
+    const uint32_t* cw = p.codes_in + vl * NW;
 #pragma unroll
     for (int k = 0; k < G::CH; ++k) {
-      b.lo[k] = cw[jc * NW + wlo[k]];
-      b.hi[k] = cw[jc * NW + whi[k]];
+      b.lo[k] = cw[wlo[k]];
+      b.hi[k] = cw[whi[k]];
     }
     return b;
   };
@@ -781,6 +771,7 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
     fwht_f32_lane_signed<D, TB::PRE>(y, t);
   };
   auto body = [&](const Batch& b, float (&y)[G::E], uint64_t base) {
+    const uint64_t v = base + slot < p.count ? base + slot : p.count - 1;
     const float f = b.scale * DimConst<D>::kInvSqrtF;
     if constexpr (kLdsStore) {
       // stage the wave's vectors in LDS, then write them back as contiguous 1 KB wave stores
@@ -797,8 +788,7 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // first vector of this wave (the wave index read as a scalar, so that wbase stays wave-uniform)
-      const uint64_t wbase = base + (uint64_t)__builtin_amdgcn_readfirstlane(tid >> 6) * G::V;
+      const uint64_t wbase = base + (uint64_t)(tid >> 6) * G::V;  // first vector of this wave
       constexpr int K = Io<IO>::kPerChunk;  // elements per 16-byte store
       static_assert((G::V * D) % (64 * K) == 0, "whole 16-byte stores per lane");
 #pragma unroll
@@ -811,22 +801,18 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
           const float4 val = *(const float4*)(ws + vq * kVecStride + K * cq + 4 * h);
           o[4 * h] = val.x; o[4 * h + 1] = val.y; o[4 * h + 2] = val.z; o[4 * h + 3] = val.w;
         }
-        uint32_t lim;
-        const uint64_t bc = clamp_base(wbase, lim);
-        const uint32_t jc = (uint32_t)vq < lim ? (uint32_t)vq : lim;
         if constexpr (KBIAS) {  // key-bias removal: restore x + o (mechanism_eval.py:113-116)
           float ob[K];
-          key_bias_offset<D, K>(p, bc + jc, K * cq, ob);
+          const uint64_t vv = wbase + vq < p.count ? wbase + vq : p.count - 1;
+          key_bias_offset<D, K>(p, vv, K * cq, ob);
 #pragma unroll
           for (int r = 0; r < K; ++r) o[r] = o[r] + ob[r];
         }
-        store_elems<IO, K>(elem_ptr<IO>(p.out, bc * D), jc * D + K * cq, o, PITCH_NT_STORE);
+        const uint64_t vd = wbase + vq < p.count ? wbase + vq : p.count - 1;
+        store_elems<IO, K>(p.out, vd * D + (uint64_t)K * cq, o, PITCH_NT_STORE);
       }
       __builtin_amdgcn_wave_barrier();
     } else {
-      uint32_t lim;
-      const uint64_t bc = clamp_base(base, lim);
-      const uint32_t jc = (uint32_t)slot < lim ? (uint32_t)slot : lim;
 #pragma unroll
       for (int k = 0; k < G::CH; ++k) {
         float o[G::W];
@@ -835,11 +821,11 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
           o[r] = __uint_as_float(__float_as_uint(y[k * G::W + r] * f) ^ flip[k * G::W + r]);
         if constexpr (KBIAS) {
           float ob[G::W];
-          key_bias_offset<D, G::W>(p, bc + jc, G::W * (k * G::T + t), ob);
+          key_bias_offset<D, G::W>(p, v, G::W * (k * G::T + t), ob);
 #pragma unroll
           for (int r = 0; r < G::W; ++r) o[r] = o[r] + ob[r];
         }
-        store_elems<IO, G::W>(elem_ptr<IO>(p.out, bc * D), jc * D + G::W * (k * G::T + t), o, PITCH_NT_STORE);
+        store_elems<IO, G::W>(p.out, v * D + G::W * (k * G::T + t), o, PITCH_NT_STORE);
       }
     }
   };
