@@ -602,11 +602,12 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
   const bool vec4 = (a.dim & 3u) == 0u;
   if (encode && vec4 && a.group <= (uint32_t)kGroupMaxW) {
     const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;
-    // 32-channel slabs double the work items and halve each lane's registers, which balances calls with few
-    // (group, 64-channel) items over the resident waves (+5-10 % at 4096-8192 items); long calls keep
-    // 64-channel slabs, whose loads read whole 256-byte rows (+4 % at 131072 items)
+    // 32-channel slabs double the work items and halve each lane's registers, which balances float32 calls
+    // with few (group, 64-channel) items over the resident waves (+5-10 % at 4096-8192 items); long calls keep
+    // 64-channel slabs, whose loads read whole 256-byte rows (+4 % at 131072 items). With 16-bit keys a
+    // 64-channel row is only 128 bytes and the wider slab measured 6-7 % faster at 4096 items as well.
     const uint64_t items64 = groups * ((a.dim + 63) / 64);
-    const int sw = PITCH_KIVI_SLAB ? PITCH_KIVI_SLAB : (items64 <= 32768 ? 32 : 64);
+    const int sw = PITCH_KIVI_SLAB ? PITCH_KIVI_SLAB : (IO == 0 && items64 <= 32768 ? 32 : 64);
     const bool dp = PITCH_KIVI_DP && (B == 2 || B == 4 || B == 8) && a.dim % (uint32_t)sw == 0u;  // full slabs
     auto go = [&](auto sw_c, auto dp_c) {
       constexpr int SW = decltype(sw_c)::value;
