@@ -195,7 +195,10 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
 #ifndef PITCH_KIVI_WAVES
 #define PITCH_KIVI_WAVES 3  // waves per SIMD the per-channel encoder's register budget allows
 #endif
-constexpr int kSlab = 64;        // channels per wave of the decoder
+constexpr int kSlab = 64;        // channels per wave of the decoder (long calls)
+#ifndef PITCH_KIVI_DEC_SLAB32
+#define PITCH_KIVI_DEC_SLAB32 1  // 1: 32-channel decoder slabs for float32 calls of at most 32768 (group, 64-channel) items
+#endif
 constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
 #ifndef PITCH_KIVI_NT
 #define PITCH_KIVI_NT 1  // the wave encoder reads keys with non-temporal loads
@@ -634,9 +637,19 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
     if (vec4) hipLaunchKernelGGL((chan_encode4<B, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
     else hipLaunchKernelGGL((chan_encode1<B, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else if (vec4 && a.group % 64u == 0u) {
-    const uint64_t items = (((uint64_t)a.count + a.group - 1) / a.group) * ((a.dim + kSlab - 1) / kSlab);
-    const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, kSlab, IO>, (items + 3) / 4);
-    hipLaunchKernelGGL((chan_decode_w<B, kSlab, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    // float32 output: 32-channel slabs for calls with few (group, 64-channel) items, which then fill the
+    // resident waves (config-3 decode +3-4 % back-to-back, within 0.5 % in kernel time); 16-bit output keeps
+    // 64-channel slabs (a 32-channel slab's rows are 64 bytes: 22 % slower)
+    const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;
+    const uint64_t items64 = groups * ((a.dim + kSlab - 1) / kSlab);
+    auto go = [&](auto sw_c) {
+      constexpr int SW = decltype(sw_c)::value;
+      const uint64_t items = groups * ((a.dim + SW - 1) / SW);
+      const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, SW, IO>, (items + 3) / 4);
+      hipLaunchKernelGGL((chan_decode_w<B, SW, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    };
+    if (PITCH_KIVI_DEC_SLAB32 && IO == 0 && items64 <= 32768) go(std::integral_constant<int, 32>{});
+    else go(std::integral_constant<int, kSlab>{});
   } else if (vec4) {
     const uint32_t P = kBlock / (a.dim >> 2);
     const uint64_t need = ((uint64_t)a.count + P * kDecR - 1) / (P * kDecR);
