@@ -212,6 +212,9 @@ constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
 #ifndef PITCH_KIVI_DP
 #define PITCH_KIVI_DP 1  // direct packing in the wave encoder where the bit width and row width allow it
 #endif
+#ifndef PITCH_KIVI_BALANCE
+#define PITCH_KIVI_BALANCE 1  // 1: the float32 wave encoder asks for balanced rounds
+#endif
 #ifndef PITCH_KIVI_SLAB
 #define PITCH_KIVI_SLAB 0        // encoder slab width: 0 = chosen per call, else 32 or 64 channels
 #endif
@@ -617,7 +620,9 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       constexpr bool DP = decltype(dp_c)::value;
       const uint64_t items = groups * ((a.dim + SW - 1) / SW);
       const void* k = (const void*)&chan_encode_w<B, IO, SW, DP>;
-      const uint64_t grid = persistent_grid(k, (items + 3) / 4);
+      // float32 keys: balanced rounds (config 3 is 1.33 rounds at full occupancy); the 16-bit encoders are
+      // bound by their arithmetic and keep every resident wave
+      const uint64_t grid = persistent_grid(k, (items + 3) / 4, kBlock, PITCH_KIVI_BALANCE && IO == 0);
       hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
     };
     using I32 = std::integral_constant<int, 32>;
