@@ -63,12 +63,13 @@ int validate_channel_config(const pitch_channel_config_t* c) {
 
 uint32_t code_stride_of(uint32_t dim, uint32_t bits) { return (dim * bits + 31u) / 32u * 4u; }
 
-// Offset alignment and "needs N bytes after offset" (Codec.swift:37-47).
-int check_buffer(const void* ptr, uint64_t bytes, uint64_t off, uint64_t need, const char* name) {
+// Offset alignment and "needs N bytes after offset" (Codec.swift:37-47). Offsets a caller passes must be multiples
+// of 4 bytes, as in the reference; offsets the library derives itself may need only element alignment (align).
+int check_buffer(const void* ptr, uint64_t bytes, uint64_t off, uint64_t need, const char* name, uint64_t align = 4) {
   if (!ptr) return fail(PITCH_ERR_INVALID_INPUT, "%s buffer is null", name);
-  if (off % 4 != 0)
-    return fail(PITCH_ERR_INVALID_INPUT, "%s offset %llu must be a non-negative multiple of 4", name,
-                (unsigned long long)off);
+  if (off % align != 0)
+    return fail(PITCH_ERR_INVALID_INPUT, "%s offset %llu must be a non-negative multiple of %llu", name,
+                (unsigned long long)off, (unsigned long long)align);
   if (bytes < off || bytes - off < need)
     return fail(PITCH_ERR_INVALID_INPUT, "%s buffer has %lld bytes after offset; needs %llu", name,
                 (long long)bytes - (long long)off, (unsigned long long)need);
@@ -235,16 +236,20 @@ int decode_impl(const pitch_config_t* config, uint32_t io, const void* codes, ui
   return ok();
 }
 
+// input_align: alignment the input offset needs (4 for a caller's offset; the element size for the offset
+// pitch_enqueue_channel_append derives, which for 16-bit keys of a dimension that is not a multiple of 4 can be
+// 2 mod 4 and is read element by element by the kernel such shapes use).
 int channel_encode_impl(const pitch_channel_config_t* config, uint32_t io, const void* input, uint64_t input_bytes,
                         uint64_t input_offset, void* codes, uint64_t codes_bytes, uint64_t codes_offset,
-                        void* ranges, uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count, void* stream) {
+                        void* ranges, uint64_t ranges_bytes, uint64_t ranges_offset, uint64_t count, void* stream,
+                        uint64_t input_align = 4) {
   PITCH_TRY(validate_channel_config(config));
   PITCH_TRY(check_io(io));
   const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
   if (count < 1) return fail(PITCH_ERR_INVALID_INPUT, "count must be at least 1");
   if (count > 0xFFFFFFFFull) return fail(PITCH_ERR_INVALID_INPUT, "per-channel count must be below 2^32 tokens");
   const uint64_t groups = (count + config->group_size - 1) / config->group_size;
-  PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * io_bytes(io), "input"));
+  PITCH_TRY(check_buffer(input, input_bytes, input_offset, count * dim * io_bytes(io), "input", input_align));
   PITCH_TRY(check_buffer(codes, codes_bytes, codes_offset, count * cs, "codes"));
   PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
   int dev = 0;
@@ -542,9 +547,10 @@ int pitch_enqueue_channel_append(const pitch_channel_config_t* config, uint32_t 
   PITCH_TRY(check_buffer(ranges, ranges_bytes, ranges_offset, groups * 4u * dim, "ranges"));
   // re-encode from the start of the group that holds the first new token
   const uint64_t g0 = (total_tokens - new_tokens) / G, first = g0 * G;
+  // input_offset itself is a multiple of 4 (checked above); the derived offset is element-aligned
   return channel_encode_impl(config, io_type, input, input_bytes, input_offset + first * dim * esize, codes,
                              codes_bytes, codes_offset + first * cs, ranges, ranges_bytes,
-                             ranges_offset + g0 * 4u * dim, total_tokens - first, stream);
+                             ranges_offset + g0 * 4u * dim, total_tokens - first, stream, esize);
 }
 
 int pitch_attention_workspace_size(const pitch_config_t* key_config, const pitch_config_t* value_config,

@@ -27,6 +27,12 @@ constexpr int kDecR = 4;           // tokens per thread per decode iteration
 __device__ __forceinline__ uint16_t f2h_bits(float x) { return __half_as_ushort(__float2half_rn(x)); }
 __device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_as_half(b)); }
 
+// Groups of G tokens in a call of count tokens, in 64 bits: count may be up to 2^32 - 1 and count + G - 1 would
+// wrap in 32 bits.
+__device__ __forceinline__ uint32_t group_count(uint32_t count, uint32_t G) {
+  return (uint32_t)(((uint64_t)count + G - 1u) / G);
+}
+
 __device__ __forceinline__ float kivi_step(float lo, float hi, float levels) {
   const float s = (hi - lo) / levels;
   return s == 0.0f ? 1.0f : s;
@@ -85,10 +91,10 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
   const uint32_t tid = threadIdx.x, pp = tid / C, col = tid - pp * C;
   const bool active = pp < P;
   const uint32_t TT = min(P * kMaxR, (uint32_t)kStageBytes / dim);  // tokens per packing tile
-  const uint32_t groups = (p.count + p.group - 1) / p.group;
+  const uint32_t groups = group_count(p.count, p.group);
 
-  for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
-    const uint32_t first = g * p.group;
+  for (uint64_t g = blockIdx.x; g < groups; g += gridDim.x) {  // 64-bit: g + gridDim.x must not wrap
+    const uint32_t first = (uint32_t)(g * p.group);
     const uint32_t n = min(p.group, p.count - first);
     const uint64_t src = (uint64_t)first * dim + 4u * col;  // element index of this thread's first channel
 
@@ -237,7 +243,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
   const int r = lane / QW, c = lane % QW;
   const uint32_t dim = p.dim, G = p.group;
   const uint32_t slabs = (dim + SW - 1) / SW;
-  const uint32_t groups = (p.count + G - 1) / G;
+  const uint32_t groups = group_count(p.count, G);
   const uint64_t items = (uint64_t)groups * slabs;
   const uint64_t waves = (uint64_t)gridDim.x * (kBlock / 64);
 
@@ -412,9 +418,9 @@ __global__ __launch_bounds__(kBlock) void chan_encode1(ChanArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_stage[kStageBytes];
   const uint32_t dim = p.dim, tid = threadIdx.x;
   const uint32_t TT = max(1u, (uint32_t)kStageBytes / dim);
-  const uint32_t groups = (p.count + p.group - 1) / p.group;
-  for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
-    const uint32_t first = g * p.group;
+  const uint32_t groups = group_count(p.count, p.group);
+  for (uint64_t g = blockIdx.x; g < groups; g += gridDim.x) {  // 64-bit: g + gridDim.x must not wrap
+    const uint32_t first = (uint32_t)(g * p.group);
     const uint32_t n = min(p.group, p.count - first);
     const uint64_t src = (uint64_t)first * dim;  // element index of the group's first token
     for (uint32_t ch = tid; ch < dim; ch += kBlock) {
@@ -470,7 +476,7 @@ __global__ __launch_bounds__(kBlock) void chan_decode4(ChanArgs p) {
       if (tk < p.count) {
         if (gcur == 0xFFFFFFFFu || tk >= gend || tk + p.group < gend) {
           gcur = (uint32_t)(tk / p.group);
-          gend = (uint64_t)(gcur + 1) * p.group;
+          gend = ((uint64_t)gcur + 1u) * p.group;
           const uint16_t* rg = p.ranges_in + (uint64_t)gcur * 2u * dim + 4u * col;
           const u32x2 l = *(const u32x2*)rg, h = *(const u32x2*)(rg + dim);
           const uint16_t l16[4] = {(uint16_t)l.x, (uint16_t)(l.x >> 16), (uint16_t)l.y, (uint16_t)(l.y >> 16)};
@@ -510,7 +516,7 @@ __global__ __launch_bounds__(kBlock) void chan_decode_w(ChanArgs p) {
   const int r = lane / QW, c = lane % QW;
   const uint32_t dim = p.dim, G = p.group;
   const uint32_t slabs = (dim + SW - 1) / SW;
-  const uint32_t groups = (p.count + G - 1) / G;
+  const uint32_t groups = group_count(p.count, G);
   const uint64_t items = (uint64_t)groups * slabs;
   const uint64_t waves = (uint64_t)gridDim.x * (kBlock / 64);
 

@@ -366,6 +366,44 @@ def test_channel_append_validation(lib):
     assert app(T, 1) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
 
 
+def test_channel_append_16bit_odd_group_offset(lib):
+    """16-bit keys with dim = 3, G = 7: the group holding the first new token starts at token 7, i.e. at byte
+    7 * 3 * 2 = 42 = 2 mod 4 of the input. That derived offset needs only element alignment: the call passes
+    every argument check and stops at the device lookup (no GPU here) or the device-memory check, never at
+    the offset check. A caller's own input offset must still be a multiple of 4."""
+    cfg = _lib.PitchChannelConfigC(3, 4, 7, 0)
+    T = 12                                            # groups [0, 7) and [7, 12)
+    inp, codes, ranges = Host(T * 3 * 2), Host(T * 4), Host(2 * 12)
+
+    def app(total, new, off=0):
+        return lib.pitch_enqueue_channel_append(ctypes.byref(cfg), _lib.IO_F16, inp.p, inp.nbytes, off, codes.p,
+                                                codes.nbytes, 0, ranges.p, ranges.nbytes, 0, total, new, None)
+
+    for io in (_lib.IO_F16, _lib.IO_BF16):
+        rc = lib.pitch_enqueue_channel_append(ctypes.byref(cfg), io, inp.p, inp.nbytes, 0, codes.p, codes.nbytes, 0,
+                                              ranges.p, ranges.nbytes, 0, T, 2, None)
+        assert rc in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+        assert "offset" not in _lib.last_error() and "needs" not in _lib.last_error(), _lib.last_error()
+    assert app(T - 1, 1, off=2) == _lib.ERR_INVALID_INPUT and "multiple of 4" in _lib.last_error()
+
+
+def test_channel_count_bound(lib):
+    """Per-channel calls take at most 2^32 - 1 tokens (the kernels count tokens and groups in 32 bits, with the
+    group count formed in 64 bits); one more is refused before any size check."""
+    cfg = _lib.PitchChannelConfigC(1, 2, 65536, 0)
+    big = Host(1 << 12)
+    rc = lib.pitch_enqueue_channel_encode(ctypes.byref(cfg), big.p, big.nbytes, 0, big.p, big.nbytes, 0, big.p,
+                                          big.nbytes, 0, 2 ** 32, None)
+    assert rc == _lib.ERR_INVALID_INPUT and "2^32" in _lib.last_error()
+    rc = lib.pitch_enqueue_channel_decode(ctypes.byref(cfg), big.p, big.nbytes, 0, big.p, big.nbytes, 0, big.p,
+                                          big.nbytes, 0, 2 ** 32, None)
+    assert rc == _lib.ERR_INVALID_INPUT and "2^32" in _lib.last_error()
+    # 2^32 - 1 tokens passes the count check and fails only on the (small) buffers
+    rc = lib.pitch_enqueue_channel_encode(ctypes.byref(cfg), big.p, big.nbytes, 0, big.p, big.nbytes, 0, big.p,
+                                          big.nbytes, 0, 2 ** 32 - 1, None)
+    assert rc == _lib.ERR_INVALID_INPUT and "needs" in _lib.last_error()
+
+
 def test_attention_channel_keys_validation(lib):
     kc = _lib.PitchChannelConfigC(64, 4, 64, 0)
     vc = _lib.PitchConfigC(0, 64, 4, 0)
