@@ -233,6 +233,29 @@ int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch
                                    uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes,
                                    uint64_t lse_offset, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* Largest workspace pitch_enqueue_attention_decode_noalloc can serve, in bytes (32 MiB: e.g. 8 KV heads x 4 query
+ * heads x 131072 tokens at dim 128 needs 18.9 MB). */
+#define PITCH_NOALLOC_SCRATCH_BYTES (32ull << 20)
+
+/* pitch_enqueue_attention_decode without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in
+ * the reference. The workspace is a scratch array compiled into the library, one per device, held until the process
+ * ends; the call allocates nothing. Calls whose workspace (pitch_attention_workspace_size) exceeds
+ * PITCH_NOALLOC_SCRATCH_BYTES fail with PITCH_ERR_INVALID_INPUT before any work is issued. Every call on a device
+ * shares that device's array: calls that overlap on one device (on different streams, or from different threads
+ * without ordering) race and must not be issued; calls ordered on one stream are safe. Results are otherwise those
+ * of pitch_enqueue_attention_decode on the same arguments. */
+int pitch_enqueue_attention_decode_noalloc(const pitch_config_t* key_config, const pitch_config_t* value_config,
+                                           const pitch_attention_desc_t* desc, const void* q, uint64_t q_bytes,
+                                           uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,
+                                           uint64_t key_codes_offset, const void* key_scales,
+                                           uint64_t key_scales_bytes, uint64_t key_scales_offset,
+                                           const void* value_codes, uint64_t value_codes_bytes,
+                                           uint64_t value_codes_offset, const void* value_scales,
+                                           uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output,
+                                           uint64_t output_bytes, uint64_t output_offset, void* lse,
+                                           uint64_t lse_bytes, uint64_t lse_offset, void* stream);
+
 /* pitch_enqueue_attention_decode with per-channel (KIVI) keys and per-vector values: the configuration the
  * reference recommends for models whose key projection has a bias (README.md:30) and evaluates as
  * "kivi_K{b}_turboV{b}" (reference/attention_extra.py:57-59). Keys decode as f32(c) * step + lo per group and

@@ -20,6 +20,8 @@ ERR_ENCODING_FAILED = -5
 ERR_DECODING_FAILED = -6
 ERR_DEVICE_UNAVAILABLE = -7
 
+NOALLOC_SCRATCH_BYTES = 32 << 20   # PITCH_NOALLOC_SCRATCH_BYTES: workspace limit of the allocation-free attention
+
 IO_F32 = 0    # element types of uncompressed vectors (PITCH_IO_*)
 IO_F16 = 1
 IO_BF16 = 2
@@ -83,6 +85,9 @@ SIGNATURES = {
     "pitch_enqueue_attention_decode": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
                                               ctypes.POINTER(PitchAttentionDescC)] + [_vp, _u64, _u64] * 7
                                        + [_vp, _u64, _vp]),
+    "pitch_enqueue_attention_decode_noalloc": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
+                                                      ctypes.POINTER(PitchAttentionDescC)] + [_vp, _u64, _u64] * 7
+                                               + [_vp]),
     "pitch_attention_channel_keys_workspace_size": (_int, [ctypes.POINTER(PitchChannelConfigC),
                                                            ctypes.POINTER(PitchConfigC),
                                                            ctypes.POINTER(PitchAttentionDescC), ctypes.POINTER(_u64)]),

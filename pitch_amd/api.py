@@ -678,11 +678,15 @@ class PITCH:
     def enqueueAttentionDecode(self, q, keyCodes, keyScales, valueCodes, valueScales, output, tokens: int,
                                keyConfig: QuantConfig, valueConfig: QuantConfig | None = None, qPerKv: int = 1,
                                kvHeads: int = 1, tokenStride: int = 1, headStride: int | None = None,
-                               scale: float | None = None, lse=None, workspace=None, stream=None) -> None:
+                               scale: float | None = None, lse=None, workspace=None, stream=None,
+                               noAlloc: bool = False) -> None:
         """out = softmax(scale * q K^T) V over caches held as codes: q and output are fp32
         [kvHeads][qPerKv][dim]; the vector of (head h, token t) is t * tokenStride + h * headStride (default
         headStride = tokens, a head-major cache). scale defaults to 1 / sqrt(dim). lse, when given, receives the
-        natural-log sum of exp of the scaled scores per query. Without a workspace one is allocated.
+        natural-log sum of exp of the scaled scores per query. Without a workspace one is allocated, unless
+        noAlloc: then the call goes to pitch_enqueue_attention_decode_noalloc, which allocates nothing and uses the
+        library's per-device scratch (at most PITCH_NOALLOC_SCRATCH_BYTES of workspace; per-vector keys only; calls
+        overlapping on one device race).
         With a ChannelQuantConfig as keyConfig the keys are per-channel: keyScales is their fp16 ranges tensor, the
         caches are head-major (tokenStride 1) and headStride, in tokens, a multiple of the group size (default:
         tokens rounded up to it)."""
@@ -695,7 +699,9 @@ class PITCH:
         if headStride is None:
             headStride = int(tokens) if not channel_keys else -(-int(tokens) // keyConfig.groupSize) * keyConfig.groupSize
         desc = _attention_desc(qPerKv, kvHeads, tokens, tokenStride, headStride, scale)
-        if workspace is None:
+        if noAlloc and (channel_keys or workspace is not None):
+            raise InvalidInput("noAlloc takes per-vector keys and no workspace")
+        if workspace is None and not noAlloc:
             nbytes = attention_workspace_bytes(valueConfig if channel_keys else keyConfig, valueConfig, tokens,
                                                qPerKv, kvHeads)
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
@@ -709,6 +715,12 @@ class PITCH:
             args += [p_, b_, 0]
         else:
             args += [None, 0, 0]
+        if noAlloc:
+            rc = self._lib.pitch_enqueue_attention_decode_noalloc(
+                ctypes.byref(keyConfig._c()), ctypes.byref(valueConfig._c()), ctypes.byref(desc), *args,
+                _stream_handle(stream, self.device))
+            _raise_for(rc)
+            return
         wp, wb = _buf(workspace, "workspace")
         fn = (self._lib.pitch_enqueue_attention_decode_channel_keys if channel_keys
               else self._lib.pitch_enqueue_attention_decode)

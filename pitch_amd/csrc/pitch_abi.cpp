@@ -563,15 +563,47 @@ int pitch_attention_workspace_size(const pitch_config_t* key_config, const pitch
   return ok();
 }
 
-int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch_config_t* value_config,
-                                   const pitch_attention_desc_t* desc, const void* q, uint64_t q_bytes,
-                                   uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,
-                                   uint64_t key_codes_offset, const void* key_scales, uint64_t key_scales_bytes,
-                                   uint64_t key_scales_offset, const void* value_codes, uint64_t value_codes_bytes,
-                                   uint64_t value_codes_offset, const void* value_scales,
-                                   uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output,
-                                   uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes,
-                                   uint64_t lse_offset, void* workspace, uint64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Scratch memory of pitch_enqueue_attention_decode_noalloc: the attention workspace for callers that cannot
+// allocate device memory. One copy per device, held until the process ends; every call on a device shares it.
+// Its device address comes from hipGetSymbolAddress (the array's name is only a host-side stand-in).
+constexpr uint64_t kNoAllocScratchBytes = PITCH_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on device dev, which must be the current device (looked up once per device).
+int scratch_address(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "device %d is out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "scratch memory of device %d is unavailable: %s", dev,
+                  hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return PITCH_OK;
+}
+
+// pitch_enqueue_attention_decode with either a caller's workspace or (workspace == nullptr) the library's scratch.
+int attention_impl(const pitch_config_t* key_config, const pitch_config_t* value_config,
+                   const pitch_attention_desc_t* desc, const void* q, uint64_t q_bytes, uint64_t q_offset,
+                   const void* key_codes, uint64_t key_codes_bytes, uint64_t key_codes_offset, const void* key_scales,
+                   uint64_t key_scales_bytes, uint64_t key_scales_offset, const void* value_codes,
+                   uint64_t value_codes_bytes, uint64_t value_codes_offset, const void* value_scales,
+                   uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output, uint64_t output_bytes,
+                   uint64_t output_offset, void* lse, uint64_t lse_bytes, uint64_t lse_offset, void* workspace,
+                   uint64_t workspace_bytes, void* stream, bool use_scratch) {
   PITCH_TRY(validate_attention(key_config, value_config, desc));
   const uint32_t dim = key_config->dim, nq = desc->q_per_kv, nqp = padded_queries(nq);
   const uint32_t kcs = code_stride_of(dim, key_config->bits), vcs = code_stride_of(dim, value_config->bits);
@@ -587,7 +619,15 @@ int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch
   if (lse) PITCH_TRY(check_buffer(lse, lse_bytes, lse_offset, queries * 4u, "lse"));
   const uint32_t chunk = pitch::attention_chunk_tokens(desc->tokens, desc->kv_heads);
   const uint64_t ws_need = 4u * pitch::attention_workspace_floats(dim, nqp, desc->kv_heads, desc->tokens, chunk);
-  PITCH_TRY(check_buffer(workspace, workspace_bytes, 0, ws_need, "workspace"));
+  if (use_scratch) {
+    if (ws_need > kNoAllocScratchBytes)
+      return fail(PITCH_ERR_INVALID_INPUT,
+                  "this call needs %llu bytes of workspace; the allocation-free entry point holds at most %llu "
+                  "(pass a workspace to pitch_enqueue_attention_decode instead)",
+                  (unsigned long long)ws_need, (unsigned long long)kNoAllocScratchBytes);
+  } else {
+    PITCH_TRY(check_buffer(workspace, workspace_bytes, 0, ws_need, "workspace"));
+  }
   int dev = 0;
   PITCH_TRY(current_device(&dev));
   PITCH_TRY(check_device(q, dev, "query"));
@@ -597,7 +637,8 @@ int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch
   PITCH_TRY(check_device(value_scales, dev, "value scales"));
   PITCH_TRY(check_device(output, dev, "output"));
   if (lse) PITCH_TRY(check_device(lse, dev, "lse"));
-  PITCH_TRY(check_device(workspace, dev, "workspace"));
+  if (use_scratch) PITCH_TRY(scratch_address(dev, &workspace));
+  else PITCH_TRY(check_device(workspace, dev, "workspace"));
   pitch::AttnArgs a{};
   a.q = at<const float>(q, q_offset);
   a.k_codes = at<const uint32_t>(key_codes, key_codes_offset);
@@ -629,6 +670,42 @@ int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch
                                  : pitch::launch_attention_d128(a, (hipStream_t)stream);
   if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Attention failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch_config_t* value_config,
+                                   const pitch_attention_desc_t* desc, const void* q, uint64_t q_bytes,
+                                   uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,
+                                   uint64_t key_codes_offset, const void* key_scales, uint64_t key_scales_bytes,
+                                   uint64_t key_scales_offset, const void* value_codes, uint64_t value_codes_bytes,
+                                   uint64_t value_codes_offset, const void* value_scales,
+                                   uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output,
+                                   uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes,
+                                   uint64_t lse_offset, void* workspace, uint64_t workspace_bytes, void* stream) {
+  return attention_impl(key_config, value_config, desc, q, q_bytes, q_offset, key_codes, key_codes_bytes,
+                        key_codes_offset, key_scales, key_scales_bytes, key_scales_offset, value_codes,
+                        value_codes_bytes, value_codes_offset, value_scales, value_scales_bytes, value_scales_offset,
+                        output, output_bytes, output_offset, lse, lse_bytes, lse_offset, workspace, workspace_bytes,
+                        stream, false);
+}
+
+int pitch_enqueue_attention_decode_noalloc(const pitch_config_t* key_config, const pitch_config_t* value_config,
+                                           const pitch_attention_desc_t* desc, const void* q, uint64_t q_bytes,
+                                           uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,
+                                           uint64_t key_codes_offset, const void* key_scales,
+                                           uint64_t key_scales_bytes, uint64_t key_scales_offset,
+                                           const void* value_codes, uint64_t value_codes_bytes,
+                                           uint64_t value_codes_offset, const void* value_scales,
+                                           uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output,
+                                           uint64_t output_bytes, uint64_t output_offset, void* lse,
+                                           uint64_t lse_bytes, uint64_t lse_offset, void* stream) {
+  return attention_impl(key_config, value_config, desc, q, q_bytes, q_offset, key_codes, key_codes_bytes,
+                        key_codes_offset, key_scales, key_scales_bytes, key_scales_offset, value_codes,
+                        value_codes_bytes, value_codes_offset, value_scales, value_scales_bytes, value_scales_offset,
+                        output, output_bytes, output_offset, lse, lse_bytes, lse_offset, nullptr, 0, stream, true);
 }
 
 int pitch_attention_channel_keys_workspace_size(const pitch_channel_config_t* key_config,
