@@ -372,6 +372,14 @@ uint64_t attention_workspace_floats(uint32_t dim, uint32_t nqp, uint32_t kv_head
   return (uint64_t)kv_heads * nqp * (dim + tokens + chunks * (2 + dim));
 }
 
+uint64_t slice_rounds(uint64_t dflt) {
+  static const long env = [] {
+    const char* e = std::getenv("PITCH_SLICE_ROUNDS");
+    return e ? std::atol(e) : -1L;
+  }();
+  return env >= 0 ? (uint64_t)env : dflt;
+}
+
 uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size, bool balance_rounds) {
   static std::mutex mu;
   static std::unordered_map<const void*, int> occ_cache;

@@ -206,6 +206,13 @@ constexpr int kSlab = 64;        // channels per wave of the decoder (long calls
 #define PITCH_KIVI_DEC_SLAB32 1  // 1: 32-channel decoder slabs for float32 calls of at most 32768 (group, 64-channel) items
 #endif
 constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
+// Calls of the wave encoder and decoder longer than this many rounds (grid-stride iterations per workgroup) are
+// issued as several launches of this many rounds. At a 17 GB footprint (config 5 keys: 33.5M tokens, d = 128) a
+// single persistent launch reaches 4.4 TB/s encoding and 4.9 TB/s decoding; launches of 2 rounds reach 5.3 and
+// 5.35 TB/s (1 round: 5.0 and 5.4). A launch boundary brings every workgroup back in step; in one long launch they
+// drift apart, and the reads of some interleave with the writes of others at the memory (a probe kernel with the
+// decoder's read/write mix showed the same gain from short launches). Calls of up to this many rounds keep one launch.
+constexpr uint64_t kChanSliceRounds = 2;
 #ifndef PITCH_KIVI_NT
 #define PITCH_KIVI_NT 1  // the wave encoder reads keys with non-temporal loads
 #endif
@@ -629,6 +636,23 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       // float32 keys: balanced rounds (config 3 is 1.33 rounds at full occupancy); the 16-bit encoders are
       // bound by their arithmetic and keep every resident wave
       const uint64_t grid = persistent_grid(k, (items + 3) / 4, kBlock, PITCH_KIVI_BALANCE && IO == 0);
+      const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRounds);
+      if (rounds && (items + 3) / 4 > grid * rounds && grid * rounds * 4 >= slabs) {
+        const uint64_t gpl = grid * rounds * 4 / slabs;  // groups per launch
+        constexpr uint64_t ES = IO == 0 ? 4 : 2;
+        for (uint64_t g0 = 0; g0 < groups; g0 += gpl) {
+          const uint64_t t0 = g0 * a.group;
+          ChanArgs b = a;
+          b.count = (uint32_t)((uint64_t)a.count - t0 < gpl * a.group ? (uint64_t)a.count - t0 : gpl * a.group);
+          b.in = (const char*)a.in + t0 * a.dim * ES;
+          b.codes_out = a.codes_out + t0 * a.nwords;
+          b.ranges_out = a.ranges_out + g0 * 2 * a.dim;
+          const uint64_t gb = ((uint64_t)b.count + a.group - 1) / a.group, nb = (gb * slabs + 3) / 4;
+          hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)(nb < grid ? nb : grid)), dim3(kBlock), 0,
+                             s, b);
+        }
+        return;
+      }
       hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
     };
     using I32 = std::integral_constant<int, 32>;
@@ -657,6 +681,22 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       constexpr int SW = decltype(sw_c)::value;
       const uint64_t items = groups * ((a.dim + SW - 1) / SW);
       const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, SW, IO>, (items + 3) / 4);
+      const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRounds);
+      if (rounds && (items + 3) / 4 > grid * rounds && grid * rounds * 4 >= slabs) {
+        const uint64_t gpl = grid * rounds * 4 / slabs;  // groups per launch
+        constexpr uint64_t ES = IO == 0 ? 4 : 2;
+        for (uint64_t g0 = 0; g0 < groups; g0 += gpl) {
+          const uint64_t t0 = g0 * a.group;
+          ChanArgs b = a;
+          b.count = (uint32_t)((uint64_t)a.count - t0 < gpl * a.group ? (uint64_t)a.count - t0 : gpl * a.group);
+          b.codes_in = a.codes_in + t0 * a.nwords;
+          b.ranges_in = a.ranges_in + g0 * 2 * a.dim;
+          b.out = (char*)a.out + t0 * a.dim * ES;
+          const uint64_t gb = ((uint64_t)b.count + a.group - 1) / a.group, nb = (gb * slabs + 3) / 4;
+          hipLaunchKernelGGL((chan_decode_w<B, SW, IO>), dim3((uint32_t)(nb < grid ? nb : grid)), dim3(kBlock), 0, s, b);
+        }
+        return;
+      }
       hipLaunchKernelGGL((chan_decode_w<B, SW, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
     };
     if (PITCH_KIVI_DEC_SLAB32 && IO == 0 && items64 <= 32768) go(std::integral_constant<int, 32>{});

@@ -95,6 +95,10 @@ int device_cu_count();
 // proportion to the workgroups they run).
 uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256, bool balance_rounds = false);
 
+// Rounds (grid-stride iterations per workgroup) per launch when a call of more rounds is split into several
+// launches, or 0 for one launch: PITCH_SLICE_ROUNDS when set (tuning aid), else dflt.
+uint64_t slice_rounds(uint64_t dflt);
+
 // Per-vector launch for one dimension D and I/O element type IO (0 float32, 1 float16, 2 bfloat16); one
 // object file per (D, IO) defines launch_vec_d<D>_io<IO>.
 #define PITCH_DECLARE_VEC_LAUNCH_IO(D, IO) \

@@ -1475,6 +1475,22 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
       const uint64_t need = (a.count + H::WAVES * H::V - 1) / (H::WAVES * H::V);
       const void* k = (const void*)&vec_encode_hs<D, B, POLAR, KBIAS>;
       const uint64_t grid = persistent_grid(k, need, 64 * H::WAVES);
+      const uint64_t rounds = KBIAS ? 0 : slice_rounds(0);
+      if (rounds && need > grid * rounds) {
+        constexpr int NW = (D * B + 31) / 32;
+        const uint64_t per = grid * rounds * H::WAVES * H::V;  // vectors per launch
+        for (uint64_t v0 = 0; v0 < a.count; v0 += per) {
+          VecArgs b = a;
+          b.count = a.count - v0 < per ? a.count - v0 : per;
+          b.in = (const float*)a.in + v0 * D;
+          b.codes_out = a.codes_out + v0 * NW;
+          b.scales_out = a.scales_out + v0;
+          const uint64_t nb = (b.count + H::WAVES * H::V - 1) / (H::WAVES * H::V);
+          hipLaunchKernelGGL((vec_encode_hs<D, B, POLAR, KBIAS>), dim3((uint32_t)(nb < grid ? nb : grid)),
+                             dim3(64 * H::WAVES), 0, s, b);
+        }
+        return hipGetLastError();
+      }
       hipLaunchKernelGGL((vec_encode_hs<D, B, POLAR, KBIAS>), dim3((uint32_t)grid), dim3(64 * H::WAVES), 0, s, a);
       return hipGetLastError();
     }
@@ -1498,7 +1514,22 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   } else {
     const void* k = (const void*)&vec_decode<D, B, POLAR, IO, KBIAS>;
     const uint64_t grid = persistent_grid(k, need, kBlock, true);
-    hipLaunchKernelGGL((vec_decode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    const uint64_t rounds = KBIAS ? 0 : slice_rounds(0);
+    if (rounds && need > grid * rounds) {
+      constexpr int NW = (D * B + 31) / 32;
+      const uint64_t per = grid * rounds * G::VPB;  // vectors per launch
+      for (uint64_t v0 = 0; v0 < a.count; v0 += per) {
+        VecArgs b = a;
+        b.count = a.count - v0 < per ? a.count - v0 : per;
+        b.codes_in = a.codes_in + v0 * NW;
+        b.scales_in = a.scales_in + v0;
+        b.out = (char*)a.out + v0 * D * Io<IO>::kBytes;
+        const uint64_t g = (b.count + G::VPB - 1) / G::VPB < grid ? (b.count + G::VPB - 1) / G::VPB : grid;
+        hipLaunchKernelGGL((vec_decode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)g), dim3(kBlock), 0, s, b);
+      }
+    } else {
+      hipLaunchKernelGGL((vec_decode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+    }
   }
   return hipGetLastError();
 }

@@ -170,3 +170,56 @@ def test_config5_k_share_one_call(q):
     """16 heads x 131072 tokens in one call: 65,536 (group, 64-channel) items, so the encoder takes its
     64-channel-slab variant (fewer items take the 32-channel one, covered above)."""
     channel_full(q, 16, 131072, 128, 4, 64, 5002, one_call=True)
+
+
+@pytest.mark.parametrize("d,bits,G", [(128, 4, 64), (64, 3, 64), (96, 2, 32), (128, 8, 128)])
+def test_kivi_long_call_partial_last_group(q, d, bits, G):
+    """One call long enough to be issued as several launches (the wave kernels split calls of more than two rounds),
+    ending in a partial group: codes, ranges and decode bit-exact against the oracle at the first, last and
+    launch-boundary-straddling groups and at random ones."""
+    import torch
+    import pitch_amd as P
+    dev = q.device
+    n = (1 << 21) + 37 if d <= 96 else (1 << 20) + 37
+    print(f"long KIVI call d={d} b={bits} G={G} tokens={n}", flush=True)
+    cfg = P.ChannelQuantConfig(d, bits, G)
+    groups = cfg.groupCount(n)
+    x = _gen(n, d, 7000 + d + bits, dev, "keys").contiguous()
+    codes = torch.zeros(n * cfg.codeStride, dtype=torch.uint8, device=dev)
+    ranges = torch.full((groups * 2 * d,), float("nan"), dtype=torch.float16, device=dev)
+    out = torch.full((n, d), float("nan"), dtype=torch.float32, device=dev)
+    q.enqueuePerChannelEncode(x, codes, ranges, n, cfg)
+    q.enqueuePerChannelDecode(codes, ranges, out, n, cfg)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(ranges).all())
+    # every group's fp16 range: the float32 min / max rounded to nearest even (pitch_reference.py:150-153), so a
+    # group skipped or written to the wrong place by any launch shows up
+    full = (n // G) * G
+    xg = x[:full].view(-1, G, d)
+    r = ranges.view(groups, 2, d)
+    assert torch.equal(r[:n // G, 0], xg.amin(1).half()) and torch.equal(r[:n // G, 1], xg.amax(1).half())
+    if n % G:
+        assert torch.equal(r[-1, 0], x[full:].amin(0).half()) and torch.equal(r[-1, 1], x[full:].amax(0).half())
+    # every element within half a step (plus the fp16 rounding of the range ends) of its input
+    rf = r.float()
+    step = ((rf[:, 1] - rf[:, 0]) / (2 ** bits - 1)).clamp_min(0)
+    tol = (0.5 * step * (1 + 1e-5) + 4.9e-4 * torch.maximum(rf[:, 0].abs(), rf[:, 1].abs()) + 6e-8)
+    tol = tol.repeat_interleave(G, 0)[:n]
+    assert not bool(((x - out).abs() > tol).any())
+    del xg, r, rf, step, tol
+    rng = np.random.default_rng(d + bits)
+    picks = sorted({0, 1, groups - 2, groups - 1} | {int(g) for g in rng.integers(0, groups, 40)}
+                   | {k * 256 + o for k in range(1, groups // 256) for o in (-1, 0)})
+    for g in picks:
+        t0 = g * G
+        m = min(G, n - t0)
+        X = x[t0:t0 + m].cpu().numpy()
+        ref_codes, ref_ranges = O.channel_encode(X, bits, G)
+        got_c = codes[t0 * cfg.codeStride:(t0 + m) * cfg.codeStride].cpu().numpy().tobytes()
+        assert got_c == O.pack_codes(ref_codes, bits), g
+        got_r = ranges[g * 2 * d:(g + 1) * 2 * d].cpu().numpy().view(np.uint16)
+        assert np.array_equal(got_r, ref_ranges.view(np.uint16).reshape(-1)), g
+        ref = O.channel_decode(ref_codes, ref_ranges, bits, G)
+        assert np.array_equal(out[t0:t0 + m].cpu().numpy().view(np.uint32), ref.view(np.uint32)), g
+    del x, codes, ranges, out
+    torch.cuda.empty_cache()
