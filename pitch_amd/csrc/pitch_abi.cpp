@@ -380,6 +380,14 @@ uint64_t slice_rounds(uint64_t dflt) {
   return env >= 0 ? (uint64_t)env : dflt;
 }
 
+uint64_t stream_decode_min_vectors() {
+  static const uint64_t v = [] {
+    const char* e = std::getenv("PITCH_STREAM_MIN_VECTORS");
+    return e ? (uint64_t)std::atoll(e) : (uint64_t)(1u << 22);
+  }();
+  return v;
+}
+
 uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size, bool balance_rounds) {
   static std::mutex mu;
   static std::unordered_map<const void*, int> occ_cache;

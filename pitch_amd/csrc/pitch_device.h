@@ -87,10 +87,15 @@ __device__ __forceinline__ double fma_t(double a, double b, double c) { return _
 #define PITCH_E128 32  // coordinates per lane at D = 128
 #endif
 
-template <int D>
+constexpr int default_lane_coords(int D) {
+  return D <= 16 ? D : (D == 64 ? PITCH_E64 : (D == 128 ? PITCH_E128 : (D < 64 ? 16 : 32)));
+}
+
+// EE: coordinates per lane (default: the decoders' and team encoders' choice for D)
+template <int D, int EE = default_lane_coords(D)>
 struct Geom {
   static constexpr int W = D >= 4 ? 4 : D;
-  static constexpr int E = D <= 16 ? D : (D == 64 ? PITCH_E64 : (D == 128 ? PITCH_E128 : (D < 64 ? 16 : 32)));
+  static constexpr int E = EE;
   static constexpr int T = D / E;
   static constexpr int CH = E / W;
   static constexpr int V = 64 / T;                  // vectors per wave
@@ -199,14 +204,14 @@ __device__ __forceinline__ void fmac_dpp16(float (&v)[E], float sg) {
 
 // Lanes of the team whose cross-lane stages fwht_f32_lane_signed runs as v_fmac_f32_dpp (distances 1 and 2,
 // when E is a multiple of 16).
-template <int D>
+template <int D, int EE = default_lane_coords(D)>
 __host__ __device__ constexpr int dpp_lane_bits() {
-  return (PITCH_DPP_FMAC && Geom<D>::E % 16 == 0) ? (3 & (Geom<D>::T - 1)) : 0;
+  return (PITCH_DPP_FMAC && Geom<D, EE>::E % 16 == 0) ? (3 & (Geom<D, EE>::T - 1)) : 0;
 }
 // Sign bit that lane t's results of fwht_f32_lane_signed carry: (-1)^popcount(t & dpp_lane_bits).
-template <int D>
+template <int D, int EE = default_lane_coords(D)>
 __device__ __forceinline__ uint32_t dpp_lane_sign_bit(int t) {
-  return (uint32_t)(__builtin_popcount((unsigned)(t & dpp_lane_bits<D>())) & 1) << 31;
+  return (uint32_t)(__builtin_popcount((unsigned)(t & dpp_lane_bits<D, EE>())) & 1) << 31;
 }
 
 // fwht<D, float> with the cross-lane stages at distances 1 and 2 done by fmac_dpp16. The high lane of each
@@ -215,16 +220,16 @@ __device__ __forceinline__ uint32_t dpp_lane_sign_bit(int t) {
 // equal the transform times (-1)^popcount(t & dpp_lane_bits<D>()), bit for bit up to that sign (b - a
 // and -(a - b) round alike; only a zero may come out with the other sign). The first PRE stages (bits
 // below PRE <= log2 W, inside a chunk) are taken as already applied by the caller.
-template <int D, int PRE = 0>
-__device__ __forceinline__ void fwht_f32_lane_signed(float (&v)[Geom<D>::E], int t) {
-  using G = Geom<D>;
+template <int D, int PRE = 0, int EE = default_lane_coords(D)>
+__device__ __forceinline__ void fwht_f32_lane_signed(float (&v)[EE], int t) {
+  using G = Geom<D, EE>;
   static_assert(PRE >= 0 && PRE <= G::LGW, "pre-applied stages lie inside a chunk");
   static_for<PRE, G::LGD>([&](auto bit_c) {
     constexpr int bit = decltype(bit_c)::value;
     if constexpr (bit >= G::LGW && bit < G::LGW + G::LGT) {
       constexpr int lm = 1 << (bit - G::LGW);
       const float sg = (t & lm) ? -1.0f : 1.0f;
-      if constexpr ((dpp_lane_bits<D>() & lm) != 0) {
+      if constexpr ((dpp_lane_bits<D, EE>() & lm) != 0) {
         static_for<0, G::E / 16>([&](auto o_c) { fmac_dpp16<lm, 16 * decltype(o_c)::value>(v, sg); });
       } else {
 #pragma unroll

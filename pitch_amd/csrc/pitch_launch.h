@@ -99,6 +99,10 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
 // launches, or 0 for one launch: PITCH_SLICE_ROUNDS when set (tuning aid), else dflt.
 uint64_t slice_rounds(uint64_t dflt);
 
+// Smallest call (vectors) the float32 D = 128 decode issues through the streaming decoder (PITCH_STREAM_MIN_VECTORS
+// when set, a tuning aid).
+uint64_t stream_decode_min_vectors();
+
 // Per-vector launch for one dimension D and I/O element type IO (0 float32, 1 float16, 2 bfloat16); one
 // object file per (D, IO) defines launch_vec_d<D>_io<IO>.
 #define PITCH_DECLARE_VEC_LAUNCH_IO(D, IO) \

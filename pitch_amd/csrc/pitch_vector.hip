@@ -613,48 +613,85 @@ struct DecTab {
   static constexpr int PRE = G == 4 ? 2 : (G == 2 ? 1 : 0);
 };
 
+// The decode table is built in two steps so that a kernel can issue its first code loads between them: the table's
+// source values are loaded first (load_dec_table), the entries are computed and written to LDS after
+// (write_dec_table). Loads complete in order, so waiting for the source values then leaves the code loads in flight.
 template <int D, int B, bool POLAR>
-__device__ __forceinline__ void build_dec_table(float* s_tab) {
+struct DecTabSrc {
   using TB = DecTab<B, POLAR, Geom<D>::W>;
+  static constexpr int ENTRIES = TB::G == 1 ? TB::L : TB::ENTRIES;  // entries (or table rows) built per call
+  static constexpr int R = (ENTRIES + kBlock - 1) / kBlock;         // entries per thread
+  static constexpr int S = POLAR ? 3 : (TB::G == 4 ? 4 : (TB::G == 2 ? 2 : 1));  // source values per entry
+  float v[R][S];
+};
+
+template <int D, int B, bool POLAR>
+__device__ __forceinline__ DecTabSrc<D, B, POLAR> load_dec_table() {
+  using TB = DecTab<B, POLAR, Geom<D>::W>;
+  using Src = DecTabSrc<D, B, POLAR>;
   constexpr int L = TB::L;
-  if constexpr (POLAR) {
-    constexpr int off = pitch_polar_offset(B);
-    const float* rad = pitch_polar_radius_tab + off;
-    const float* cs = pitch_polar_cos_tab + off;
-    const float* sn = pitch_polar_sin_tab + off;
-    if constexpr (TB::G == 2) {
-      for (int i = threadIdx.x; i < TB::ENTRIES; i += kBlock) {
-        const float r = rad[i & (L - 1)];
-        const float x = r * cs[i >> B], y = r * sn[i >> B];
-        s_tab[2 * i] = x + y;
-        s_tab[2 * i + 1] = x - y;
-      }
+  Src src;
+  // Threads past the last entry build the last entry again (the same value to the same place), so loads and writes
+  // are unconditional and the loads stay where they are written, ahead of the caller's next loads.
+#pragma unroll
+  for (int r = 0; r < Src::R; ++r) {
+    const int i = threadIdx.x + r * kBlock;
+    const int ic = i < Src::ENTRIES ? i : Src::ENTRIES - 1;
+    if constexpr (POLAR) {
+      constexpr int off = pitch_polar_offset(B);
+      const int ir = TB::G == 2 ? (ic & (L - 1)) : ic, ia = TB::G == 2 ? (ic >> B) : ic;
+      src.v[r][0] = pitch_polar_radius_tab[off + ir];
+      src.v[r][1] = pitch_polar_cos_tab[off + ia];
+      src.v[r][2] = pitch_polar_sin_tab[off + ia];
     } else {
-      for (int i = threadIdx.x; i < L; i += kBlock) {
-        s_tab[i] = rad[i];
-        s_tab[L + i] = cs[i];
-        s_tab[2 * L + i] = sn[i];
+      const float* cb = pitch_codebook_tab + pitch_codebook_offset(ilog2(D), B);
+      if constexpr (TB::G == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) src.v[r][j] = cb[(ic >> (2 * j)) & 3];
+      } else if constexpr (TB::G == 2) {
+        src.v[r][0] = cb[ic & (L - 1)];
+        src.v[r][1] = cb[ic >> B];
+      } else {
+        src.v[r][0] = cb[ic];
       }
     }
-  } else {
-    const float* cb = pitch_codebook_tab + pitch_codebook_offset(ilog2(D), B);
-    if constexpr (TB::G == 4) {
-      for (int i = threadIdx.x; i < 256; i += kBlock) {
-        const float q0 = cb[i & 3], q1 = cb[(i >> 2) & 3], q2 = cb[(i >> 4) & 3], q3 = cb[i >> 6];
-        const float a0 = q0 + q1, a1 = q0 - q1, a2 = q2 + q3, a3 = q2 - q3;
-        s_tab[4 * i] = a0 + a2;
-        s_tab[4 * i + 1] = a1 + a3;
-        s_tab[4 * i + 2] = a0 - a2;
-        s_tab[4 * i + 3] = a1 - a3;
-      }
-    } else if constexpr (TB::G == 2) {
-      for (int i = threadIdx.x; i < TB::ENTRIES; i += kBlock) {
-        const float x = cb[i & (L - 1)], y = cb[i >> B];
+  }
+  return src;
+}
+
+template <int D, int B, bool POLAR>
+__device__ __forceinline__ void write_dec_table(const DecTabSrc<D, B, POLAR>& src, float* s_tab) {
+  using TB = DecTab<B, POLAR, Geom<D>::W>;
+  using Src = DecTabSrc<D, B, POLAR>;
+  constexpr int L = TB::L;
+#pragma unroll
+  for (int r = 0; r < Src::R; ++r) {
+    const int i0 = threadIdx.x + r * kBlock;
+    const int i = i0 < Src::ENTRIES ? i0 : Src::ENTRIES - 1;
+    if constexpr (POLAR) {
+      const float rr = src.v[r][0];
+      if constexpr (TB::G == 2) {
+        const float x = rr * src.v[r][1], y = rr * src.v[r][2];
         s_tab[2 * i] = x + y;
         s_tab[2 * i + 1] = x - y;
+      } else {
+        s_tab[i] = rr;
+        s_tab[L + i] = src.v[r][1];
+        s_tab[2 * L + i] = src.v[r][2];
       }
+    } else if constexpr (TB::G == 4) {
+      const float q0 = src.v[r][0], q1 = src.v[r][1], q2 = src.v[r][2], q3 = src.v[r][3];
+      const float a0 = q0 + q1, a1 = q0 - q1, a2 = q2 + q3, a3 = q2 - q3;
+      s_tab[4 * i] = a0 + a2;
+      s_tab[4 * i + 1] = a1 + a3;
+      s_tab[4 * i + 2] = a0 - a2;
+      s_tab[4 * i + 3] = a1 - a3;
+    } else if constexpr (TB::G == 2) {
+      const float x = src.v[r][0], y = src.v[r][1];
+      s_tab[2 * i] = x + y;
+      s_tab[2 * i + 1] = x - y;
     } else {
-      for (int i = threadIdx.x; i < L; i += kBlock) s_tab[i] = cb[i];
+      s_tab[i] = src.v[r][0];
     }
   }
 }
@@ -716,12 +753,17 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   constexpr int kWaveOutFloats = G::V * kVecStride;
   __shared__ __attribute__((aligned(16))) float s_out[kLdsStore ? 4 * kWaveOutFloats : 4];
 
+  // per wave, the codes (V * NW words) and scales of its V vectors, loaded coalesced and read back per lane
+  constexpr int kWaveCodeWords = G::V * NW;
+  constexpr int NPL = (kWaveCodeWords + 63) / 64;  // code words each lane loads per batch
+  __shared__ uint32_t s_codes[kBlock / 64][kWaveCodeWords];
+  __shared__ float s_scale[kBlock / 64][G::V];
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int t = lane & (G::T - 1);
-  const int slot = (tid >> 6) * G::V + lane / G::T;
+  const int wave = tid >> 6, vw = lane / G::T;  // vector of this lane's team within the wave
 
-  build_dec_table<D, B, POLAR>(s_tab);
   const uint32_t fbits = p.lane_flips[t];
   // the transform's lane sign (fwht_f32_lane_signed) is folded into the random sign flips
   const uint32_t lane_sign = dpp_lane_sign_bit<D>(t);
@@ -738,45 +780,67 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
     wsh[k] = (uint32_t)(pos & 31);
     whi[k] = ((pos & 31) + CB > 32) ? wlo[k] + 1 : wlo[k];
   }
-  __syncthreads();
 
-  // Software pipeline: the codes and scale of the next iteration are loaded before the current one is
-  // transformed, so every wave keeps a batch of loads in flight while it computes. Loads and stores are
-  // unconditional: an index past the end is clamped to the last vector, whose decode such a lane then computes
-  // and writes to the last vector's place (the same bytes to the same address). With a fixed number of
-  // memory operations per iteration the compiler waits for the next batch's loads without waiting for the
-  // previous iteration's stores (gfx9 counts loads and stores together, in order).
+  // Software pipeline: the codes and scales of the next iteration are loaded before the current one is
+  // transformed, so every wave keeps a batch of loads in flight while it computes. A wave loads the contiguous code
+  // words of its V vectors with coalesced loads (NPL per lane; per-lane loads of each chunk's own words measured
+  // 15 % slower at a 17 GB footprint), stages them in LDS and each lane reads its chunks back. Loads and stores are
+  // unconditional: a wave whose vectors run past the end takes the last V vectors instead (the whole call when it
+  // has fewer), so it decodes and writes the same bytes to the same places as the wave that owns them. With a
+  // fixed number of memory operations per iteration the compiler waits for the next batch's loads without waiting
+  // for the previous iteration's stores (gfx9 counts loads and stores together, in order).
   struct Batch {
-    uint32_t lo[G::CH], hi[G::CH];
+    uint32_t w[NPL];
     float scale;
+    uint64_t wb;  // first vector of the wave's block
   };
   auto fetch = [&](uint64_t base) {
     Batch b;
-    const uint64_t v = base + slot;
-    const uint64_t vl = v < p.count ? v : p.count - 1;
-    b.scale = p.scales_in[vl];
-    const uint32_t* cw = p.codes_in + vl * NW;
+    const uint64_t nominal = base + (uint64_t)wave * G::V;
+    b.wb = p.count >= (uint64_t)G::V ? (nominal < p.count - G::V ? nominal : p.count - G::V) : 0;
+    const uint32_t* cw = p.codes_in + b.wb * NW;
+    // in a call of fewer than V vectors, words past the call's last one read the last word (never used)
+    const uint64_t last = p.count * NW - 1 - b.wb * NW;
 #pragma unroll
-    for (int k = 0; k < G::CH; ++k) {
-      b.lo[k] = cw[wlo[k]];
-      b.hi[k] = cw[whi[k]];
+    for (int m = 0; m < NPL; ++m) {
+      const uint64_t i = (uint64_t)(lane + 64 * m < kWaveCodeWords ? lane + 64 * m : kWaveCodeWords - 1);
+      b.w[m] = cw[i < last ? i : last];
     }
+    const uint64_t vs = b.wb + (uint64_t)(lane % G::V);
+    b.scale = p.scales_in[vs < p.count ? vs : p.count - 1];
     return b;
   };
-  // table lookups and the transform, shared by the full and the tail iteration
-  auto transform = [&](const Batch& b, float (&y)[G::E]) {
+  // the team's vector within the wave's block: vw, or the call's last vector for teams past the end (only in a
+  // call of fewer than V vectors)
+  auto local_vector = [&](const Batch& b) -> int {
+    const uint64_t lastv = p.count - 1 - b.wb;
+    return (uint64_t)vw < lastv ? vw : (int)lastv;
+  };
+  // stage the batch in LDS, read the lane's chunks back, table lookups and the transform
+  auto transform = [&](const Batch& b, float (&y)[G::E], float& scale) {
+#pragma unroll
+    for (int m = 0; m < NPL; ++m) {
+      const int i = lane + 64 * m < kWaveCodeWords ? lane + 64 * m : kWaveCodeWords - 1;
+      s_codes[wave][i] = b.w[m];
+    }
+    if (lane < G::V) s_scale[wave][lane] = b.scale;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int lv = local_vector(b);
+    const uint32_t* row = s_codes[wave] + lv * NW;
+    scale = s_scale[wave][lv];
 #pragma unroll
     for (int k = 0; k < G::CH; ++k)
-      decode_chunk<D, B, POLAR>(__builtin_amdgcn_alignbit(b.hi[k], b.lo[k], wsh[k]), s_tab, y + k * G::W);
+      decode_chunk<D, B, POLAR>(__builtin_amdgcn_alignbit(row[whi[k]], row[wlo[k]], wsh[k]), s_tab, y + k * G::W);
     fwht_f32_lane_signed<D, TB::PRE>(y, t);
   };
-  auto body = [&](const Batch& b, float (&y)[G::E], uint64_t base) {
-    const uint64_t v = base + slot < p.count ? base + slot : p.count - 1;
-    const float f = b.scale * DimConst<D>::kInvSqrtF;
+  auto body = [&](const Batch& b, float (&y)[G::E], float scale) {
+    const uint64_t v = b.wb + (uint64_t)local_vector(b);
+    const float f = scale * DimConst<D>::kInvSqrtF;
     if constexpr (kLdsStore) {
       // stage the wave's vectors in LDS, then write them back as contiguous 1 KB wave stores
       float* ws = s_out + (tid >> 6) * kWaveOutFloats;
-      const int vw = lane / G::T;  // vector within the wave
 #pragma unroll
       for (int k = 0; k < G::CH; ++k) {
         float o[G::W];
@@ -788,7 +852,7 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const uint64_t wbase = base + (uint64_t)(tid >> 6) * G::V;  // first vector of this wave
+      const uint64_t wbase = b.wb;  // first vector of this wave
       constexpr int K = Io<IO>::kPerChunk;  // elements per 16-byte store
       static_assert((G::V * D) % (64 * K) == 0, "whole 16-byte stores per lane");
 #pragma unroll
@@ -835,14 +899,25 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   // fetch B(i + 3), compute A(i + 2), ...
   const uint64_t stride = (uint64_t)gridDim.x * G::VPB;
   uint64_t base = (uint64_t)blockIdx.x * G::VPB;
-  if (base >= p.count) return;  // uniform per workgroup; no barrier follows
-  auto compute = [&](const Batch& b, uint64_t at) {
+  auto compute = [&](const Batch& b, uint64_t) {
     float y[G::E];
-    transform(b, y);
-    body(b, y, at);
+    float scale;
+    transform(b, y, scale);
+    body(b, y, scale);
   };
+  // The first two batches are requested before the decode table is built, so their latency overlaps the table's
+  // (a short launch pays one memory latency before its first stores instead of two); the barrier that publishes
+  // the table orders LDS only and leaves these loads in flight.
+  const auto tab_src = load_dec_table<D, B, POLAR>();
+  __builtin_amdgcn_sched_barrier(0);
   Batch ba = fetch(base);
   Batch bb = fetch(base + stride);
+  write_dec_table<D, B, POLAR>(tab_src, s_tab);
+  asm volatile("" ::"v"(fbits));  // the sign word (loaded before the batches) is waited for here, not after them
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if (base >= p.count) return;  // uniform per workgroup; no barrier follows
   compute(ba, base);
   for (;;) {
     base += stride;
@@ -861,9 +936,9 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
 }
 
 // Per-team-lane sign bits for the seed (cached per thread for the last seed).
-template <int D>
+template <int D, int EE = default_lane_coords(D)>
 void fill_lane_flips(uint32_t seed, uint32_t* out) {
-  using G = Geom<D>;
+  using G = Geom<D, EE>;
   thread_local uint32_t cached_seed = 0;
   thread_local bool have = false;
   thread_local uint32_t cached[32];
@@ -879,6 +954,96 @@ void fill_lane_flips(uint32_t seed, uint32_t* out) {
     have = true;
   }
   for (int t = 0; t < 32; ++t) out[t] = cached[t];
+}
+
+// ----------------------------------------------------------------------------------------------------
+// Streaming decoder for long float32 calls at D = 128. At a footprint of many GB the persistent decoder above runs
+// at ~5.0 TB/s, while a write stream with the same 10 % of reads reaches ~6 TB/s when the GPU holds 8 workgroups per
+// CU, each wave writes ~8 KB, and each launch gives every workgroup one block (so launches of ~2048 workgroups follow
+// each other; within one long launch the workgroups drift apart and reads and writes interleave at the memory).
+// This kernel is shaped for that: a team of 8 lanes per vector (16 coordinates per lane), two passes of 8 vectors per
+// wave, no output staging (a store instruction writes, for each of 8 vectors, the 128-byte line its team holds), at
+// most 64 VGPRs and a few KB of LDS; the host issues the call as launches of one block per workgroup.
+constexpr int kStreamE = 16;     // coordinates per lane at D = 128: teams of 8 lanes
+constexpr int kStreamPasses = 2; // vectors per wave = passes x 8
+constexpr int kStreamWaves = 8;  // waves per SIMD the kernel is built for (64 VGPRs)
+
+template <int D, int B, bool POLAR>
+__global__ __launch_bounds__(kBlock, kStreamWaves) void vec_decode_stream(VecArgs p) {
+  using G = Geom<D, kStreamE>;
+  using TB = DecTab<B, POLAR, G::W>;
+  static_assert(G::T == 8 && G::W == 4, "full 128-byte lines per team and chunk index");
+  constexpr int NW = (D * B + 31) / 32;
+  constexpr int CB = G::W * B;            // bits of codes per chunk (<= 32)
+  constexpr int P = kStreamPasses;
+  constexpr int VW = G::V * P;            // vectors per wave
+  constexpr int WORDS = VW * NW;          // their code words, contiguous
+  constexpr int NPL = (WORDS + 63) / 64;  // code words each lane loads
+  __shared__ __attribute__((aligned(16))) float s_tab[TB::FLOATS];
+  __shared__ uint32_t s_codes[kBlock / 64][WORDS];
+  __shared__ float s_scale[kBlock / 64][VW];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = lane & (G::T - 1), vw = lane / G::T;
+  // this wave's VW vectors; a wave past the end takes the call's last VW vectors (the same bytes to the same places
+  // as the wave that owns them), or the whole call when it has fewer
+  const uint64_t nominal = ((uint64_t)blockIdx.x * (kBlock / 64) + wave) * VW;
+  const uint64_t wb = p.count >= (uint64_t)VW ? (nominal < p.count - VW ? nominal : p.count - VW) : 0;
+  // table source values and the sign word first, then the coalesced code and scale loads; waiting for the former
+  // leaves the latter in flight (loads complete in order)
+  const auto tab_src = load_dec_table<D, B, POLAR>();
+  const uint32_t fbits = p.lane_flips[t];
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t w[NPL];
+  {
+    const uint32_t* cw = p.codes_in + wb * NW;
+    const uint64_t last = p.count * NW - 1 - wb * NW;  // only binding in a call of fewer than VW vectors
+#pragma unroll
+    for (int m = 0; m < NPL; ++m) {
+      const uint64_t i = (uint64_t)(lane + 64 * m < WORDS ? lane + 64 * m : WORDS - 1);
+      w[m] = cw[i < last ? i : last];
+    }
+  }
+  const uint64_t vs = wb + (uint64_t)(lane % VW);
+  const float scale_l = p.scales_in[vs < p.count ? vs : p.count - 1];
+  write_dec_table<D, B, POLAR>(tab_src, s_tab);
+  asm volatile("" ::"v"(fbits));
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+  for (int m = 0; m < NPL; ++m) s_codes[wave][lane + 64 * m < WORDS ? lane + 64 * m : WORDS - 1] = w[m];
+  if (lane < VW) s_scale[wave][lane] = scale_l;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint32_t lane_sign = dpp_lane_sign_bit<D, kStreamE>(t);
+  const uint64_t lastv = p.count - 1 - wb;
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const int lv0 = j * G::V + vw;
+    const int lv = (uint64_t)lv0 < lastv ? lv0 : (int)lastv;  // past the end (a short call): the last vector
+    const uint32_t* row = s_codes[wave] + lv * NW;
+    float y[G::E];
+#pragma unroll
+    for (int k = 0; k < G::CH; ++k) {
+      const int pos = CB * (k * G::T + t);
+      const int wl = pos >> 5, wh = (pos & 31) + CB > 32 ? wl + 1 : wl;
+      decode_chunk<D, B, POLAR>(__builtin_amdgcn_alignbit(row[wh], row[wl], (uint32_t)(pos & 31)), s_tab,
+                                y + k * G::W);
+    }
+    fwht_f32_lane_signed<D, TB::PRE, kStreamE>(y, t);
+    const float f = s_scale[wave][lv] * DimConst<D>::kInvSqrtF;
+    const uint64_t v = wb + (uint64_t)lv;
+#pragma unroll
+    for (int k = 0; k < G::CH; ++k) {
+      float o[G::W];
+#pragma unroll
+      for (int r = 0; r < G::W; ++r) {
+        const int e = k * G::W + r;
+        o[r] = __uint_as_float(__float_as_uint(y[e] * f) ^ (((fbits >> e) & 1u) << 31) ^ lane_sign);
+      }
+      store_elems<0, G::W>(p.out, v * D + G::W * (k * G::T + t), o, true);
+    }
+  }
 }
 
 // ----------------------------------------------------------------------------------------------------
@@ -1512,6 +1677,26 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
     const uint64_t grid = persistent_grid(k, need);
     hipLaunchKernelGGL((vec_encode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else {
+    if constexpr (D == 128 && IO == 0 && !KBIAS) {
+      if (a.count >= stream_decode_min_vectors()) {
+        using GS = Geom<D, kStreamE>;
+        constexpr uint64_t kVpb = (uint64_t)GS::V * kStreamPasses * (kBlock / 64);  // vectors per workgroup
+        const void* ks = (const void*)&vec_decode_stream<D, B, POLAR>;
+        const uint64_t blocks = (a.count + kVpb - 1) / kVpb;
+        const uint64_t grid = persistent_grid(ks, blocks);  // resident workgroups: one block each per launch
+        VecArgs b = a;
+        fill_lane_flips<D, kStreamE>(a.seed, b.lane_flips);
+        for (uint64_t b0 = 0; b0 < blocks; b0 += grid) {
+          const uint64_t nb = blocks - b0 < grid ? blocks - b0 : grid, v0 = b0 * kVpb;
+          b.count = a.count - v0 < nb * kVpb ? a.count - v0 : nb * kVpb;
+          b.codes_in = a.codes_in + v0 * ((D * B + 31) / 32);
+          b.scales_in = a.scales_in + v0;
+          b.out = (float*)a.out + v0 * D;
+          hipLaunchKernelGGL((vec_decode_stream<D, B, POLAR>), dim3((uint32_t)nb), dim3(kBlock), 0, s, b);
+        }
+        return hipGetLastError();
+      }
+    }
     const void* k = (const void*)&vec_decode<D, B, POLAR, IO, KBIAS>;
     const uint64_t grid = persistent_grid(k, need, kBlock, true);
     const uint64_t rounds = KBIAS ? 0 : slice_rounds(0);

@@ -1,0 +1,55 @@
+"""GPU parity of the streaming decoder that long float32 calls at d = 128 use (at least 2^22 vectors per call).
+
+Codes are random bytes (at d = 128 every bit width packs into whole words, so any byte pattern is a valid code
+stream) with random positive scales. One call of 2^22 + 4099 vectors (a ragged last launch) per method and bit
+width is checked:
+* sampled rows against the oracle's decode of the same codes: relative L2 <= 1e-5 (pitch_reference.py:104-107,
+  123-129);
+* the first and last 65536 vectors against the persistent decoder (separate calls below the streaming size, through
+  byte offsets): relative L2 <= 1e-6 per vector (both float32, different transform orders);
+* every output element written (pre-filled with NaN) and finite.
+"""
+import numpy as np
+import pytest
+
+from oracle import pitch_oracle as O
+from test_gpu_parity import max_rel_diff, REL_L2_BAR
+
+pytestmark = pytest.mark.gpu
+
+N = (1 << 22) + 4099
+D = 128
+
+
+@pytest.mark.parametrize("method", ["turboQuant", "polarQuant"])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 7, 8])
+def test_stream_decode(q, method, bits):
+    import torch
+    import pitch_amd as P
+    dev = q.device
+    print(f"streaming decode {method} b={bits} n={N}", flush=True)
+    cfg = P.QuantConfig(method, D, bits, 0x1234 + bits)
+    g = torch.Generator(device=dev).manual_seed(900 + bits + (method == "polarQuant"))
+    codes = torch.randint(0, 256, (N * cfg.codeStride,), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    scales = torch.exp(torch.randn(N, generator=g, device=dev))
+    out = torch.full((N, D), float("nan"), device=dev)
+    q.enqueueDecode(codes, scales, out, N, cfg)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    rng = np.random.default_rng(bits)
+    idx = np.unique(np.concatenate([np.arange(64), np.arange(N - 64, N), rng.integers(0, N, 512)]))
+    it = torch.from_numpy(idx).to(dev)
+    C = codes.view(N, cfg.codeStride)[it].cpu().numpy().tobytes()
+    S = scales[it].cpu().numpy().astype(np.float64)
+    ref = O.DECODERS[method](O.unpack_codes(C, len(idx), D, bits), S, bits, cfg.seed)
+    assert max_rel_diff(out[it].cpu().numpy(), ref, D) < REL_L2_BAR
+    m = 65536
+    for v0 in (0, N - m):
+        part = torch.empty(m, D, device=dev)
+        q.enqueueDecode(codes, scales, part, m, cfg, codesOffset=v0 * cfg.codeStride, scalesOffset=v0 * 4)
+        torch.cuda.synchronize()
+        a, b = out[v0:v0 + m].double(), part.double()
+        rel = ((a - b).square().sum(1) / b.square().sum(1).clamp_min(1e-300)).sqrt().max()
+        assert float(rel) < 1e-6, (v0, float(rel))
+    del codes, scales, out
+    torch.cuda.empty_cache()
