@@ -964,8 +964,14 @@ void fill_lane_flips(uint32_t seed, uint32_t* out) {
 // This kernel is shaped for that: a team of 8 lanes per vector (16 coordinates per lane), two passes of 8 vectors per
 // wave, no output staging (a store instruction writes, for each of 8 vectors, the 128-byte line its team holds), at
 // most 64 VGPRs and a few KB of LDS; the host issues the call as launches of one block per workgroup.
+#ifndef PITCH_STREAM_PASSES
+#define PITCH_STREAM_PASSES 2  // vectors per wave of the streaming decoder = passes x 8
+#endif
+#ifndef PITCH_STREAM_NT
+#define PITCH_STREAM_NT 1  // the streaming decoder writes with non-temporal stores
+#endif
 constexpr int kStreamE = 16;     // coordinates per lane at D = 128: teams of 8 lanes
-constexpr int kStreamPasses = 2; // vectors per wave = passes x 8
+constexpr int kStreamPasses = PITCH_STREAM_PASSES;
 constexpr int kStreamWaves = 8;  // waves per SIMD the kernel is built for (64 VGPRs)
 
 template <int D, int B, bool POLAR>
@@ -1041,7 +1047,7 @@ __global__ __launch_bounds__(kBlock, kStreamWaves) void vec_decode_stream(VecArg
         const int e = k * G::W + r;
         o[r] = __uint_as_float(__float_as_uint(y[e] * f) ^ (((fbits >> e) & 1u) << 31) ^ lane_sign);
       }
-      store_elems<0, G::W>(p.out, v * D + G::W * (k * G::T + t), o, true);
+      store_elems<0, G::W>(p.out, v * D + G::W * (k * G::T + t), o, PITCH_STREAM_NT);
     }
   }
 }
@@ -1683,7 +1689,8 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
         constexpr uint64_t kVpb = (uint64_t)GS::V * kStreamPasses * (kBlock / 64);  // vectors per workgroup
         const void* ks = (const void*)&vec_decode_stream<D, B, POLAR>;
         const uint64_t blocks = (a.count + kVpb - 1) / kVpb;
-        const uint64_t grid = persistent_grid(ks, blocks);  // resident workgroups: one block each per launch
+        // one block per resident workgroup per launch (1.5x, 2x, 3x and 4x as many measured 3-6 % slower)
+        const uint64_t grid = persistent_grid(ks, blocks);
         VecArgs b = a;
         fill_lane_flips<D, kStreamE>(a.seed, b.lane_flips);
         for (uint64_t b0 = 0; b0 < blocks; b0 += grid) {
