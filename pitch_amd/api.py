@@ -315,13 +315,15 @@ class CompressedBatch:
 
     @classmethod
     def from_json(cls, text: str) -> "CompressedBatch":
-        obj = json.loads(text)
-        if obj.get("formatVersion") != cls.formatVersion:
-            raise InvalidInput(f"Unsupported PITCH format version {obj.get('formatVersion')}; "
-                               f"expected {cls.formatVersion}")
-        c = obj["config"]
-        cfg = QuantConfig(c["method"], c["dim"], c["bits"], c["seed"])
-        return cls(cfg, base64.b64decode(obj["codes"]), np.array(obj["scales"], dtype=np.float32))
+        """Decodes a CompressedBatch as Swift's JSONDecoder does for the reference's CodingKeys
+        (CompressedBatch.swift:95-121, QuantConfig.swift:37-45): any key order, `codes` strict base64, `scales` a
+        number array, `config` {method, dim, bits, seed}; the config and sizes are validated."""
+        obj = _json_object(text)
+        _check_version(obj, cls.formatVersion, "")
+        c = _json_field(obj, "config", dict)
+        cfg = QuantConfig(_json_field(c, "method", str), _json_int(c, "dim"), _json_int(c, "bits"),
+                          _json_int(c, "seed"))
+        return cls(cfg, _json_base64(obj, "codes"), _json_numbers(obj, "scales", np.float32))
 
 
 @dataclass
@@ -418,13 +420,63 @@ class ChannelCompressedBlock:
 
     @classmethod
     def from_json(cls, text: str) -> "ChannelCompressedBlock":
+        """Decodes a ChannelCompressedBlock as Swift's JSONDecoder does for the reference's CodingKeys
+        (PerChannel.swift:143-168, :45-52): `codes` strict base64, `ranges` an array of 16-bit integers, `config`
+        {dim, bits, groupSize}."""
+        obj = _json_object(text)
+        _check_version(obj, cls.formatVersion, "per-channel ")
+        c = _json_field(obj, "config", dict)
+        cfg = ChannelQuantConfig(_json_int(c, "dim"), _json_int(c, "bits"), _json_int(c, "groupSize"))
+        return cls(cfg, _json_base64(obj, "codes"), _json_numbers(obj, "ranges", np.uint16))
+
+
+# JSON decoding with the reference's failure modes (Swift's DecodingError becomes InvalidInput here)
+def _json_object(text: str) -> dict:
+    try:
         obj = json.loads(text)
-        if obj.get("formatVersion") != cls.formatVersion:
-            raise InvalidInput(f"Unsupported PITCH per-channel format version {obj.get('formatVersion')}; "
-                               f"expected {cls.formatVersion}")
-        c = obj["config"]
-        cfg = ChannelQuantConfig(c["dim"], c["bits"], c["groupSize"])
-        return cls(cfg, base64.b64decode(obj["codes"]), np.array(obj["ranges"], dtype=np.uint16))
+    except (ValueError, TypeError) as e:
+        raise InvalidInput(f"not a JSON document: {e}") from e
+    if not isinstance(obj, dict):
+        raise InvalidInput("a container is a JSON object")
+    return obj
+
+
+def _json_field(obj: dict, key: str, kind):
+    if key not in obj:
+        raise InvalidInput(f"missing key '{key}'")
+    v = obj[key]
+    if not isinstance(v, kind) or isinstance(v, bool):
+        raise InvalidInput(f"'{key}' has the wrong type")
+    return v
+
+
+def _json_int(obj: dict, key: str) -> int:
+    v = _json_field(obj, key, (int, float))
+    if isinstance(v, float) and not v.is_integer():
+        raise InvalidInput(f"'{key}' is not an integer")
+    return int(v)
+
+
+def _check_version(obj: dict, version: int, what: str) -> None:
+    v = _json_int(obj, "formatVersion")
+    if v != version:
+        raise InvalidInput(f"Unsupported PITCH {what}format version {v}; expected {version}")
+
+
+def _json_base64(obj: dict, key: str) -> bytes:
+    try:
+        return base64.b64decode(_json_field(obj, key, str), validate=True)
+    except ValueError as e:   # binascii.Error
+        raise InvalidInput(f"'{key}' is not valid base64") from e
+
+
+def _json_numbers(obj: dict, key: str, dtype) -> np.ndarray:
+    v = _json_field(obj, key, list)
+    if not all(isinstance(x, (int, float)) and not isinstance(x, bool) for x in v):
+        raise InvalidInput(f"'{key}' must be an array of numbers")
+    if dtype == np.uint16 and not all(float(x).is_integer() and 0 <= x <= 0xFFFF for x in v):
+        raise InvalidInput(f"'{key}' must hold 16-bit unsigned integers")
+    return np.array(v, dtype=np.float64).astype(dtype) if dtype != np.uint16 else np.array(v, dtype=np.uint16)
 
 
 # ----------------------------------------------------------------------------------------- torch plumbing

@@ -131,7 +131,22 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
         l = make_float4(fminf(l.x, a.x), fminf(l.y, a.y), fminf(l.z, a.z), fminf(l.w, a.w));
         h = make_float4(fmaxf(h.x, b.x), fmaxf(h.y, b.y), fmaxf(h.z, b.z), fmaxf(h.w, b.w));
       }
-      const float lv[4] = {l.x, l.y, l.z, l.w}, hv[4] = {h.x, h.y, h.z, h.w};
+      float lv[4] = {l.x, l.y, l.z, l.w}, hv[4] = {h.x, h.y, h.z, h.w};
+      // an extreme of zero takes the sign of the channel's last zero in token order (numpy's min / max keep the
+      // last of equal values); rare, so the channel is scanned again
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (lv[r] == 0.0f || hv[r] == 0.0f) {
+          float zs = 0.0f;
+          for (uint32_t tk = 0; tk < n; ++tk) {
+            float v[1];
+            load_elems<IO, 1>(p.in, (uint64_t)first * dim + (uint64_t)tk * dim + 4u * tid + r, v);
+            if (v[0] == 0.0f) zs = v[0];
+          }
+          if (lv[r] == 0.0f) lv[r] = zs;
+          if (hv[r] == 0.0f) hv[r] = zs;
+        }
+      }
       uint16_t l16[4], h16[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -315,6 +330,26 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_KI
         h[k] = fmax_hw(h[k], __shfl_xor(h[k], off));
       }
     }
+    // an extreme of zero takes the sign of the channel's last zero in token order, as numpy's min / max keep the
+    // last of equal values (rare: the lanes of a channel take this branch together, and exchange only among
+    // themselves)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (l[k] == 0.0f || h[k] == 0.0f) {
+        int z = -1;
+#pragma unroll
+        for (int i = 0; i < TPL; ++i) {
+          const uint32_t tk = r + (uint32_t)RPI * i;
+          const float xv = k == 0 ? x[i].x : k == 1 ? x[i].y : k == 2 ? x[i].z : x[i].w;
+          if (tk < n && xv == 0.0f) z = max(z, (int)(2u * tk + (__float_as_uint(xv) >> 31)));
+        }
+#pragma unroll
+        for (int off = QW; off < 64; off <<= 1) z = max(z, __shfl_xor(z, off));
+        const float zs = (z & 1) ? -0.0f : 0.0f;
+        if (l[k] == 0.0f) l[k] = zs;
+        if (h[k] == 0.0f) h[k] = zs;
+      }
+    }
     uint16_t l16[4], h16[4];
     float bs[4], stc[4], inv[4];
     constexpr float kInvLevels = 1.0f / (float)((1 << B) - 1);
@@ -431,13 +466,15 @@ __global__ __launch_bounds__(kBlock) void chan_encode1(ChanArgs p) {
     const uint32_t n = min(p.group, p.count - first);
     const uint64_t src = (uint64_t)first * dim;  // element index of the group's first token
     for (uint32_t ch = tid; ch < dim; ch += kBlock) {
+      // in token order, keeping the later of equal values as numpy's min / max do (a zero extreme takes the sign
+      // of the channel's last zero)
       float lo = __builtin_inff(), hi = -__builtin_inff();
       for (uint32_t tk = 0; tk < n; ++tk) {
         float xv[1];
         load_elems<IO, 1>(p.in, src + (uint64_t)tk * dim + ch, xv);
         const float x = xv[0];
-        lo = fminf(lo, x);
-        hi = fmaxf(hi, x);
+        lo = lo < x ? lo : x;
+        hi = hi > x ? hi : x;
       }
       const uint16_t l16 = f2h_bits(lo), h16 = f2h_bits(hi);
       p.ranges_out[(uint64_t)g * 2u * dim + ch] = l16;

@@ -6,10 +6,12 @@ At full size the oracle cannot check every vector in seconds, so each case check
   decode of the kernel's own codes within 1e-5 relative L2 (per-vector) or bit-exact (KIVI);
 * that encoding a slice through byte offsets into the whole cache gives the same bytes as the whole call;
 * the decode/encode error statistics (Theorem 1 band for TurboQuant on Gaussian rows).
-Inputs are generated on the device with torch's seeded generator. Sizes follow the BASELINE configs: config 2
-(32768 x 12 x 64, TurboQuant b = 2/3/4), config 3 (8 heads x 32768 x 64 KIVI keys, G = 64, b = 4), config 4
-(917,504 x 128, TurboQuant and PolarQuant b = 4), config 5 at one GPU's share under 8-way tensor parallelism
-(32 layers x 131072 x 128: V TurboQuant b = 3, K KIVI b = 4), and one call of more than 2^32 floats.
+Inputs are generated on the device with torch's seeded generator, with the configs' distributions (config 4: a
+per-head bias and outlier channels; KIVI keys: per-head scales, outliers and bias). Sizes follow the BASELINE
+configs: config 2 (32768 x 12 x 64, TurboQuant b = 2/3/4), config 3 (8 heads x 32768 x 64 KIVI keys, G = 64,
+b = 4), config 4 (917,504 x 128, TurboQuant and PolarQuant b = 4), config 5 at one GPU's share under 8-way tensor
+parallelism (32 layers x 131072 x 128: V TurboQuant b = 3, K KIVI b = 4), and one call of more than 2^32 floats.
+Config 5 at its full single-GPU size is in test_gpu_config5.py.
 """
 import math
 
@@ -29,18 +31,20 @@ def _gen(n, d, seed, dev, kind):
     if kind == "gauss":
         return torch.randn(n, d, generator=g, device=dev)
     if kind == "t5":       # Student-t nu = 5 times a per-row log-uniform factor in [0.5, 4]
-        z = torch.randn(n, d, generator=g, device=dev)
-        chi = torch.randn(n, d, 5, generator=g, device=dev).square_().sum(-1) if n * d <= 64 << 20 else None
-        if chi is None:    # large sizes: a cheaper heavy-tailed stand-in with the same support
-            u = torch.rand(n, d, generator=g, device=dev)
-            chi = 5 * (u.clamp_min(1e-6) ** 0.8)
+        from pitch_amd import workloads as W
+        x = W.student_t(torch, (n, d), 5.0, g, dev)
         f = torch.exp(torch.empty(n, 1, device=dev).uniform_(math.log(0.5), math.log(4), generator=g))
-        return z / torch.sqrt(chi / 5) * f
+        return x.mul_(f)
     if kind == "keys":     # per-channel scales, a few outlier channels and a per-channel bias
         z = torch.randn(n, d, generator=g, device=dev)
         s = torch.exp(torch.randn(d, generator=g, device=dev))
         s[:4] *= 20
         return z * s + 3 * torch.randn(d, generator=g, device=dev)
+    if kind == "qwen":     # config 4: N(0,1) + per-head bias N(0, 5^2) + 2 outlier channels per head at 30x
+        from pitch_amd import workloads as W
+        heads = 56         # 28 layers x 2 KV heads, head-major rows
+        assert n % heads == 0
+        return W.qwen_keys(torch, g, dev, heads, n // heads, d).reshape(n, d)
     raise ValueError(kind)
 
 
@@ -98,7 +102,13 @@ def test_config2_gpt2_v_cache(q, bits):
 
 @pytest.mark.parametrize("method", ["turboQuant", "polarQuant"])
 def test_config4_qwen_d128(q, method):
-    per_vector_full(q, method, 28 * 2 * 16384, 128, 4, 4000, "gauss", theorem1=(method == "turboQuant"))
+    """Config 4 on its own key distribution (a per-head bias and two outlier channels per head)."""
+    per_vector_full(q, method, 28 * 2 * 16384, 128, 4, 4000, "qwen")
+
+
+def test_config4_shape_gaussian_theorem1(q):
+    """Config 4's shape on N(0,1) rows, where TurboQuant's mean error is inside the Theorem-1 band."""
+    per_vector_full(q, "turboQuant", 28 * 2 * 16384, 128, 4, 4001, "gauss", theorem1=True)
 
 
 def test_config5_v_share(q):
@@ -117,7 +127,10 @@ def channel_full(q, heads, tokens, d, bits, G, seed, one_call=False):
     print(f"full-size KIVI heads={heads} tokens={tokens} d={d} b={bits} G={G}", flush=True)
     cfg = P.ChannelQuantConfig(d, bits, G)
     groups = cfg.groupCount(tokens)
-    x = _gen(heads * tokens, d, seed, dev, "keys").contiguous()
+    # the config-3 distribution drawn per head: each head has its own scales, outlier channels and bias
+    from pitch_amd import workloads as W
+    gk = torch.Generator(device=dev).manual_seed(seed)
+    x = W.biased_keys(torch, gk, dev, heads, tokens, d, first_head=seed).reshape(heads * tokens, d).contiguous()
     codes = torch.empty(heads * tokens * cfg.codeStride, dtype=torch.uint8, device=dev)
     ranges = torch.empty(heads * groups * cfg.rangeStride // 2, dtype=torch.float16, device=dev)
     out = torch.empty(heads * tokens, d, dtype=torch.float32, device=dev)

@@ -117,6 +117,67 @@ def test_batch_json_round_trip_and_version():
         P.CompressedBatch.from_json(bad)
 
 
+def _swift_base64(data: bytes) -> str:
+    """Base64 as Swift's JSONEncoder writes Data (.base64), with '/' escaped as '\\/' (its default)."""
+    import base64
+    return base64.b64encode(data).decode().replace("/", "\\/")
+
+
+def test_batch_json_as_swift_writes_it():
+    """A CompressedBatch document laid out by the reference's CodingKeys (CompressedBatch.swift:95-121:
+    formatVersion, config, codes, scales; QuantConfig.swift:37: method, dim, bits, seed), written the way Swift's
+    JSONEncoder does (Data as base64 with escaped slashes, [Float] as shortest round-trip numbers, keys in any
+    order, compact or pretty-printed), parses to the same batch; malformed documents raise InvalidInput."""
+    codes = bytes([0xFB, 0xFF, 0xBF, 0x00, 0x01, 0x02, 0x03, 0xFE, 0x3F, 0x10, 0x20, 0x30])
+    b64 = _swift_base64(codes)
+    assert "\\/" in b64
+    compact = ('{"scales":[1.5,0.1,3.1415927],"formatVersion":3,"codes":"%s","config":{"seed":1346982979,"bits":4,'
+               '"method":"turboQuant","dim":8}}' % b64)
+    pretty = ('{\n  "codes" : "%s",\n  "config" : {\n    "bits" : 4,\n    "dim" : 8,\n    "method" : "turboQuant",\n'
+              '    "seed" : 1346982979\n  },\n  "formatVersion" : 3,\n  "scales" : [\n    1.5,\n    0.1,\n'
+              '    3.1415927\n  ]\n}' % b64)
+    for doc in (compact, pretty):
+        b = P.CompressedBatch.from_json(doc)
+        assert b.codes == codes and b.count == 3
+        assert (b.config.method, b.config.dim, b.config.bits, b.config.seed) == ("turboQuant", 8, 4, 0x50495443)
+        assert np.array_equal(b.scales, np.array([1.5, 0.1, 3.1415927], np.float32))
+        assert P.CompressedBatch.from_json(b.to_json()) == b
+    bad = [compact.replace('"formatVersion":3', '"formatVersion":2'),       # other version
+           compact.replace(b64, "@@@@" + b64[4:]),                          # not base64
+           compact.replace('"scales":[1.5,0.1,3.1415927],', ""),            # missing key
+           compact.replace("1.5,", '"1.5",'),                               # wrong element type
+           compact.replace('"turboQuant"', '"fooQuant"'),                   # unknown method
+           compact.replace('[1.5,0.1,3.1415927]', '[1.5,0.1]'),             # scales do not match the codes
+           "[]", "not json"]
+    for doc in bad:
+        with pytest.raises(P.InvalidInput):
+            P.CompressedBatch.from_json(doc)
+    with pytest.raises(P.InvalidDimension):
+        P.CompressedBatch.from_json(compact.replace('"dim":8', '"dim":12'))
+
+
+def test_block_json_as_swift_writes_it():
+    """A ChannelCompressedBlock document laid out by the reference's CodingKeys (PerChannel.swift:143-168:
+    formatVersion, config, codes, ranges; :45: dim, bits, groupSize; ranges as [UInt16]), as Swift's JSONEncoder
+    writes it, parses to the same block, including a partial last group and a negative-zero minimum."""
+    codes = bytes(range(0xF0, 0xFC))                        # 3 tokens x codeStride 4
+    ranges = [0xBC00, 0x0000, 0x3C00, 0x3C00, 0x4000, 0x4000,  # group 0: min row, max row
+              0x8000, 0x3800, 0xC000, 0x0000, 0x3C00, 0x0000]  # group 1 (one token): -0.0 .. 0.0, 0.5 .. 1, -2 .. 0
+    doc = ('{"ranges":[%s],"formatVersion":1,"config":{"groupSize":2,"dim":3,"bits":4},"codes":"%s"}'
+           % (",".join(str(r) for r in ranges), _swift_base64(codes)))
+    blk = P.ChannelCompressedBlock.from_json(doc)
+    assert blk.codes == codes and blk.count == 3 and blk.groupCount == 2
+    assert (blk.config.dim, blk.config.bits, blk.config.groupSize) == (3, 4, 2)
+    assert blk.ranges.dtype == np.uint16 and blk.ranges.tolist() == ranges
+    assert blk.range(1, 0) == (-0.0, 0.0) and np.signbit(blk.range(1, 0)[0])
+    assert P.ChannelCompressedBlock.from_json(blk.to_json()) == blk
+    for bad in (doc.replace('"formatVersion":1', '"formatVersion":3'), doc.replace("48128", "70000"),
+                doc.replace("48128", "-1"), doc.replace('"groupSize":2', '"groupSize":0'),
+                doc.replace("15360,15360", "15360")):
+        with pytest.raises(P.InvalidInput):
+            P.ChannelCompressedBlock.from_json(bad)
+
+
 # ----------------------------------------------------------------------------- ChannelCompressedBlock
 def _block(cfg, n, seed=0):
     rng = np.random.default_rng(seed)

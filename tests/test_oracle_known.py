@@ -290,3 +290,29 @@ def test_near_boundary_classifiers():
     Xk = np.array([[0.0], [1.0], [0.5], [0.25]], np.float32)
     mk = O.channel_near_boundary(Xk, 2, 4)[:, 0]
     assert list(mk) == [False, False, True, False]
+
+
+def test_numpy_min_max_keep_the_last_of_equal_values():
+    """The per-channel ranges follow numpy's ndarray.min / max over a group's tokens (pitch_reference.py:150-153),
+    which keep the last of equal values: an extreme of zero carries the sign of the channel's last zero. The GPU
+    encoders reproduce this rule (tests/test_gpu_signed_zero.py); here it is pinned for the numpy the oracle runs
+    on, in 1-D reductions and in the (tokens, channels) axis-0 reductions of a 64-token group."""
+    import numpy as np
+    # (column, expected sign of the minimum if it is zero, expected sign of the maximum if it is zero)
+    cases = [([0.0, -0.0, 1.0], "-", None), ([-0.0, 0.0, 1.0], "+", None), ([1.0, -0.0, 0.0, 2.0], "+", None),
+             ([1.0, 0.0, -0.0, 2.0], "-", None), ([-1.0, 0.0, -0.0], None, "-"), ([-1.0, -0.0, 0.0], None, "+"),
+             ([0.0, -0.0, 0.0, -0.0], "-", "-"), ([-0.0, 0.0], "+", "+")]
+    for col, lo, hi in cases:
+        a = np.array(col, np.float32)
+        blk = np.empty((64, 9), np.float32)
+        blk[:] = 7.0 if lo is not None and hi is None else -7.0   # fillers that do not move a zero extreme
+        if lo is not None and hi is not None:
+            blk[:] = a[-1]
+        blk[:len(a), 5] = a
+        if lo is not None and hi is not None:   # all zeros: pad with copies of the last zero
+            blk[len(a):, 5] = a[-1]
+        for got_lo, got_hi in ((a.min(), a.max()), (blk.min(0)[5], blk.max(0)[5])):
+            if lo is not None:
+                assert got_lo == 0 and bool(np.signbit(got_lo)) == (lo == "-"), (col, "min")
+            if hi is not None:
+                assert got_hi == 0 and bool(np.signbit(got_hi)) == (hi == "-"), (col, "max")
