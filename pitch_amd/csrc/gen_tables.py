@@ -10,6 +10,8 @@
   reference's operation order and rounded once to float32.
 * The bucket tables of the TurboQuant encoder (lut_for) and the float32 atan polynomials of the PolarQuant
   encoder's fast angle path (atan_poly), each checked here against the exact answer.
+* For the PolarQuant encoder's angle codes at b <= 5: the tangents of the sector boundaries inside the first
+  octant, RN(tan((k - 1/2) 2 pi / 2^b)) for k = 1 .. ceil(2^b / 8) (sector_tans).
 
 Usage: python gen_tables.py <codebooks.json> <out.inc>
 """
@@ -112,6 +114,19 @@ def atan_poly(deg: int = 7):
     return c32
 
 
+SECTOR_BITS = range(2, 6)  # bit widths whose angle codes the encoder decides by boundary comparisons
+
+
+def sector_tans(b: int) -> np.ndarray:
+    """float32 tangents of the angle-code boundaries (k - 1/2) * 2 pi / 2^b inside the first octant [0, pi / 4]
+    (pitch_reference.py:117 rounds theta / (2 pi) * 2^b + 0.5 down, so code k starts half a sector below k).
+    At b = 2 the only boundary is the octant's edge, pi / 4, whose tangent is 1."""
+    k = np.arange(1, ((1 << b) + 7) // 8 + 1, dtype=np.float64)
+    t = np.tan((k - 0.5) * 2 * np.pi / (1 << b)).astype(np.float32)
+    assert np.all(t <= 1) and np.all(np.diff(t) > 0)
+    return t
+
+
 def main(src: str, dst: str) -> None:
     books = json.loads(open(src).read())
     cb_all, edge_all = [], []
@@ -189,6 +204,9 @@ def main(src: str, dst: str) -> None:
     lines.append(f"static constexpr float pitch_atan_coef[9][9] = {{{','.join(rows)}}};")
     lines.append("static constexpr int pitch_atan_degree(int bits) { return "
                  + " : ".join(f"bits == {b} ? {d}" for b, d in ATAN_DEG.items()) + " : 7; }")
+    # sector-boundary tangents: row b - 2 holds the ceil(2^b / 8) tangents of bit width b (zero-padded)
+    rows = ["{" + _floats(list(sector_tans(b)) + [0.0] * (4 - len(sector_tans(b)))) + "}" for b in SECTOR_BITS]
+    lines.append(f"static constexpr float pitch_sector_tan[{len(rows)}][4] = {{{','.join(rows)}}};")
     for b in BITS:
         assert poffs[b] == (1 << b) - 4
     open(dst, "w").write("\n".join(lines) + "\n")

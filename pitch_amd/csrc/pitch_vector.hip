@@ -129,6 +129,56 @@ __device__ __forceinline__ uint32_t guarded_code(float t, bool& ok) {
   return (uint32_t)t;
 }
 
+// floor(u + g) for u + g >= 0 from u = t - g, when t lies at least g from an integer: then fract(u) < 1 - 2g
+// and floor(u) = floor(t) (ok is left alone); else ok = false. A NaN u fails.
+__device__ __forceinline__ uint32_t guarded_code_shifted(float u, float g, bool& ok) {
+  ok = ok && __builtin_amdgcn_fractf(u) < 1.f - 2.f * g;
+  return (uint32_t)u;
+}
+
+// Guard of the staged-stage encoder's radius t = sqrt_f32(fma(a, a, RN(c c))) * RN((2^B - 1) / rmax) + 0.5 on the
+// float32 pair (a, c), whose error is under (2^B - 1) * 4e-7 (the pair's roundings, two in the squared radius,
+// a square root within an ulp, the scale's rounding and the fused add): (2^B - 1) * 1.2e-6, three times that.
+template <int B>
+constexpr float polar_radius_guard() { return float((1 << B) - 1) * 1.2e-6f; }
+
+// Angle codes at B <= 5 by comparisons with the sector boundaries instead of an arctangent. Code k of
+// floor(theta / (2 pi) * 2^B + 0.5) mod 2^B (pitch_reference.py:117) covers the directions from (k - 1/2) to
+// (k + 1/2) sectors. In the first octant, with mx = max(|a|, |c|) and mn = min(|a|, |c|), the direction's
+// angle atan(mn / mx) lies past boundary j (angle (j - 1/2) 2 pi / 2^B, j = 1 .. ceil(2^B / 8)) exactly when
+// d_j = mn - mx tan_j > 0. d_j = fma(mx, -RN(tan_j), mn) errs by under 2.4e-7 mx (the roundings of mn, mx and
+// tan_j to float32, and of the fused result) for mx >= 1e-30 (products far from float32's subnormals), so a
+// decision with |d_j| > 2e-6 mx is certain; otherwise, or for mx < 1e-30 (the origin included), the float64
+// path decides. The octant's reflections map the first-octant code n1 to L/4 - n1 (|c| > |a|), L/2 - n
+// (a negative) and L - n (c negative), exact on integers: a first-octant direction at a boundary fails the
+// guard, and for B >= 3 the octant edges are sector centres; at B = 2 the edge pi / 4 is the one boundary
+// (tan = 1). A zero of either sign on an axis reflects onto itself, so the sign bit alone is tested.
+template <int B>
+constexpr int polar_sector_bounds() { return ((1 << B) + 7) / 8; }
+constexpr float kSectorGuard = 2e-6f;
+
+template <int B>
+__device__ __forceinline__ uint32_t sector_code(float c, float a, bool& ok) {
+  constexpr int L = 1 << B, K = polar_sector_bounds<B>();
+  static_assert(B >= 2 && B <= 5 && K <= 4, "sector boundaries of the first octant");
+  const float ax = __builtin_fabsf(a), ay = __builtin_fabsf(c);
+  const float mx = __builtin_fmaxf(ax, ay), mn = __builtin_fminf(ax, ay);
+  const float gm = kSectorGuard * mx;
+  bool good = mx >= 1e-30f;
+  uint32_t n = 0;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const float dj = __builtin_fmaf(mx, -pitch_sector_tan[B - 2][j], mn);
+    n += dj > 0.f ? 1u : 0u;
+    good = good && __builtin_fabsf(dj) > gm;
+  }
+  ok = ok && good;
+  n = ay > ax ? (uint32_t)(L / 4) - n : n;
+  n = __float_as_uint(a) >> 31 ? (uint32_t)(L / 2) - n : n;
+  n = __float_as_uint(c) >> 31 ? (uint32_t)L - n : n;
+  return n & (uint32_t)(L - 1);
+}
+
 // y / sqrt(D) rounded as the reference's division (pitch_reference.py:33).
 template <int D>
 __device__ __forceinline__ double div_sqrt_d(double y) {
@@ -1424,48 +1474,69 @@ __device__ __forceinline__ void hs_stage(const VecArgs& p, const u32x4 (&pf)[Hs<
 // depend only on the directions and on the radii relative to rmax, which the division by sqrt(d) of rotate()
 // leaves unchanged (up to float64 rounding, far inside the near-boundary band): the pairs come from the
 // unnormalised transform and only rmax is scaled. Each pair is decided in float32 on the unscaled pair (the
-// angle is scale-invariant; the radius is multiplied by (2^B - 1) / rmax) when its t values are at least
-// kPolarGuard from an integer; otherwise, for a pair at the origin, or for a vector whose rmax lies outside
-// [1e-30, 1e30] (where the unscaled float32 pair could lose precision), the float64 path in the reference's
-// order decides. A NaN or an overflow in the float32 path fails the guard as well.
+// angle is scale-invariant; the radius is multiplied by (2^B - 1) / rmax): the radius behind
+// polar_radius_guard, the angle by sector_code at B <= 5 and by angle_sectors behind kPolarGuard above. A pair
+// that fails a guard, and every pair of a vector whose rmax lies outside [1e-30, 1e30] (where the unscaled
+// float32 pair could lose precision), is decided afterwards by the float64 path in the reference's order, in
+// one block per lane that the waves enter only when one of their lanes has such a pair.
+template <int B, int NWL>
+__device__ __forceinline__ void put_code(uint32_t (&w)[NWL], int pos, uint32_t cd, bool clear) {
+  const int wi = pos >> 5, sh = pos & 31;
+  constexpr uint32_t M = (1u << B) - 1u;
+  if (clear) w[wi] &= ~(M << sh);
+  w[wi] |= cd << sh;
+  if (sh + B > 32) {
+    if (clear) w[wi + 1] &= ~(M >> (32 - sh));
+    w[wi + 1] |= cd >> (32 - sh);
+  }
+}
+
 template <int D, int T, int B, int NWL>
 __device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w)[NWL]) {
   constexpr int E = Hs<D, T>::E, NP = E / 2, L = 1 << B;
+  constexpr bool kSectors = B <= 5;
+  constexpr float kRg = polar_radius_guard<B>();
   fwht_contig<E, 1, double>(x, 0);
   double m = 0.0;
 #pragma unroll
-  for (int q = 0; q < NP; ++q) {
-    const double r2 = __builtin_fma(x[2 * q], x[2 * q], x[2 * q + 1] * x[2 * q + 1]);
-    m = r2 > m ? r2 : m;
-  }
-  m = team_reduce<T>(m, [](double a, double b) { return a > b ? a : b; });
+  for (int q = 0; q < NP; ++q) m = __builtin_fmax(__builtin_fma(x[2 * q], x[2 * q], x[2 * q + 1] * x[2 * q + 1]), m);
+  m = team_reduce<T>(m, [](double a, double b) { return __builtin_fmax(a, b); });
   const double rmax = __builtin_sqrt(m);  // = the largest radius: sqrt is monotone
   const double safe = rmax > 0.0 ? rmax : 1.0;
   const bool inrange = rmax > 1e-30 && rmax < 1e30;
   const float sr = (float)(double(L - 1) / safe);
 #pragma unroll
   for (int i = 0; i < NWL; ++i) w[i] = 0u;
+  bool okq[NP];
+  bool all = true;
 #pragma unroll
   for (int q = 0; q < NP; ++q) {
     const float af = (float)x[2 * q], cf = (float)x[2 * q + 1];
     const float rf = __builtin_amdgcn_sqrtf(__builtin_fmaf(af, af, cf * cf));
-    // rf <= rmax up to rounding, so t_r < 2^B - 1/2 + 1e-5 and its floor needs no clip; a pair at the origin
-    // gives a NaN angle (0 * 1/0), which fails the guard
+    // rf <= rmax up to rounding, so t_r < 2^B - 1/2 + 1e-5 and its floor needs no clip
     bool ok = inrange;
-    uint32_t cr = guarded_code(__builtin_fmaf(rf, sr, 0.5f), ok);
-    uint32_t ca = guarded_code(angle_sectors<B>(cf, af) + 0.5f, ok) & (uint32_t)(L - 1);
-    if (!ok) {  // rare: one shared out-of-line copy
-      const double a = x[2 * q], c = x[2 * q + 1];
-      const uint2 cc = polar_codes_exact<B>(a, c, __builtin_fma(a, a, c * c), safe);
-      cr = cc.x;
-      ca = cc.y;
+    const uint32_t cr = guarded_code_shifted(__builtin_fmaf(rf, sr, 0.5f - kRg), kRg, ok);
+    uint32_t ca;
+    if constexpr (kSectors) {
+      ca = sector_code<B>(cf, af, ok);
+    } else {  // a pair at the origin gives a NaN angle (0 * 1/0), which fails the guard
+      ca = guarded_code_shifted(angle_sectors<B>(cf, af) + (0.5f - kPolarGuard), kPolarGuard, ok) &
+           (uint32_t)(L - 1);
     }
+    okq[q] = ok;
+    all = all && ok;
+    put_code<B>(w, 2 * q * B, cr, false);
+    put_code<B>(w, (2 * q + 1) * B, ca, false);
+  }
+  if (!all) {  // rare
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t cd = h ? ca : cr;
-      const int pos = (2 * q + h) * B, wi = pos >> 5, sh = pos & 31;
-      w[wi] |= cd << sh;
-      if (sh + B > 32) w[wi + 1] |= cd >> (32 - sh);
+    for (int q = 0; q < NP; ++q) {
+      if (!okq[q]) {
+        const double a = x[2 * q], c = x[2 * q + 1];
+        const uint2 cc = polar_codes_exact<B>(a, c, __builtin_fma(a, a, c * c), safe);
+        put_code<B>(w, 2 * q * B, cc.x, true);
+        put_code<B>(w, (2 * q + 1) * B, cc.y, true);
+      }
     }
   }
   return (float)div_sqrt_d<D>(rmax);
@@ -1562,7 +1633,7 @@ __device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLu
 #define PITCH_HS_WAVES128 3
 #endif
 #ifndef PITCH_HS_WAVES_POLAR
-#define PITCH_HS_WAVES_POLAR 2  // PolarQuant is bound by its arithmetic, not by latency
+#define PITCH_HS_WAVES_POLAR 3  // PolarQuant: 3 (a few spills, in the float64 fallback call only; LDS allows 3)
 #endif
 template <int D, bool POLAR, bool KBIAS>
 constexpr int hs_waves() {

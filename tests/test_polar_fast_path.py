@@ -6,14 +6,16 @@ decides. There are two formulations:
 * the team encoder (vec_encode; 16-bit inputs and dimensions other than 64 and 128) scales each pair by
   1 / rmax in float64 before rounding it to float32, and takes the angle in turns (angle_turns);
 * the staged-stage encoder (vec_encode_hs; float32 inputs at d = 64 and 128) rounds the unscaled pair of the
-  unnormalised transform to float32, multiplies the radius by RN((2^b - 1) / rmax), and takes the angle in
-  sector units (angle_sectors: the factor 2^b / (2 pi) folded into the polynomial's coefficients).
+  unnormalised transform to float32, multiplies the radius by RN((2^b - 1) / rmax) behind a guard of
+  (2^b - 1) * 1.2e-6, and takes the angle at b <= 5 from the signs of d_j = fma(mx, -RN(tan_j), mn) against
+  the sector boundaries of the first octant (sector_code, guard |d_j| > 2e-6 mx), above that in sector units
+  (angle_sectors: the factor 2^b / (2 pi) folded into the polynomial's coefficients).
 This test evaluates the same float32 steps in numpy (fused multiply-adds as one rounding, the reciprocal and
 square root correctly rounded, which the hardware's 1-ulp versions can differ from by one ulp) on rotated
 K/V-like vectors and checks, for both, that
-* the float32 t stays within a third of the guard of the float64 t of the oracle at every bit width,
-* every code the guard accepts equals the oracle's code (pitch_reference.py:109-121),
-* the guard sends only a small fraction of pairs to the float64 path.
+* the float32 t (and d_j) stays within a third of its guard of the float64 value of the oracle at every bit width,
+* every code the guards accept equals the oracle's code (pitch_reference.py:109-121),
+* the guards send only a small fraction of pairs to the float64 path.
 """
 import importlib.util
 import math
@@ -71,6 +73,61 @@ def angle_sectors(c, a, coef, b):
     return np.where(c < 0, (L - w).astype(f32), w)
 
 
+SECTOR_GUARD = 2e-6
+
+
+def radius_guard(b):
+    return (2 ** b - 1) * 1.2e-6
+
+
+def sector_code(c, a, b):
+    """sector_code of pitch_vector.hip: (code, accepted, d_j values, mx) of float32 pairs (a, c)."""
+    L = 2 ** b
+    tans = G.sector_tans(b)
+    ax, ay = np.abs(a), np.abs(c)
+    mx, mn = np.maximum(ax, ay), np.minimum(ax, ay)
+    gm = (f32(SECTOR_GUARD) * mx).astype(f32)
+    ok = mx >= f32(1e-30)
+    n = np.zeros(a.shape, np.int64)
+    ds = []
+    for t in tans:
+        dj = _fma32(mx, np.full_like(mx, -t), mn)
+        ds.append(dj)
+        n += dj > 0
+        ok &= np.abs(dj) > gm
+    n = np.where(ay > ax, L // 4 - n, n)
+    n = np.where(np.signbit(a), L // 2 - n, n)
+    n = np.where(np.signbit(c), L - n, n)
+    return n & (L - 1), ok, ds, mx
+
+
+@pytest.mark.parametrize("b", list(G.SECTOR_BITS))
+def test_sector_code_error_budget(b):
+    """Full circle at several magnitudes: each computed d_j lies within a third of the guard (2e-6 mx) of the
+    float64 value of mn - mx tan((j - 1/2) 2 pi / 2^b) for the same float32 pair, and the accepted codes equal
+    floor(atan2 / (2 pi) * 2^b + 0.5) mod 2^b in float64 (pitch_reference.py:114-117)."""
+    th = np.linspace(-math.pi, math.pi, 200001)
+    L = 2 ** b
+    for mag in (1e-29, 1e-3, 1.0, 7.5e4, 1e29):
+        a, c = (mag * np.cos(th)).astype(f32), (mag * np.sin(th)).astype(f32)
+        code, ok, ds, mx = sector_code(c, a, b)
+        a64, c64 = a.astype(np.float64), c.astype(np.float64)
+        mx64 = np.maximum(np.abs(a64), np.abs(c64))
+        mn64 = np.minimum(np.abs(a64), np.abs(c64))
+        k = np.arange(1, len(ds) + 1)
+        for j, dj in zip(k, ds):
+            exact = mn64 - mx64 * np.tan((j - 0.5) * 2 * np.pi / L)
+            assert np.abs(dj.astype(np.float64) - exact).max() < SECTOR_GUARD / 3 * mx64.max(), (b, mag, j)
+        th64 = np.mod(np.arctan2(c64, a64), 2 * np.pi)
+        ref = np.floor(th64 / (2 * np.pi) * L + 0.5).astype(np.int64) & (L - 1)
+        assert np.array_equal(code[ok], ref[ok]), (b, mag)
+        assert ok.mean() > 0.999, (b, mag, ok.mean())
+    # the origin and pairs below 1e-30 are left to the float64 path
+    z = np.array([0.0, -0.0, 1e-31, 0.0], f32)
+    _, ok, _, _ = sector_code(z, z[::-1].copy(), b)
+    assert not ok.any()
+
+
 @pytest.mark.parametrize("d", [64, 128])
 def test_staged_fast_path_matches_oracle(d):
     """The staged-stage encoder's formulation, on the unnormalised transform as the kernel holds it."""
@@ -94,17 +151,23 @@ def test_staged_fast_path_matches_oracle(d):
         ta_exact = theta / (2 * np.pi) * L + 0.5
         da = np.abs(ta - ta_exact)
         da = np.minimum(da, np.abs(da - L))
-        assert np.abs(tr - tr_exact).max() < GUARD / 3, b
+        gr = radius_guard(b)
+        assert np.abs(tr - tr_exact).max() < gr / 3, b
         assert da.max() < GUARD / 3, b
         assert tr.max() < L - 0.5 + 1e-4, b  # the radius code needs no clip
         fr, fa = tr - np.floor(tr), ta - np.floor(ta)
-        ok = (r > 0) & (fr > GUARD) & (fr < 1 - GUARD) & (fa > GUARD) & (fa < 1 - GUARD)
+        ok = (r > 0) & (fr > gr) & (fr < 1 - gr)
+        ac = np.floor(ta).astype(np.int64) & (L - 1)
+        if b in G.SECTOR_BITS:
+            ac, oka, _, _ = sector_code(cf, af, b)
+            ok &= oka
+        else:
+            ok &= (fa > GUARD) & (fa < 1 - GUARD)
         codes, _ = O.polar_encode(X, b)
         rc = np.floor(tr).astype(np.int64)
-        ac = np.floor(ta).astype(np.int64) & (L - 1)
         assert np.array_equal(rc[ok], codes[:, 0::2][ok]), b
         assert np.array_equal(ac[ok], codes[:, 1::2][ok]), b
-        assert ok.mean() > 0.99, (b, ok.mean())
+        assert ok.mean() > (0.9999 if b in G.SECTOR_BITS else 0.998), (b, ok.mean())
 
 
 @pytest.mark.parametrize("b", range(2, 9))
