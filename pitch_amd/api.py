@@ -135,9 +135,10 @@ class QuantConfig:
         object.__setattr__(self, "bits", int(self.bits))
         object.__setattr__(self, "seed", int(self.seed))
         object.__setattr__(self, "_cs", int(cs.value))
+        object.__setattr__(self, "_cstruct", c)  # the C ABI's view, built once (the config is immutable)
 
     def _c(self) -> _lib.PitchConfigC:
-        return _lib.PitchConfigC(self.method.code, self.dim, self.bits, self.seed)
+        return self._cstruct
 
     @property
     def codeStride(self) -> int:
@@ -189,9 +190,10 @@ class ChannelQuantConfig:
                                                         ctypes.byref(cs), ctypes.byref(rs)))
         object.__setattr__(self, "_cs", int(cs.value))
         object.__setattr__(self, "_rs", int(rs.value))
+        object.__setattr__(self, "_cstruct", c)
 
     def _c(self) -> _lib.PitchChannelConfigC:
-        return _lib.PitchChannelConfigC(self.dim, self.bits, self.groupSize, 0)
+        return self._cstruct
 
     @property
     def codeStride(self) -> int:
@@ -487,6 +489,11 @@ def _torch():
 
 def _buf(t, name: str):
     """(pointer, byte length) of a contiguous device tensor used as a raw buffer."""
+    try:
+        if t.is_cuda and t.is_contiguous():
+            return t.data_ptr(), t.nbytes
+    except AttributeError:
+        pass
     torch = _torch()
     if not isinstance(t, torch.Tensor):
         raise InvalidInput(f"{name} must be a torch tensor")
@@ -514,8 +521,14 @@ def _io_type(t, element_type=None) -> int:
 
 
 def _stream_handle(stream, device=None):
+    """HIP stream handle: the given stream (an int handle or a torch stream), else torch's current stream of
+    device (read with the raw query when torch has it: a fraction of a microsecond instead of about two)."""
     torch = _torch()
     if stream is None:
+        raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+        if raw is not None:
+            idx = device.index if device is not None and device.index is not None else torch.cuda.current_device()
+            return raw(idx)
         return torch.cuda.current_stream(device).cuda_stream
     if isinstance(stream, int):
         return stream
