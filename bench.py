@@ -293,9 +293,22 @@ def run_config5_values(torch, q, P, O, W, timer, dev, args) -> tuple[dict, dict]
     single = timer.single_calls(lambda i: q.enqueueEncode(xa[i % L], codes, scales, H, cfg,
                                                           codesOffset=((i % L) * per_layer + (i % T) * H) * cs,
                                                           scalesOffset=((i % L) * per_layer + (i % T) * H) * 4))
+    # the same append as one batched call over the 32 layers (EncodeBatch -> pitch_enqueue_encode_batch)
+    import numpy as np
+    tab = P.EncodeBatch(q, cfg, [xa[layer] for layer in range(L)], [codes] * L, [scales] * L)
+    lbase = np.arange(L, dtype=np.int64) * per_layer
+
+    def append_token_batched(i):
+        v0 = lbase + (i % T) * H
+        tab.enqueue(H, codesOffsets=v0 * cs, scalesOffsets=v0 * 4)
+
+    ms_tok_b = timer.time(append_token_batched, 50, 5)
+    single_b = timer.single_calls(append_token_batched)
     extra["cfg5_V_append_8_vectors_per_layer"] = {
         "token_all_32_layers_us_backtoback": round(ms_tok * 1e3, 2),
-        "per_layer_call_us_backtoback": round(ms_tok * 1e3 / L, 2), "single_call": single}
+        "per_layer_call_us_backtoback": round(ms_tok * 1e3 / L, 2), "single_call": single,
+        "token_all_32_layers_one_batched_call_us_backtoback": round(ms_tok_b * 1e3, 2),
+        "batched_single_call": single_b}
     del codes, scales, out, xa
     torch.cuda.empty_cache()
     return head, extra

@@ -101,6 +101,28 @@ int pitch_enqueue_encode_io(const pitch_config_t* config, uint32_t io_type, cons
                             uint64_t codes_offset, void* scales, uint64_t scales_bytes, uint64_t scales_offset,
                             uint64_t count, void* stream);
 
+/* One segment of a batched encode: count vectors of the batch's element type from input + input_offset, their
+ * codes to codes + codes_offset and their scales to scales + scales_offset (byte offsets and sizes as in
+ * pitch_enqueue_encode_io). */
+typedef struct pitch_encode_item {
+  const void* input;
+  uint64_t input_bytes, input_offset;
+  void* codes;
+  uint64_t codes_bytes, codes_offset;
+  void* scales;
+  uint64_t scales_bytes, scales_offset;
+  uint64_t count;
+} pitch_encode_item_t;
+
+/* Encodes n_items independent segments with one configuration and element type io_type (PITCH_IO_*) in as few
+ * launches as it can (one per 32 segments), with the same codes and scales as one pitch_enqueue_encode_io per
+ * segment. Every segment is validated as that call validates it, before anything is launched. For the
+ * decode-phase append of a token's vectors across many layers: README.md:65-71 issues one
+ * PITCH.enqueueEncode (Sources/PITCH/PITCH.swift:144-153) per cache, and a launch costs several microseconds
+ * of host time here, so appending to 32 layers' caches through one call takes a fraction of 32 calls' time. */
+int pitch_enqueue_encode_batch(const pitch_config_t* config, uint32_t io_type, const pitch_encode_item_t* items,
+                               uint32_t n_items, void* stream);
+
 /* Decodes count vectors into count * dim fp32 values.
  * Replaces PITCH.enqueueDecode(codes:codesOffset:scales:scalesOffset:output:outputOffset:count:config:
  * commandBuffer:) (Sources/PITCH/PITCH.swift:156-165 -> Sources/PITCH/Core/Codec.swift:107-140). */

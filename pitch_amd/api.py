@@ -701,6 +701,35 @@ class PITCH:
             rc = self._lib.pitch_enqueue_encode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
 
+    def enqueueEncodeBatch(self, items, config: QuantConfig, stream=None, elementType=None) -> None:
+        """Encodes independent segments with one configuration in one call (pitch_enqueue_encode_batch), with
+        the same results as one enqueueEncode per segment. items: a sequence of (input, codes, scales, count)
+        or (input, codes, scales, count, inputOffset, codesOffset, scalesOffset); every input has the element
+        type elementType, else the first input's, chosen as for enqueueEncode. For the per-token append across
+        many layers' caches (README.md:65-71 appends with one enqueueEncode per cache); EncodeBatch keeps the
+        segment table between calls."""
+        items = list(items)
+        if not items:
+            raise InvalidInput("a batch needs at least one segment")
+        io = _io_type(items[0][0], elementType)
+        arr = (_lib.PitchEncodeItemC * len(items))()
+        for i, it in enumerate(items):
+            if len(it) not in (4, 7):
+                raise InvalidInput("a segment is (input, codes, scales, count[, inputOffset, codesOffset, "
+                                   "scalesOffset])")
+            offs = it[4:] if len(it) == 7 else (0, 0, 0)
+            _check_offsets(*offs)
+            if _io_type(it[0], elementType) != io:
+                raise InvalidInput("every segment's input must have the batch's element type")
+            e = arr[i]
+            e.input, e.input_bytes = _buf(it[0], "input")
+            e.codes, e.codes_bytes = _buf(it[1], "codes")
+            e.scales, e.scales_bytes = _buf(it[2], "scales")
+            e.input_offset, e.codes_offset, e.scales_offset = (int(o) for o in offs)
+            e.count = _count(it[3])
+        _raise_for(self._lib.pitch_enqueue_encode_batch(ctypes.byref(config._c()), io, arr, len(items),
+                                                        _stream_handle(stream, self.device)))
+
     def enqueueDecode(self, codes, scales, output, count: int, config: QuantConfig, codesOffset: int = 0,
                       scalesOffset: int = 0, outputOffset: int = 0, stream=None, elementType=None,
                       keyBias: KeyBias | None = None) -> None:
@@ -866,6 +895,49 @@ class PITCH:
         else:
             rc = self._lib.pitch_enqueue_channel_decode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
+
+
+class EncodeBatch:
+    """A segment table for pitch_enqueue_encode_batch kept between calls: one segment per (input, codes, scales)
+    buffer triple, e.g. one per layer's cache. Each enqueue sets the segments' counts and byte offsets in place
+    (scalars or one value per segment) and issues one batched encode, so a decode step's append to every layer
+    costs one call. The buffers are held for the table's lifetime."""
+
+    def __init__(self, pitch: "PITCH", config: QuantConfig, inputs, codes, scales, elementType=None):
+        self._pitch, self.config = pitch, config
+        self._bufs = (list(inputs), list(codes), list(scales))
+        n = len(self._bufs[0])
+        if n < 1 or len(self._bufs[1]) != n or len(self._bufs[2]) != n:
+            raise InvalidInput("inputs, codes and scales need one buffer per segment")
+        self._io = _io_type(self._bufs[0][0], elementType)
+        if any(_io_type(t, elementType) != self._io for t in self._bufs[0]):
+            raise InvalidInput("every segment's input must have the batch's element type")
+        self._arr = (_lib.PitchEncodeItemC * n)()
+        self._tab = np.frombuffer(self._arr, dtype=np.uint64).reshape(n, 10)  # the C array's fields, in place
+        for i in range(n):
+            e = self._arr[i]
+            e.input, e.input_bytes = _buf(self._bufs[0][i], "input")
+            e.codes, e.codes_bytes = _buf(self._bufs[1][i], "codes")
+            e.scales, e.scales_bytes = _buf(self._bufs[2][i], "scales")
+        self._n = n
+
+    def __len__(self) -> int:
+        return self._n
+
+    def enqueue(self, count, inputOffsets=0, codesOffsets=0, scalesOffsets=0, stream=None) -> None:
+        for name, v in (("count", count), ("offset", inputOffsets), ("offset", codesOffsets),
+                        ("offset", scalesOffsets)):
+            a = np.asarray(v)
+            if a.dtype.kind not in "iu" or (a < (1 if name == "count" else 0)).any():
+                raise InvalidInput(f"{name} {v!r} must be {'at least 1' if name == 'count' else 'non-negative'}")
+        t = self._tab
+        t[:, 9] = count
+        t[:, 2] = inputOffsets
+        t[:, 5] = codesOffsets
+        t[:, 8] = scalesOffsets
+        p = self._pitch
+        _raise_for(p._lib.pitch_enqueue_encode_batch(ctypes.byref(self.config._c()), self._io, self._arr, self._n,
+                                                     _stream_handle(stream, p.device)))
 
 
 def _attention_desc(q_per_kv: int, kv_heads: int, tokens: int, token_stride: int, head_stride: int,

@@ -128,6 +128,28 @@ hipError_t launch_vec(uint32_t dim, uint32_t io, bool encode, bool polar, int bi
   return kVecLaunch[li][io](encode, polar, bits, a, s);
 }
 
+using VecBatchLaunch = hipError_t (*)(bool, int, const pitch::VecBatchArgs&, hipStream_t);
+using VecBatchVpb = uint32_t (*)();
+
+#define PITCH_VEC_ROW(D) \
+  {pitch::launch_vec_batch_d##D##_io0, pitch::launch_vec_batch_d##D##_io1, pitch::launch_vec_batch_d##D##_io2}
+constexpr VecBatchLaunch kVecBatchLaunch[10][3] = {
+    PITCH_VEC_ROW(2),  PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),   PITCH_VEC_ROW(16),  PITCH_VEC_ROW(32),
+    PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
+#undef PITCH_VEC_ROW
+#define PITCH_VEC_ROW(D) \
+  {pitch::vec_batch_vpb_d##D##_io0, pitch::vec_batch_vpb_d##D##_io1, pitch::vec_batch_vpb_d##D##_io2}
+constexpr VecBatchVpb kVecBatchVpb[10][3] = {
+    PITCH_VEC_ROW(2),  PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),   PITCH_VEC_ROW(16),  PITCH_VEC_ROW(32),
+    PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
+#undef PITCH_VEC_ROW
+
+int dim_index(uint32_t dim) {
+  int li = 0;
+  while ((2u << li) < dim) ++li;
+  return li;
+}
+
 hipError_t launch_channel(uint32_t io, bool encode, int bits, const pitch::ChanArgs& a, hipStream_t s) {
   switch (io) {
     case PITCH_IO_F32: return pitch::launch_channel_io0(encode, bits, a, s);
@@ -202,6 +224,60 @@ int encode_impl(const pitch_config_t* config, uint32_t io, const void* input, ui
   const hipError_t e = launch_vec(dim, io, true, config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
                                   (hipStream_t)stream);
   if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+// Workgroups a batched encode gives one segment: enough for every round of the segment, at most this many
+// (a longer segment loops over its rounds; a batch is meant for short segments).
+constexpr uint64_t kBatchMaxBlocks = 1024;
+
+int encode_batch_impl(const pitch_config_t* config, uint32_t io, const pitch_encode_item_t* items, uint32_t n,
+                      void* stream) {
+  PITCH_TRY(validate_config(config));
+  PITCH_TRY(check_io(io));
+  if (n < 1) return fail(PITCH_ERR_INVALID_INPUT, "a batch needs at least one segment");
+  if (!items) return fail(PITCH_ERR_INVALID_INPUT, "segment array is null");
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  for (uint32_t i = 0; i < n; ++i) {
+    const pitch_encode_item_t& it = items[i];
+    if (it.count < 1) return fail(PITCH_ERR_INVALID_INPUT, "segment %u: count must be at least 1", i);
+    if (mul_overflows(it.count, (uint64_t)dim * 4u))
+      return fail(PITCH_ERR_INVALID_INPUT, "segment %u: count is too large", i);
+    PITCH_TRY(check_buffer(it.input, it.input_bytes, it.input_offset, it.count * dim * io_bytes(io), "input"));
+    PITCH_TRY(check_buffer(it.codes, it.codes_bytes, it.codes_offset, it.count * cs, "codes"));
+    PITCH_TRY(check_buffer(it.scales, it.scales_bytes, it.scales_offset, it.count * 4u, "scales"));
+  }
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  for (uint32_t i = 0; i < n; ++i) {
+    const pitch_encode_item_t& it = items[i];
+    PITCH_TRY(check_device(it.input, dev, "input"));
+    PITCH_TRY(check_device(it.codes, dev, "codes"));
+    PITCH_TRY(check_device(it.scales, dev, "scales"));
+  }
+  const int li = dim_index(dim);
+  const uint64_t vpb = kVecBatchVpb[li][io]();
+  pitch::VecBatchArgs a{};
+  a.common.seed = config->seed;
+  for (uint32_t i0 = 0; i0 < n; i0 += pitch::kBatchItems) {
+    const uint32_t m = n - i0 < pitch::kBatchItems ? n - i0 : pitch::kBatchItems;
+    a.items = m;
+    uint32_t blocks = 0;
+    for (uint32_t j = 0; j < m; ++j) {
+      const pitch_encode_item_t& it = items[i0 + j];
+      const uint64_t need = (it.count + vpb - 1) / vpb;
+      a.block_start[j] = blocks;
+      blocks += (uint32_t)(need < kBatchMaxBlocks ? need : kBatchMaxBlocks);
+      a.in[j] = at<const char>(it.input, it.input_offset);
+      a.codes_out[j] = at<uint32_t>(it.codes, it.codes_offset);
+      a.scales_out[j] = at<float>(it.scales, it.scales_offset);
+      a.count[j] = it.count;
+    }
+    a.block_start[m] = blocks;
+    const hipError_t e = kVecBatchLaunch[li][io](config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
+                                                (hipStream_t)stream);
+    if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
+  }
   return ok();
 }
 
@@ -471,6 +547,11 @@ int pitch_enqueue_encode_io(const pitch_config_t* config, uint32_t io_type, cons
                             uint64_t count, void* stream) {
   return encode_impl(config, io_type, input, input_bytes, input_offset, codes, codes_bytes, codes_offset, scales,
                      scales_bytes, scales_offset, count, stream);
+}
+
+int pitch_enqueue_encode_batch(const pitch_config_t* config, uint32_t io_type, const pitch_encode_item_t* items,
+                               uint32_t n_items, void* stream) {
+  return encode_batch_impl(config, io_type, items, n_items, stream);
 }
 
 int pitch_enqueue_decode(const pitch_config_t* config, const void* codes, uint64_t codes_bytes,

@@ -28,6 +28,21 @@ struct VecArgs {
   uint32_t lane_flips[32];
 };
 
+// Arguments of one batched encode launch: up to kBatchItems independent segments with one configuration.
+// Segment i (count[i] vectors from in[i] to codes_out[i] / scales_out[i]) is encoded by the workgroups
+// [block_start[i], block_start[i + 1]); block_start[items] is the grid size. common supplies the seed (the
+// launcher fills its lane_flips); its pointers and count are unused.
+constexpr uint32_t kBatchItems = 32;
+struct VecBatchArgs {
+  VecArgs common;
+  uint32_t items;
+  uint32_t block_start[kBatchItems + 1];
+  const void* in[kBatchItems];
+  uint32_t* codes_out[kBatchItems];
+  float* scales_out[kBatchItems];
+  uint64_t count[kBatchItems];
+};
+
 // Arguments of one per-channel (KIVI) launch.
 struct ChanArgs {
   const void* in;   // encode: count * dim elements of the I/O type
@@ -104,9 +119,12 @@ uint64_t slice_rounds(uint64_t dflt);
 uint64_t stream_decode_min_vectors();
 
 // Per-vector launch for one dimension D and I/O element type IO (0 float32, 1 float16, 2 bfloat16); one
-// object file per (D, IO) defines launch_vec_d<D>_io<IO>.
-#define PITCH_DECLARE_VEC_LAUNCH_IO(D, IO) \
-  hipError_t launch_vec_d##D##_io##IO(bool encode, bool polar, int bits, const VecArgs& a, hipStream_t s);
+// object file per (D, IO) defines launch_vec_d<D>_io<IO>, the batched encode launch_vec_batch_d<D>_io<IO> and
+// vec_batch_vpb_d<D>_io<IO>, the vectors each of the batched encode's workgroups takes per round.
+#define PITCH_DECLARE_VEC_LAUNCH_IO(D, IO)                                                                     \
+  hipError_t launch_vec_d##D##_io##IO(bool encode, bool polar, int bits, const VecArgs& a, hipStream_t s);      \
+  hipError_t launch_vec_batch_d##D##_io##IO(bool polar, int bits, const VecBatchArgs& a, hipStream_t s);        \
+  uint32_t vec_batch_vpb_d##D##_io##IO();
 #define PITCH_DECLARE_VEC_LAUNCH(D) \
   PITCH_DECLARE_VEC_LAUNCH_IO(D, 0) PITCH_DECLARE_VEC_LAUNCH_IO(D, 1) PITCH_DECLARE_VEC_LAUNCH_IO(D, 2)
 PITCH_DECLARE_VEC_LAUNCH(2)

@@ -481,8 +481,11 @@ struct TqLut8 {
 #ifndef PITCH_POLAR_WAVES
 #define PITCH_POLAR_WAVES 1  // minimum waves per SIMD requested for the team encoder (caps its VGPRs)
 #endif
+// The team encoder's work on one segment: count vectors from in to codes_out / scales_out, blocks of VPB vectors
+// from vector first on, stride vectors apart. p supplies the rotation signs and the key-bias tables.
 template <int D, int B, bool POLAR, int IO, bool KBIAS>
-__global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode(VecArgs p) {
+__device__ __forceinline__ void vec_encode_run(const VecArgs& p, const void* in, uint32_t* codes_out,
+                                               float* scales_out, uint64_t count, uint64_t first, uint64_t stride) {
   using G = Geom<D>;
   constexpr int L = 1 << B;
   constexpr int NW = (D * B + 31) / 32;  // 32-bit words of codes per vector
@@ -511,24 +514,24 @@ __global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode(VecArgs 
   auto body = [&](uint64_t base, auto tail_c) {
     constexpr bool TAIL = decltype(tail_c)::value;
     const uint64_t v = base + slot;
-    const bool valid = !TAIL || v < p.count;
-    const uint64_t row = (valid ? v : p.count - 1) * D;
+    const bool valid = !TAIL || v < count;
+    const uint64_t row = (valid ? v : count - 1) * D;
 
     // load every chunk before converting (all loads in flight together), then apply the signs (exact)
     float f[G::E];
 #pragma unroll
     for (int k = 0; k < G::CH; ++k) {
       if constexpr (PITCH_VEC_ENC_NT && G::W == 4)  // read-once input: streamed past the caches
-        load4_nt<IO>(p.in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
+        load4_nt<IO>(in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
       else
-        load_elems<IO, G::W>(p.in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
+        load_elems<IO, G::W>(in, row + G::W * (k * G::T + t), *(float(*)[G::W])(f + k * G::W));
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (KBIAS) {  // key-bias removal: encode x - o (mechanism_eval.py:113-116)
 #pragma unroll
       for (int k = 0; k < G::CH; ++k) {
         float o[G::W];
-        key_bias_offset<D, G::W>(p, valid ? v : p.count - 1, G::W * (k * G::T + t), o);
+        key_bias_offset<D, G::W>(p, valid ? v : count - 1, G::W * (k * G::T + t), o);
 #pragma unroll
         for (int r = 0; r < G::W; ++r) f[k * G::W + r] = f[k * G::W + r] - o[r];
       }
@@ -614,9 +617,9 @@ __global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode(VecArgs 
         w[wi] |= code[i] << sh;
         if (sh + B > 32) w[wi + 1] |= code[i] >> (32 - sh);
       }
-      if (valid) store_words<NW>(p.codes_out + v * NW, w);
+      if (valid) store_words<NW>(codes_out + v * NW, w);
     }
-    if (t == 0 && valid) p.scales_out[v] = scale;
+    if (t == 0 && valid) scales_out[v] = scale;
 
     if constexpr (kStage) {
       __syncthreads();
@@ -628,24 +631,41 @@ __global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode(VecArgs 
         if (NG % kBlock == 0 || g < NG) {
           const int vs = g / GPV, gi = g % GPV;
           const uint64_t vv = base + vs;
-          if (!TAIL || vv < p.count) {
+          if (!TAIL || vv < count) {
             const uint4* q = (const uint4*)(s_stage + vs * kStageRow + 8 * gi);
             const uint4 q0 = q[0], q1 = q[1];
             const uint32_t bytes[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
             uint32_t w[B];
             pack32<B>(bytes, w);
-            store_words<B>(p.codes_out + vv * NW + gi * B, w);
+            store_words<B>(codes_out + vv * NW + gi * B, w);
           }
         }
       }
       __syncthreads();
     }
   };
-  for (uint64_t base = (uint64_t)blockIdx.x * G::VPB; base < p.count;
-       base += (uint64_t)gridDim.x * G::VPB) {
-    if (base + G::VPB <= p.count) body(base, std::false_type{});
+  for (uint64_t base = first; base < count; base += stride) {
+    if (base + G::VPB <= count) body(base, std::false_type{});
     else body(base, std::true_type{});
   }
+}
+
+template <int D, int B, bool POLAR, int IO, bool KBIAS>
+__global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode(VecArgs p) {
+  vec_encode_run<D, B, POLAR, IO, KBIAS>(p, p.in, p.codes_out, p.scales_out, p.count,
+                                         (uint64_t)blockIdx.x * Geom<D>::VPB, (uint64_t)gridDim.x * Geom<D>::VPB);
+}
+
+// A batch of independent segments with one configuration in one launch (pitch_enqueue_encode_batch): the blocks
+// [block_start[i], block_start[i + 1]) encode segment i with the team encoder.
+template <int D, int B, bool POLAR, int IO>
+__global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode_batch(VecBatchArgs pb) {
+  uint32_t i = 0;  // the segment of this block (uniform: kernel arguments and the block index)
+  for (uint32_t j = 1; j < pb.items; ++j) i = pb.block_start[j] <= blockIdx.x ? j : i;
+  const uint64_t nb = pb.block_start[i + 1] - pb.block_start[i];
+  vec_encode_run<D, B, POLAR, IO, false>(pb.common, pb.in[i], pb.codes_out[i], pb.scales_out[i], pb.count[i],
+                                         (uint64_t)(blockIdx.x - pb.block_start[i]) * Geom<D>::VPB,
+                                         nb * Geom<D>::VPB);
 }
 
 // ----------------------------------------------------------------------------------------------------
@@ -1817,6 +1837,36 @@ hipError_t launch_bits(bool encode, bool polar, const VecArgs& a, hipStream_t s)
 
 #define PITCH_CAT2(a, b) a##b
 #define PITCH_CAT(a, b) PITCH_CAT2(a, b)
+
+namespace {
+template <int D, int B, bool POLAR>
+hipError_t launch_batch(VecBatchArgs a, hipStream_t s) {
+  fill_lane_flips<D>(a.common.seed, a.common.lane_flips);
+  hipLaunchKernelGGL((vec_encode_batch<D, B, POLAR, PITCH_IO>), dim3(a.block_start[a.items]), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+template <int D, int B>
+hipError_t launch_batch_bits(bool polar, const VecBatchArgs& a, hipStream_t s) {
+  return polar ? launch_batch<D, B, true>(a, s) : launch_batch<D, B, false>(a, s);
+}
+}  // namespace
+
+uint32_t PITCH_CAT(PITCH_CAT(PITCH_CAT(vec_batch_vpb_d, PITCH_DIM), _io), PITCH_IO)() { return Geom<PITCH_DIM>::VPB; }
+
+hipError_t PITCH_CAT(PITCH_CAT(PITCH_CAT(launch_vec_batch_d, PITCH_DIM), _io), PITCH_IO)(bool polar, int bits,
+                                                                                    const VecBatchArgs& a,
+                                                                                    hipStream_t s) {
+  switch (bits) {
+    case 2: return launch_batch_bits<PITCH_DIM, 2>(polar, a, s);
+    case 3: return launch_batch_bits<PITCH_DIM, 3>(polar, a, s);
+    case 4: return launch_batch_bits<PITCH_DIM, 4>(polar, a, s);
+    case 5: return launch_batch_bits<PITCH_DIM, 5>(polar, a, s);
+    case 6: return launch_batch_bits<PITCH_DIM, 6>(polar, a, s);
+    case 7: return launch_batch_bits<PITCH_DIM, 7>(polar, a, s);
+    case 8: return launch_batch_bits<PITCH_DIM, 8>(polar, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t PITCH_CAT(PITCH_CAT(PITCH_CAT(launch_vec_d, PITCH_DIM), _io), PITCH_IO)(bool encode, bool polar, int bits,
                                                                               const VecArgs& a, hipStream_t s) {

@@ -432,3 +432,42 @@ def test_attention_channel_keys_validation(lib):
     assert call(d=_lib.PitchAttentionDescC(2, 2, 100, 1, 96, 0.125, 0)) == _lib.ERR_INVALID_INPUT   # head stride
     assert call(kranges=4 * 256 - 4) == _lib.ERR_INVALID_INPUT and "key ranges" in _lib.last_error()
     assert call(kcfg=_lib.PitchChannelConfigC(128, 4, 64, 0)) == _lib.ERR_CONFIGURATION_MISMATCH
+
+
+def test_encode_batch_validation(lib):
+    """pitch_enqueue_encode_batch checks every segment as pitch_enqueue_encode checks its buffers (sizes after the
+    offsets, 4-byte offsets, count >= 1), naming the segment, before it looks for a device."""
+    assert ctypes.sizeof(_lib.PitchEncodeItemC) == 80
+    cfg = _lib.PitchConfigC(0, 64, 4, 0)                 # code stride 32 bytes
+    bufs = []
+
+    def items(specs):
+        arr = (_lib.PitchEncodeItemC * len(specs))()
+        for e, (count, ib, cb, sb, offs) in zip(arr, specs):
+            i, c, s = Host(ib), Host(cb), Host(sb)
+            bufs.extend((i, c, s))
+            e.input, e.input_bytes, e.input_offset = i.p, ib, offs[0]
+            e.codes, e.codes_bytes, e.codes_offset = c.p, cb, offs[1]
+            e.scales, e.scales_bytes, e.scales_offset = s.p, sb, offs[2]
+            e.count = count
+        return arr
+
+    good = (3, 3 * 256, 3 * 32, 12, (0, 0, 0))
+    call = lambda arr, n=None, c=cfg, io=0: lib.pitch_enqueue_encode_batch(  # noqa: E731
+        ctypes.byref(c) if c is not None else None, io, arr, len(arr) if n is None else n, None)
+    assert call(items([good, good])) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+    assert "segment" not in _lib.last_error()
+    assert call(items([good]), n=0) == _lib.ERR_INVALID_INPUT
+    assert lib.pitch_enqueue_encode_batch(ctypes.byref(cfg), 0, None, 1, None) == _lib.ERR_INVALID_INPUT
+    assert call(items([good]), c=None) == _lib.ERR_INVALID_INPUT
+    assert call(items([good]), c=_lib.PitchConfigC(0, 96, 4, 0)) == _lib.ERR_INVALID_DIMENSION
+    assert call(items([good]), io=3) == _lib.ERR_INVALID_INPUT
+    assert call(items([good, (0, 0, 0, 0, (0, 0, 0))])) == _lib.ERR_INVALID_INPUT
+    assert "segment 1" in _lib.last_error()
+    assert call(items([good, good, (3, 3 * 256, 3 * 32 - 4, 12, (0, 0, 0))])) == _lib.ERR_INVALID_INPUT
+    assert "codes" in _lib.last_error()
+    assert call(items([(3, 3 * 256 + 8, 3 * 32, 12, (6, 0, 0))])) == _lib.ERR_INVALID_INPUT   # misaligned
+    assert call(items([(3, 3 * 256, 3 * 32, 16, (0, 0, 8))])) == _lib.ERR_INVALID_INPUT       # 8 bytes left
+    assert call(items([(3, 3 * 128, 3 * 32, 12, (0, 0, 0))]), io=1) in (_lib.ERR_INVALID_INPUT,
+                                                                       _lib.ERR_DEVICE_UNAVAILABLE)
+    assert "segment" not in _lib.last_error() and "needs" not in _lib.last_error()
