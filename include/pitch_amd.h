@@ -255,6 +255,22 @@ int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch
                                    uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes,
                                    uint64_t lse_offset, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* pitch_enqueue_attention_decode over a key cache encoded with key-bias removal (pitch_enqueue_encode_key_bias):
+ * the scores are q . (decode(k) + o_t) with o_t = b_h cos_t + rotate_half(b_h) sin_t, the cache's k - o_t
+ * restored as pitch_enqueue_decode_key_bias restores it (reference/mechanism_eval.py:113-116: the keys are
+ * compress(k - R_t b) + R_t b). key_bias->heads must equal desc->kv_heads (row h of the bias is KV head h) and
+ * token t of the cache is at position key_bias->first_position + t, so the tables need first_position + tokens
+ * rows. Per-vector keys only (per-channel keys need no bias removal). Extends the fused attention, which the
+ * reference does not have (README.md:96, 100). */
+int pitch_enqueue_attention_decode_key_bias(
+    const pitch_config_t* key_config, const pitch_config_t* value_config, const pitch_attention_desc_t* desc,
+    const pitch_key_bias_t* key_bias, const void* q, uint64_t q_bytes, uint64_t q_offset, const void* key_codes,
+    uint64_t key_codes_bytes, uint64_t key_codes_offset, const void* key_scales, uint64_t key_scales_bytes,
+    uint64_t key_scales_offset, const void* value_codes, uint64_t value_codes_bytes, uint64_t value_codes_offset,
+    const void* value_scales, uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output,
+    uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes, uint64_t lse_offset,
+    void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Largest workspace pitch_enqueue_attention_decode_noalloc can serve, in bytes (32 MiB: e.g. 8 KV heads x 4 query
  * heads x 131072 tokens at dim 128 needs 18.9 MB). */
 #define PITCH_NOALLOC_SCRATCH_BYTES (32ull << 20)

@@ -95,6 +95,10 @@ SIGNATURES = {
     "pitch_enqueue_attention_decode": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
                                               ctypes.POINTER(PitchAttentionDescC)] + [_vp, _u64, _u64] * 7
                                        + [_vp, _u64, _vp]),
+    "pitch_enqueue_attention_decode_key_bias": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
+                                                       ctypes.POINTER(PitchAttentionDescC),
+                                                       ctypes.POINTER(PitchKeyBiasC)] + [_vp, _u64, _u64] * 7
+                                                + [_vp, _u64, _vp]),
     "pitch_enqueue_attention_decode_noalloc": (_int, [ctypes.POINTER(PitchConfigC), ctypes.POINTER(PitchConfigC),
                                                       ctypes.POINTER(PitchAttentionDescC)] + [_vp, _u64, _u64] * 7
                                                + [_vp]),

@@ -773,7 +773,7 @@ class PITCH:
                                keyConfig: QuantConfig, valueConfig: QuantConfig | None = None, qPerKv: int = 1,
                                kvHeads: int = 1, tokenStride: int = 1, headStride: int | None = None,
                                scale: float | None = None, lse=None, workspace=None, stream=None,
-                               noAlloc: bool = False) -> None:
+                               noAlloc: bool = False, keyBias: KeyBias | None = None) -> None:
         """out = softmax(scale * q K^T) V over caches held as codes: q and output are fp32
         [kvHeads][qPerKv][dim]; the vector of (head h, token t) is t * tokenStride + h * headStride (default
         headStride = tokens, a head-major cache). scale defaults to 1 / sqrt(dim). lse, when given, receives the
@@ -783,11 +783,15 @@ class PITCH:
         overlapping on one device race).
         With a ChannelQuantConfig as keyConfig the keys are per-channel: keyScales is their fp16 ranges tensor, the
         caches are head-major (tokenStride 1) and headStride, in tokens, a multiple of the group size (default:
-        tokens rounded up to it)."""
+        tokens rounded up to it).
+        With keyBias (per-vector keys encoded with that key bias, pitch_enqueue_attention_decode_key_bias) the
+        scores use decode(k) + R_t b: keyBias.heads must be kvHeads and token t sits at keyBias.firstPosition + t."""
         torch = _torch()
         channel_keys = isinstance(keyConfig, ChannelQuantConfig)
         if channel_keys and valueConfig is None:
             raise InvalidInput("per-channel keys need a per-vector valueConfig")
+        if keyBias is not None and (channel_keys or noAlloc):
+            raise InvalidInput("key-bias removal takes per-vector keys and a workspace")
         valueConfig = valueConfig or keyConfig
         scale = 1.0 / math.sqrt(keyConfig.dim) if scale is None else scale
         if headStride is None:
@@ -816,6 +820,12 @@ class PITCH:
             _raise_for(rc)
             return
         wp, wb = _buf(workspace, "workspace")
+        if keyBias is not None:
+            rc = self._lib.pitch_enqueue_attention_decode_key_bias(
+                ctypes.byref(keyConfig._c()), ctypes.byref(valueConfig._c()), ctypes.byref(desc),
+                ctypes.byref(keyBias._c()), *args, wp, wb, _stream_handle(stream, self.device))
+            _raise_for(rc)
+            return
         fn = (self._lib.pitch_enqueue_attention_decode_channel_keys if channel_keys
               else self._lib.pitch_enqueue_attention_decode)
         rc = fn(ctypes.byref(keyConfig._c()), ctypes.byref(valueConfig._c()), ctypes.byref(desc), *args, wp, wb,

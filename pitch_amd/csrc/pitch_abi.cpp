@@ -445,7 +445,7 @@ uint32_t attention_chunk_tokens(uint64_t tokens, uint32_t kv_heads) {
 
 uint64_t attention_workspace_floats(uint32_t dim, uint32_t nqp, uint32_t kv_heads, uint64_t tokens, uint32_t chunk) {
   const uint64_t chunks = (tokens + chunk - 1) / chunk;
-  return (uint64_t)kv_heads * nqp * (dim + tokens + chunks * (2 + dim));
+  return (uint64_t)kv_heads * nqp * (3 * dim + tokens + chunks * (2 + dim));
 }
 
 uint64_t slice_rounds(uint64_t dflt) {
@@ -700,7 +700,8 @@ int attention_impl(const pitch_config_t* key_config, const pitch_config_t* value
                    uint64_t value_codes_bytes, uint64_t value_codes_offset, const void* value_scales,
                    uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output, uint64_t output_bytes,
                    uint64_t output_offset, void* lse, uint64_t lse_bytes, uint64_t lse_offset, void* workspace,
-                   uint64_t workspace_bytes, void* stream, bool use_scratch) {
+                   uint64_t workspace_bytes, void* stream, bool use_scratch,
+                   const pitch_key_bias_t* kb = nullptr) {
   PITCH_TRY(validate_attention(key_config, value_config, desc));
   const uint32_t dim = key_config->dim, nq = desc->q_per_kv, nqp = padded_queries(nq);
   const uint32_t kcs = code_stride_of(dim, key_config->bits), vcs = code_stride_of(dim, value_config->bits);
@@ -714,6 +715,12 @@ int attention_impl(const pitch_config_t* key_config, const pitch_config_t* value
   PITCH_TRY(check_buffer(value_scales, value_scales_bytes, value_scales_offset, vectors * 4u, "value scales"));
   PITCH_TRY(check_buffer(output, output_bytes, output_offset, queries * dim * 4u, "output"));
   if (lse) PITCH_TRY(check_buffer(lse, lse_bytes, lse_offset, queries * 4u, "lse"));
+  if (kb) {
+    if (kb->heads != desc->kv_heads)
+      return fail(PITCH_ERR_INVALID_INPUT, "key bias has %u heads; the call has %u KV heads", kb->heads,
+                  desc->kv_heads);
+    PITCH_TRY(check_key_bias(kb, dim, desc->tokens * desc->kv_heads));  // positions first .. first + tokens - 1
+  }
   const uint32_t chunk = pitch::attention_chunk_tokens(desc->tokens, desc->kv_heads);
   const uint64_t ws_need = 4u * pitch::attention_workspace_floats(dim, nqp, desc->kv_heads, desc->tokens, chunk);
   if (use_scratch) {
@@ -736,6 +743,11 @@ int attention_impl(const pitch_config_t* key_config, const pitch_config_t* value
   if (lse) PITCH_TRY(check_device(lse, dev, "lse"));
   if (use_scratch) PITCH_TRY(scratch_address(dev, &workspace));
   else PITCH_TRY(check_device(workspace, dev, "workspace"));
+  if (kb) {
+    PITCH_TRY(check_device(kb->bias, dev, "key bias"));
+    PITCH_TRY(check_device(kb->cos, dev, "RoPE cos"));
+    PITCH_TRY(check_device(kb->sin, dev, "RoPE sin"));
+  }
   pitch::AttnArgs a{};
   a.q = at<const float>(q, q_offset);
   a.k_codes = at<const uint32_t>(key_codes, key_codes_offset);
@@ -763,6 +775,13 @@ int attention_impl(const pitch_config_t* key_config, const pitch_config_t* value
   // softmax scale, log2(e) (scores in log2 units) and the key decode's 1 / sqrt(d), folded into the query
   a.qscale = (float)((double)desc->scale * 1.4426950408889634 / __builtin_sqrt((double)dim));
   a.oscale = (float)(1.0 / __builtin_sqrt((double)dim));
+  if (kb) {
+    a.kb_bias = (const float*)kb->bias;
+    a.kb_cos = (const float*)kb->cos;
+    a.kb_sin = (const float*)kb->sin;
+    a.kb_first = kb->first_position;
+    a.kscale = (float)((double)desc->scale * 1.4426950408889634);  // the bias term is in the keys' own scale
+  }
   const hipError_t e = dim == 64 ? pitch::launch_attention_d64(a, (hipStream_t)stream)
                                  : pitch::launch_attention_d128(a, (hipStream_t)stream);
   if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Attention failed: %s", hipGetErrorString(e));
@@ -787,6 +806,22 @@ int pitch_enqueue_attention_decode(const pitch_config_t* key_config, const pitch
                         value_codes_bytes, value_codes_offset, value_scales, value_scales_bytes, value_scales_offset,
                         output, output_bytes, output_offset, lse, lse_bytes, lse_offset, workspace, workspace_bytes,
                         stream, false);
+}
+
+int pitch_enqueue_attention_decode_key_bias(
+    const pitch_config_t* key_config, const pitch_config_t* value_config, const pitch_attention_desc_t* desc,
+    const pitch_key_bias_t* key_bias, const void* q, uint64_t q_bytes, uint64_t q_offset, const void* key_codes,
+    uint64_t key_codes_bytes, uint64_t key_codes_offset, const void* key_scales, uint64_t key_scales_bytes,
+    uint64_t key_scales_offset, const void* value_codes, uint64_t value_codes_bytes, uint64_t value_codes_offset,
+    const void* value_scales, uint64_t value_scales_bytes, uint64_t value_scales_offset, void* output,
+    uint64_t output_bytes, uint64_t output_offset, void* lse, uint64_t lse_bytes, uint64_t lse_offset,
+    void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (!key_bias) return fail(PITCH_ERR_INVALID_INPUT, "key bias is null");
+  return attention_impl(key_config, value_config, desc, q, q_bytes, q_offset, key_codes, key_codes_bytes,
+                        key_codes_offset, key_scales, key_scales_bytes, key_scales_offset, value_codes,
+                        value_codes_bytes, value_codes_offset, value_scales, value_scales_bytes, value_scales_offset,
+                        output, output_bytes, output_offset, lse, lse_bytes, lse_offset, workspace, workspace_bytes,
+                        stream, false, key_bias);
 }
 
 int pitch_enqueue_attention_decode_noalloc(const pitch_config_t* key_config, const pitch_config_t* value_config,

@@ -35,13 +35,15 @@ constexpr int kMaxChunk = 1024;          // tokens per workgroup; a chunk's scor
 constexpr float kLn2 = 0x1.62e430p-1f;   // ln(2)
 
 // Workspace regions (floats): rotated queries [kv][D/2][nqp][2], weights p [kv][T][nqp],
-// chunk (max, sum) [kv][nqp][chunks][2], chunk accumulators [kv][nqp][chunks][D].
+// chunk (max, sum) [kv][nqp][chunks][2], chunk accumulators [kv][nqp][chunks][D], and for key-bias removal the
+// query products (q (.) b, q (.) rotate_half(b)) * scale * log2(e) as [kv][D][nqp][2].
 struct WsLayout {
-  uint64_t p, ml, acc;
+  uint64_t p, ml, acc, kbq;
   __host__ __device__ explicit WsLayout(const AttnArgs& a) {
     p = (uint64_t)a.kv_heads * a.dim * a.nqp;
     ml = p + (uint64_t)a.kv_heads * a.tokens * a.nqp;
     acc = ml + (uint64_t)a.kv_heads * a.nqp * a.chunks * 2;
+    kbq = acc + (uint64_t)a.kv_heads * a.nqp * a.chunks * a.dim;
   }
 };
 
@@ -157,6 +159,48 @@ __global__ __launch_bounds__(64) void attn_prep(AttnArgs a) {
     const int j = lane * E + e;
     qp[((uint64_t)(j >> 1) * a.nqp + h) * 2 + (j & 1)] = v[e] * a.qscale;
   }
+  if (a.kb_cos) {
+    // q . o_t = sum_j (q_j b_j) cos_tj + (q_j rotate_half(b)_j) sin_tj, rotate_half(b)_j = -b_(j+D/2) for j < D/2
+    // and b_(j-D/2) above; the products carry the scores' scale and log2(e)
+    const float* bb = a.kb_bias + (uint64_t)kv * D;
+    float* kq = a.ws + WsLayout(a).kbq + (uint64_t)kv * D * a.nqp * 2;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int j = lane * E + e;
+      const float x = h < a.nq ? a.q[((uint64_t)kv * a.nq + h) * D + j] : 0.f;
+      const float rh = j < D / 2 ? -bb[j + D / 2] : bb[j - D / 2];
+      kq[((uint64_t)j * a.nqp + h) * 2] = x * bb[j] * a.kscale;
+      kq[((uint64_t)j * a.nqp + h) * 2 + 1] = x * rh * a.kscale;
+    }
+  }
+}
+
+// Key-bias term of token t's scores for NQ queries, in log2 units: sum_j U_hj cos_tj + W_hj sin_tj over the row
+// of position kb_first + t (U, W from attn_prep; their reads are wave-uniform), with two partial sums per query.
+template <int D, int NQ>
+__device__ __forceinline__ void key_bias_scores(const AttnArgs& a, const float* __restrict__ kq, uint64_t t,
+                                                float (&bias)[NQ]) {
+  const f32x4* cr = (const f32x4*)(a.kb_cos + (a.kb_first + t) * D);
+  const f32x4* sr = (const f32x4*)(a.kb_sin + (a.kb_first + t) * D);
+  float s0[NQ], s1[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) s0[h] = s1[h] = 0.f;
+  for (int j4 = 0; j4 < D / 4; ++j4) {
+    const f32x4 c4 = cr[j4], n4 = sr[j4];
+    const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {n4.x, n4.y, n4.z, n4.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float* u = kq + (uint64_t)(4 * j4 + r) * NQ * 2;
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        float& acc = (r & 1) ? s1[h] : s0[h];
+        acc = __builtin_fmaf(u[2 * h], cs[r], acc);
+        acc = __builtin_fmaf(u[2 * h + 1], sn[r], acc);
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) bias[h] = s0[h] + s1[h];
 }
 
 // ---------------------------------------------------------------------------------------------- scores
@@ -206,7 +250,14 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
         acc[h] = __builtin_fmaf(qp[(p * NQ + h) * 2 + 1], t.y, acc[h]);
       }
     }
-    if (valid) {
+    if (a.kb_cos) {  // key-bias removal: + q . o_t (position of a token past the chunk's end: its first)
+      float kb[NQ];
+      key_bias_scores<D, NQ>(a, a.ws + WsLayout(a).kbq + (uint64_t)kv * D * NQ * 2, t0 + (valid ? i : 0u), kb);
+      if (valid) {
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) s_s[i * NQ + h] = __builtin_fmaf(acc[h], nk, kb[h]);
+      }
+    } else if (valid) {
 #pragma unroll
       for (int h = 0; h < NQ; ++h) s_s[i * NQ + h] = acc[h] * nk;
     }
@@ -690,6 +741,7 @@ hipError_t PITCH_CAT(launch_attention_d, PITCH_DIM)(const AttnArgs& a, hipStream
   if (a.dim != (uint32_t)D || a.chunk < 64 || a.chunk > (uint32_t)kMaxChunk || a.chunks == 0) return hipErrorInvalidValue;
   if (a.k_ranges && (a.k_group == 0 || a.k_group % 64 != 0 || a.head_stride % a.k_group != 0 || a.token_stride != 1))
     return hipErrorInvalidValue;
+  if (a.kb_cos && (a.k_ranges || !a.kb_bias || !a.kb_sin)) return hipErrorInvalidValue;
   if (!a.k_ranges) hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
   hipError_t e;
   switch (a.nqp) {

@@ -93,6 +93,12 @@ struct AttnArgs {
   const uint16_t* k_ranges;
   uint32_t k_group;          // tokens per key group (a multiple of 64)
   float kscale;              // softmax scale * log2(e), folded into the per-group query products
+  // Key-bias removal (kb_cos non-null, per-vector keys): the keys were encoded as k - o_t with
+  // o_t = b_h cos_t + rotate_half(b_h) sin_t at position kb_first + t, and the scores add q . o_t.
+  const float* kb_bias;      // [kv_heads][dim]
+  const float* kb_cos;       // [positions][dim]
+  const float* kb_sin;       // [positions][dim]
+  uint64_t kb_first;
 };
 
 // Chunk length (tokens per workgroup) the attention kernels use for a call, and the workspace it needs.

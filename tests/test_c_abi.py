@@ -471,3 +471,36 @@ def test_encode_batch_validation(lib):
     assert call(items([(3, 3 * 128, 3 * 32, 12, (0, 0, 0))]), io=1) in (_lib.ERR_INVALID_INPUT,
                                                                        _lib.ERR_DEVICE_UNAVAILABLE)
     assert "segment" not in _lib.last_error() and "needs" not in _lib.last_error()
+
+
+def test_attention_key_bias_validation(lib):
+    """The key-bias attention entry: null key bias, a head count other than the call's KV heads and RoPE tables
+    too short for first_position + tokens rows are rejected before any device work."""
+    kc = _lib.PitchConfigC(0, 64, 4, 0)
+    T, kv, nq, d = 100, 2, 2, 64
+    desc = _lib.PitchAttentionDescC(nq, kv, T, kv, 1, 0.125, 0)
+    n = ctypes.c_uint64(0)
+    assert lib.pitch_attention_workspace_size(ctypes.byref(kc), ctypes.byref(kc), ctypes.byref(desc),
+                                              ctypes.byref(n)) == 0
+    vecs = T * kv
+    bufs = [Host(x) for x in (kv * nq * d * 4, vecs * 32, vecs * 4, vecs * 32, vecs * 4, kv * nq * d * 4,
+                              kv * nq * 4)]
+    w = Host(n.value)
+    bias, cos, sin = Host(kv * d * 4), Host((T + 10) * d * 4), Host((T + 10) * d * 4)
+
+    def call(first=0, heads=kv, kb=True, tb=(T + 10) * d * 4):
+        k = _lib.PitchKeyBiasC(bias.p, kv * d * 4, cos.p, sin.p, tb, first, heads, 0)
+        args = []
+        for b in bufs:
+            args += [b.p, b.nbytes, 0]
+        return lib.pitch_enqueue_attention_decode_key_bias(ctypes.byref(kc), ctypes.byref(kc), ctypes.byref(desc),
+                                                           ctypes.byref(k) if kb else None, *args, w.p, w.nbytes,
+                                                           None)
+
+    assert call() in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE) and "positions" not in _lib.last_error()
+    assert call(kb=False) == _lib.ERR_INVALID_INPUT
+    assert call(heads=1) == _lib.ERR_INVALID_INPUT and "KV heads" in _lib.last_error()
+    assert call(first=10) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)   # exactly T rows left
+    assert "positions" not in _lib.last_error()
+    assert call(first=11) == _lib.ERR_INVALID_INPUT and "positions" in _lib.last_error()
+    assert call(tb=T * d * 4 - 4) == _lib.ERR_INVALID_INPUT

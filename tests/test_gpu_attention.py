@@ -242,3 +242,68 @@ def test_attention_channel_keys(q, kb, vb, d, G, nq, kv, T):
         ro, rl = O.attention_decode_channel_keys(Qn[h], ck, rk, kb, G, cv, vsn[h, :T], "turboQuant", vb,
                                                  1 / math.sqrt(d), 77)
         _check(out[h], lse[h], ro, rl, OUT_REL_L2, LSE_TOL, f"{label} head {h}")
+
+
+KEY_BIAS_CASES = [
+    # (key method, value method, kb, vb, d, nq, kv, T, first position)
+    ("turboQuant", "turboQuant", 4, 4, 128, 4, 2, 2000, 0),
+    ("polarQuant", "turboQuant", 4, 4, 128, 2, 3, 1500, 17),
+    ("turboQuant", "polarQuant", 3, 4, 64, 1, 2, 777, 5),
+    ("turboQuant", "turboQuant", 2, 2, 64, 8, 1, 70000, 100),
+    ("polarQuant", "polarQuant", 5, 3, 128, 5, 1, 300, 0),
+]
+
+
+@pytest.mark.parametrize("km,vm,kb,vb,d,nq,kv,T,first", KEY_BIAS_CASES)
+def test_attention_key_bias(q, km, vm, kb, vb, d, nq, kv, T, first):
+    """Keys with a RoPE'd projection bias (Qwen-style, mechanism_eval.py:88-97), encoded with the bias removed
+    (pitch_enqueue_encode_key_bias) into a token-major cache; the attention with the same KeyBias scores
+    q . (decode(k) + R_t b). Checked against the oracle over the library's codes with R_t b added
+    (mechanism_eval.py:113-116), and against float64 attention over the library's own key-bias decode."""
+    import torch
+    import pitch_amd as P
+    from test_gpu_cache_ops import _rope
+    dev = q.device
+    print(f"attention key bias {km}/{vm} kb={kb} vb={vb} d={d} nq={nq} kv={kv} T={T}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(T + d + kb)
+    n = T * kv
+    bias = (torch.randn(kv, d, generator=g, device=dev) * 6).contiguous()
+    cos, sin = _rope(first + T + 3, d, dev)
+    t = first + torch.arange(n, device=dev) // kv
+    bb = bias[torch.arange(n, device=dev) % kv]
+    o = bb * cos[t] + torch.cat([-bb[:, d // 2:], bb[:, :d // 2]], 1) * sin[t]
+    K = (torch.randn(n, d, generator=g, device=dev) + o).contiguous()
+    V = torch.randn(n, d, generator=g, device=dev)
+    kcfg, vcfg = P.QuantConfig(km, d, kb, 0x51), P.QuantConfig(vm, d, vb, 0x52)
+    kbias = P.KeyBias(bias, cos, sin, firstPosition=first, heads=kv)
+    kc = torch.empty(n * kcfg.codeStride, dtype=torch.uint8, device=dev)
+    vc = torch.empty(n * vcfg.codeStride, dtype=torch.uint8, device=dev)
+    ks, vs = torch.empty(n, device=dev), torch.empty(n, device=dev)
+    q.enqueueEncode(K, kc, ks, n, kcfg, keyBias=kbias)
+    q.enqueueEncode(V, vc, vs, n, vcfg)
+    Q = torch.randn(kv, nq, d, generator=g, device=dev)
+    out = torch.empty(kv, nq, d, device=dev)
+    lse = torch.empty(kv, nq, device=dev)
+    q.enqueueAttentionDecode(Q, kc, ks, vc, vs, out, T, kcfg, vcfg, qPerKv=nq, kvHeads=kv, tokenStride=kv,
+                             headStride=1, lse=lse, keyBias=kbias)
+    Kd = torch.empty(n, d, device=dev)
+    q.enqueueDecode(kc, ks, Kd, n, kcfg, keyBias=kbias)
+    torch.cuda.synchronize()
+    Ob = O.key_bias_offsets(bias.cpu().numpy(), cos.cpu().numpy(), sin.cpu().numpy(), first, n, kv)
+    codes_k = O.unpack_codes(kc.cpu().numpy().tobytes(), n, d, kb)
+    codes_v = O.unpack_codes(vc.cpu().numpy().tobytes(), n, d, vb)
+    Kr = (O.DECODERS[km](codes_k, ks.cpu().numpy().astype(np.float64), kb, kcfg.seed) + Ob).reshape(T, kv, d)
+    Vr = O.DECODERS[vm](codes_v, vs.cpu().numpy().astype(np.float64), vb, vcfg.seed).reshape(T, kv, d)
+    Kl = Kd.cpu().numpy().reshape(T, kv, d)
+    out, lse, Qn = out.cpu().numpy(), lse.cpu().numpy(), Q.cpu().numpy().astype(np.float64)
+    for h in range(kv):
+        ro, rl = O.attend(Qn[h], Kr[:, h], Vr[:, h], 1 / math.sqrt(d))
+        _check(out[h], lse[h], ro, rl, OUT_REL_L2, LSE_TOL, f"key bias head {h}")
+        ro2, rl2 = O.attend(Qn[h], Kl[:, h], Vr[:, h], 1 / math.sqrt(d))
+        _check(out[h], lse[h], ro2, rl2, OUT_REL_L2, LSE_TOL, f"key bias head {h} vs library decode")
+    # without the key bias the scores lack q . R_t b: the outputs differ (the case the feature exists for)
+    plain = torch.empty(kv, nq, d, device=dev)
+    q.enqueueAttentionDecode(Q, kc, ks, vc, vs, plain, T, kcfg, vcfg, qPerKv=nq, kvHeads=kv, tokenStride=kv,
+                             headStride=1)
+    torch.cuda.synchronize()
+    assert _rel_l2(plain.cpu().numpy()[0, 0], out[0, 0]) > 1e-3
