@@ -744,6 +744,66 @@ def run_attention(torch, q, P, O, W, timer, gen, dev, args) -> dict:
         "parity_max_rel_l2_head0": rel}
     del K, V, kc, kr, vc, vs, Kd, Vd, ws
     torch.cuda.empty_cache()
+    # key-bias removal inside attention: a config-4 layer (Qwen2.5-1.5B: 2 KV heads x 6 query heads, d = 128) of
+    # RoPE'd biased keys encoded with the bias removed, token-major cache (pitch_enqueue_attention_decode_key_bias)
+    kv, nq, d, T = 2, 6, 128, 16384
+    cfg = P.QuantConfig("turboQuant", d, 4)
+    n = kv * T
+    inv = 1.0 / 1e6 ** (torch.arange(0, d, 2, dtype=torch.float64) / d)
+    ang = torch.arange(T, dtype=torch.float64)[:, None] * inv[None, :]
+    cos = torch.cat([torch.cos(ang)] * 2, 1).float().to(dev).contiguous()
+    sin = torch.cat([torch.sin(ang)] * 2, 1).float().to(dev).contiguous()
+    bias = (torch.randn(kv, d, generator=gen, device=dev) * 5).contiguous()
+    kb = P.KeyBias(bias, cos, sin, firstPosition=0, heads=kv)
+    tpos = torch.arange(n, device=dev) // kv
+    bb = bias[torch.arange(n, device=dev) % kv]
+    K = (torch.randn(n, d, generator=gen, device=dev) + bb * cos[tpos]
+         + torch.cat([-bb[:, d // 2:], bb[:, :d // 2]], 1) * sin[tpos]).contiguous()
+    V = torch.randn(n, d, generator=gen, device=dev)
+    kc = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=dev)
+    vc = torch.empty_like(kc)
+    ks, vs = torch.empty(n, device=dev), torch.empty(n, device=dev)
+    q.enqueueEncode(K, kc, ks, n, cfg, keyBias=kb)
+    q.enqueueEncode(V, vc, vs, n, cfg)
+    Q = torch.randn(kv, nq, d, generator=gen, device=dev)
+    o = torch.empty(kv, nq, d, device=dev)
+    ws = torch.empty(P.attention_workspace_bytes(cfg, cfg, T, nq, kv), dtype=torch.uint8, device=dev)
+    ms = timer.time(lambda i: q.enqueueAttentionDecode(Q, kc, ks, vc, vs, o, T, cfg, qPerKv=nq, kvHeads=kv,
+                                                       tokenStride=kv, headStride=1, workspace=ws, keyBias=kb),
+                    steps, warm)
+    o2 = torch.empty_like(o)
+    ms_plain = timer.time(lambda i: q.enqueueAttentionDecode(Q, kc, ks, vc, vs, o2, T, cfg, qPerKv=nq, kvHeads=kv,
+                                                             tokenStride=kv, headStride=1, workspace=ws),
+                          steps, warm)
+    Kd = torch.empty(n, d, device=dev)
+    Vd = torch.empty(n, d, device=dev)
+
+    def decode_then_attend_bias(i):
+        q.enqueueDecode(kc, ks, Kd, n, cfg, keyBias=kb)
+        q.enqueueDecode(vc, vs, Vd, n, cfg)
+        Kh = Kd.view(T, kv, d).transpose(0, 1).transpose(1, 2).contiguous()
+        S = torch.bmm(Q, Kh) / math.sqrt(d)
+        return torch.bmm(torch.softmax(S, -1), Vd.view(T, kv, d).transpose(0, 1).contiguous())
+
+    ms_b = timer.time(decode_then_attend_bias, max(5, steps // 4), 2)
+    torch.cuda.synchronize()
+    ck = O.unpack_codes(kc.cpu().numpy().tobytes(), n, d, 4).reshape(T, kv, d)[:, 0]
+    cv = O.unpack_codes(vc.cpu().numpy().tobytes(), n, d, 4).reshape(T, kv, d)[:, 0]
+    Ob = O.key_bias_offsets(bias.cpu().numpy(), cos.cpu().numpy(), sin.cpu().numpy(), 0, n, kv).reshape(T, kv, d)
+    Kr = O.turbo_decode(ck, ks.view(T, kv)[:, 0].cpu().numpy().astype(np.float64), 4) + Ob[:, 0]
+    Vr = O.turbo_decode(cv, vs.view(T, kv)[:, 0].cpu().numpy().astype(np.float64), 4)
+    ro, _ = O.attend(Q[0].cpu().numpy().astype(np.float64), Kr, Vr, 1 / math.sqrt(d))
+    got = o[0].cpu().numpy().astype(np.float64)
+    rel = float(max(np.linalg.norm(got[i] - ro[i]) / np.linalg.norm(ro[i]) for i in range(nq)))
+    if rel > 1e-5:
+        raise SystemExit(f"attention parity failed for key-bias removal: rel L2 {rel}")
+    nb = n * 2 * (cfg.codeStride + 4)
+    out["cfg4_qwen_layer_attention_key_bias_T16384"] = {
+        "kv_heads": kv, "q_per_kv": nq, "dim": d, "tokens": T, "ms": round(ms, 5), "ms_without_key_bias": round(ms_plain, 5),
+        "codes_gbps": round(nb / ms / 1e6, 1), "decode_then_attend_ms": round(ms_b, 4),
+        "speedup_vs_decode_then_attend": round(ms_b / ms, 2), "parity_max_rel_l2_head0": rel}
+    del K, V, kc, vc, ks, vs, Kd, Vd, ws, cos, sin
+    torch.cuda.empty_cache()
     return out
 
 

@@ -209,7 +209,7 @@ __device__ __forceinline__ void key_bias_scores(const AttnArgs& a, const float* 
 // WRITE_P go to the workspace for a separate values kernel. The table s_tab holds the key codes' pair values.
 // qp (the rotated queries of this KV head, read-only here) is passed separately so its wave-uniform reads can
 // be scalar loads.
-template <int D, int B, int NQ, bool WRITE_P>
+template <int D, int B, int NQ, bool WRITE_P, bool KB = false>
 __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __restrict__ qp_all, const float2* s_tab,
                                              float* s_s, float* s_red, uint32_t kv, uint32_t c) {
   using P = PairLut<D, B>;
@@ -250,7 +250,7 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
         acc[h] = __builtin_fmaf(qp[(p * NQ + h) * 2 + 1], t.y, acc[h]);
       }
     }
-    if (a.kb_cos) {  // key-bias removal: + q . o_t (position of a token past the chunk's end: its first)
+    if constexpr (KB) {  // key-bias removal: + q . o_t (position of a token past the chunk's end: its first)
       float kb[NQ];
       key_bias_scores<D, NQ>(a, a.ws + WsLayout(a).kbq + (uint64_t)kv * D * NQ * 2, t0 + (valid ? i : 0u), kb);
       if (valid) {
@@ -306,8 +306,8 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
   }
 }
 
-// Workgroup (chunk, KV head); thread = token.
-template <int D, int B, int NQ>
+// Workgroup (chunk, KV head); thread = token. KB: with the key-bias term (such calls always take these kernels).
+template <int D, int B, int NQ, bool KB>
 __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* __restrict__ qp_all) {
   using P = PairLut<D, B>;
   __shared__ float2 s_tab[P::N];
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
   __shared__ float s_red[4 * NQ];
   P::build(s_tab, a.kpolar != 0);
   __syncthreads();
-  scores_phase<D, B, NQ, true>(a, qp_all, s_tab, s_s, s_red, blockIdx.y, blockIdx.x);
+  scores_phase<D, B, NQ, true, KB>(a, qp_all, s_tab, s_s, s_red, blockIdx.y, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------------------------- scores, KIVI keys
@@ -691,7 +691,7 @@ hipError_t launch_nq(const AttnArgs& a, hipStream_t s) {
   constexpr int D = PITCH_DIM;
   const dim3 grid(a.chunks, a.kv_heads);
   const float* qp = a.ws;
-  if (!a.k_ranges && a.kbits == a.vbits && PITCH_ATTN_FUSED) {
+  if (!a.k_ranges && !a.kb_cos && a.kbits == a.vbits && PITCH_ATTN_FUSED) {
     bool done = false;
     switch (a.kbits) {
 #define PITCH_FUSED(B) \
@@ -713,8 +713,11 @@ hipError_t launch_nq(const AttnArgs& a, hipStream_t s) {
     }
   } else {
     switch (a.kbits) {
-#define PITCH_SCORES(B) \
-  case B: hipLaunchKernelGGL((attn_scores<D, B, NQ>), grid, dim3(kBlock), 0, s, a, qp); break;
+#define PITCH_SCORES(B)                                                                          \
+  case B:                                                                                        \
+    if (a.kb_cos) hipLaunchKernelGGL((attn_scores<D, B, NQ, true>), grid, dim3(kBlock), 0, s, a, qp); \
+    else hipLaunchKernelGGL((attn_scores<D, B, NQ, false>), grid, dim3(kBlock), 0, s, a, qp);        \
+    break;
       PITCH_SCORES(2) PITCH_SCORES(3) PITCH_SCORES(4) PITCH_SCORES(5) PITCH_SCORES(6) PITCH_SCORES(7) PITCH_SCORES(8)
 #undef PITCH_SCORES
       default: return hipErrorInvalidValue;
