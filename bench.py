@@ -601,6 +601,7 @@ def run_extras(torch, q, P, O, W, timer, dev, args) -> dict:
     del x2, keys4
     torch.cuda.empty_cache()
     out.update(run_attention(torch, q, P, O, W, timer, gen, dev, args))
+    out.update(run_decode_step(torch, q, P, timer, gen, dev, args))
     out.update(run_key_bias(torch, q, P, timer, gen, dev, args))
     return out
 
@@ -637,6 +638,73 @@ def run_key_bias(torch, q, P, timer, gen, dev, args) -> dict:
                                                      "decode_gbps": round(nb / ms_d / 1e6, 1)}
     del layers
     torch.cuda.empty_cache()
+    return out
+
+
+def run_decode_step(torch, q, P, timer, gen, dev, args) -> dict:
+    """A decode step of the config-5 model (Llama-3-8B: 32 layers, 8 KV x 4 query heads, d = 128; TurboQuant b = 4
+    keys, b = 3 values) over a cache of T tokens: one batched append of the token's keys and one of its values to
+    all 32 layers (pitch_enqueue_encode_batch), then the allocation-free attention of every layer. Timed eagerly
+    and as a replay of the same step captured in a HIP graph (torch.cuda.graph); the replay's outputs must equal
+    the eager ones bit for bit."""
+    out = {}
+    layers, heads, nq, d = 32, 8, 4, 128
+    kcfg, vcfg = P.QuantConfig("turboQuant", d, 4), P.QuantConfig("turboQuant", d, 3)
+    steps, warm = max(20, args.steps), 5
+    for T in (4096, 32768):
+        n = (T + 1) * heads
+        caches = []
+        for _ in range(layers):
+            kc = torch.empty(n * kcfg.codeStride, dtype=torch.uint8, device=dev)
+            vc = torch.empty(n * vcfg.codeStride, dtype=torch.uint8, device=dev)
+            ks, vs = torch.empty(n, device=dev), torch.empty(n, device=dev)
+            x = torch.randn(T * heads, d, generator=gen, device=dev)
+            q.enqueueEncode(x, kc, ks, T * heads, kcfg)
+            q.enqueueEncode(x, vc, vs, T * heads, vcfg)
+            caches.append((kc, ks, vc, vs))
+        new_k = [torch.randn(heads, d, generator=gen, device=dev) for _ in range(layers)]
+        new_v = [torch.randn(heads, d, generator=gen, device=dev) for _ in range(layers)]
+        Q = [torch.randn(heads, nq, d, generator=gen, device=dev) for _ in range(layers)]
+        outs = [torch.empty(heads, nq, d, device=dev) for _ in range(layers)]
+        tk = P.EncodeBatch(q, kcfg, new_k, [c[0] for c in caches], [c[1] for c in caches])
+        tv = P.EncodeBatch(q, vcfg, new_v, [c[2] for c in caches], [c[3] for c in caches])
+
+        def step(i):
+            tk.enqueue(heads, codesOffsets=T * heads * kcfg.codeStride, scalesOffsets=T * heads * 4)
+            tv.enqueue(heads, codesOffsets=T * heads * vcfg.codeStride, scalesOffsets=T * heads * 4)
+            for l in range(layers):
+                c = caches[l]
+                q.enqueueAttentionDecode(Q[l], c[0], c[1], c[2], c[3], outs[l], T + 1, kcfg, vcfg, qPerKv=nq,
+                                         kvHeads=heads, tokenStride=heads, headStride=1, noAlloc=True)
+
+        ms_eager = timer.time(step, steps, warm)
+        torch.cuda.synchronize()
+        ref = [o.clone() for o in outs]
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
+            step(0)
+        torch.cuda.synchronize()
+        for o in outs:
+            o.zero_()
+        ms_graph = timer.time(lambda i: graph.replay(), steps, warm)
+        torch.cuda.synchronize()
+        if not all(torch.equal(a, b) for a, b in zip(outs, ref)):
+            raise SystemExit("decode step: the graph replay's attention differs from the eager step")
+        wall = []
+        for _ in range(20):
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            graph.replay()
+            torch.cuda.synchronize()
+            wall.append((time.perf_counter() - w0) * 1e6)
+        wall.sort()
+        out[f"cfg5_decode_step_32_layers_T{T}"] = {
+            "layers": layers, "kv_heads": heads, "q_per_kv": nq, "tokens": T + 1,
+            "eager_us_per_step_backtoback": round(ms_eager * 1e3, 1),
+            "graph_replay_us_per_step_backtoback": round(ms_graph * 1e3, 1),
+            "graph_replay_wall_us_median": round(wall[len(wall) // 2], 1)}
+        del caches, graph
+        torch.cuda.empty_cache()
     return out
 
 
