@@ -129,7 +129,7 @@ hipError_t launch_vec(uint32_t dim, uint32_t io, bool encode, bool polar, int bi
 }
 
 using VecBatchLaunch = hipError_t (*)(bool, int, const pitch::VecBatchArgs&, hipStream_t);
-using VecBatchVpb = uint32_t (*)();
+using VecBatchVpb = uint32_t (*)(bool);
 
 #define PITCH_VEC_ROW(D) \
   {pitch::launch_vec_batch_d##D##_io0, pitch::launch_vec_batch_d##D##_io1, pitch::launch_vec_batch_d##D##_io2}
@@ -256,7 +256,7 @@ int encode_batch_impl(const pitch_config_t* config, uint32_t io, const pitch_enc
     PITCH_TRY(check_device(it.scales, dev, "scales"));
   }
   const int li = dim_index(dim);
-  const uint64_t vpb = kVecBatchVpb[li][io]();
+  const uint64_t vpb = kVecBatchVpb[li][io](config->method == PITCH_METHOD_POLAR);
   pitch::VecBatchArgs a{};
   a.common.seed = config->seed;
   for (uint32_t i0 = 0; i0 < n; i0 += pitch::kBatchItems) {

@@ -126,11 +126,11 @@ uint64_t stream_decode_min_vectors();
 
 // Per-vector launch for one dimension D and I/O element type IO (0 float32, 1 float16, 2 bfloat16); one
 // object file per (D, IO) defines launch_vec_d<D>_io<IO>, the batched encode launch_vec_batch_d<D>_io<IO> and
-// vec_batch_vpb_d<D>_io<IO>, the vectors each of the batched encode's workgroups takes per round.
+// vec_batch_vpb_d<D>_io<IO>, the vectors each of the batched encode's workgroups takes per round (per method).
 #define PITCH_DECLARE_VEC_LAUNCH_IO(D, IO)                                                                     \
   hipError_t launch_vec_d##D##_io##IO(bool encode, bool polar, int bits, const VecArgs& a, hipStream_t s);      \
   hipError_t launch_vec_batch_d##D##_io##IO(bool polar, int bits, const VecBatchArgs& a, hipStream_t s);        \
-  uint32_t vec_batch_vpb_d##D##_io##IO();
+  uint32_t vec_batch_vpb_d##D##_io##IO(bool polar);
 #define PITCH_DECLARE_VEC_LAUNCH(D) \
   PITCH_DECLARE_VEC_LAUNCH_IO(D, 0) PITCH_DECLARE_VEC_LAUNCH_IO(D, 1) PITCH_DECLARE_VEC_LAUNCH_IO(D, 2)
 PITCH_DECLARE_VEC_LAUNCH(2)

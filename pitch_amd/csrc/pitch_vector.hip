@@ -47,6 +47,29 @@ struct DimConst {
   static constexpr float kInvSqrtF = float(kInvSqrt);
 };
 
+// One segment of an encode: count vectors from in to codes_out / scales_out. A single call has one (the call's
+// own buffers); a batched launch gives each of its workgroups the segment that block_start assigns it.
+struct EncSeg {
+  const void* in;
+  uint32_t* codes_out;
+  float* scales_out;
+  uint64_t count;
+};
+__device__ __forceinline__ EncSeg call_segment(const VecArgs& p) {
+  return EncSeg{p.in, p.codes_out, p.scales_out, p.count};
+}
+// The segment of this workgroup in a batched launch, and the workgroup's index and count within it.
+struct BatchSlot {
+  EncSeg seg;
+  uint64_t block, blocks;
+};
+__device__ __forceinline__ BatchSlot batch_slot(const VecBatchArgs& pb) {
+  uint32_t i = 0;  // uniform: kernel arguments and the block index
+  for (uint32_t j = 1; j < pb.items; ++j) i = pb.block_start[j] <= blockIdx.x ? j : i;
+  return BatchSlot{EncSeg{pb.in[i], pb.codes_out[i], pb.scales_out[i], pb.count[i]},
+                   (uint64_t)(blockIdx.x - pb.block_start[i]), (uint64_t)(pb.block_start[i + 1] - pb.block_start[i])};
+}
+
 constexpr double kTwoPi = 0x1.921fb54442d18p+2;  // 2 * np.pi
 
 // Fast PolarQuant quantisation. A radius or angle code is floor(t) with t = value * levels + 0.5
@@ -657,15 +680,13 @@ __global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode(VecArgs 
 }
 
 // A batch of independent segments with one configuration in one launch (pitch_enqueue_encode_batch): the blocks
-// [block_start[i], block_start[i + 1]) encode segment i with the team encoder.
+// [block_start[i], block_start[i + 1]) encode segment i. Each encoder below has such a batched form, and a batch
+// runs the one a single call of its configuration runs (enc_kind), so both write the same bytes.
 template <int D, int B, bool POLAR, int IO>
 __global__ __launch_bounds__(kBlock, PITCH_POLAR_WAVES) void vec_encode_batch(VecBatchArgs pb) {
-  uint32_t i = 0;  // the segment of this block (uniform: kernel arguments and the block index)
-  for (uint32_t j = 1; j < pb.items; ++j) i = pb.block_start[j] <= blockIdx.x ? j : i;
-  const uint64_t nb = pb.block_start[i + 1] - pb.block_start[i];
-  vec_encode_run<D, B, POLAR, IO, false>(pb.common, pb.in[i], pb.codes_out[i], pb.scales_out[i], pb.count[i],
-                                         (uint64_t)(blockIdx.x - pb.block_start[i]) * Geom<D>::VPB,
-                                         nb * Geom<D>::VPB);
+  const BatchSlot s = batch_slot(pb);
+  vec_encode_run<D, B, POLAR, IO, false>(pb.common, s.seg.in, s.seg.codes_out, s.seg.scales_out, s.seg.count,
+                                         s.block * Geom<D>::VPB, s.blocks * Geom<D>::VPB);
 }
 
 // ----------------------------------------------------------------------------------------------------
@@ -1178,8 +1199,7 @@ __device__ __forceinline__ void chunk_floats(const u32x4& w, float (&f)[Io<IO>::
 }
 
 template <int D, int B, int IO, bool KBIAS>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(PITCH_ENC_WAVES)))
-void tq_encode_lpv(VecArgs p) {
+__device__ __forceinline__ void lpv_run(const VecArgs& p, const EncSeg sg, uint64_t block, uint64_t nblocks) {
   using Lp = Lpv<D, IO>;
   constexpr int K = Lp::K;
   constexpr int E = Lp::E, T = Lp::T, V = Lp::V;
@@ -1199,7 +1219,7 @@ void tq_encode_lpv(VecArgs p) {
   // software pipeline: the next block's loads are in flight while this block is computed; the first block's
   // loads are issued before the table set-up so the two latencies overlap
   u32x4 pf[Lp::QPL];
-  if ((uint64_t)blockIdx.x * V < p.count) lpv_fetch<D, IO>(p.in, (uint64_t)blockIdx.x * V, p.count, lane, pf);
+  if (block * V < sg.count) lpv_fetch<D, IO>(sg.in, block * V, sg.count, lane, pf);
 #endif
   Q::load(s_q, lane, 64);
   // Every 16-byte chunk this lane stages holds coordinates K * pq .. K * pq + K - 1 with pq = lane % QPV (64 is
@@ -1210,12 +1230,12 @@ void tq_encode_lpv(VecArgs p) {
   for (int r = 0; r < K; ++r)
     smask[r] = sign_is_negative(p.seed, (uint32_t)(K * (lane % Lp::QPV) + r)) ? 0x80000000u : 0u;
   __syncthreads();
-  for (uint64_t base = (uint64_t)blockIdx.x * V; base < p.count; base += (uint64_t)gridDim.x * V) {
+  for (uint64_t base = block * V; base < sg.count; base += nblocks * V) {
     // stage the wave's block of V vectors in LDS with coalesced loads
     {
 #if !PITCH_ENC_PREFETCH
       u32x4 pf[Lp::QPL];
-      lpv_fetch<D, IO>(p.in, base, p.count, lane, pf);
+      lpv_fetch<D, IO>(sg.in, base, sg.count, lane, pf);
 #endif
 #pragma unroll
       for (int i = 0; i < Lp::QPL; ++i) {
@@ -1226,7 +1246,7 @@ void tq_encode_lpv(VecArgs p) {
         chunk_floats<IO>(pf[i], fv);
         if constexpr (KBIAS) {  // key-bias removal: encode x - o (mechanism_eval.py:113-116)
           float o[K];
-          key_bias_offset<D, K>(p, base + vq < p.count ? base + vq : p.count - 1, K * pq, o);
+          key_bias_offset<D, K>(p, base + vq < sg.count ? base + vq : sg.count - 1, K * pq, o);
 #pragma unroll
           for (int r = 0; r < K; ++r) fv[r] = fv[r] - o[r];
         }
@@ -1237,8 +1257,8 @@ void tq_encode_lpv(VecArgs p) {
           *(float4*)(s_in + vq * Lp::STRIDE + h * Lp::HALF + pe + r) = float4{fv[r], fv[r + 1], fv[r + 2], fv[r + 3]};
       }
 #if PITCH_ENC_PREFETCH
-      const uint64_t nb = base + (uint64_t)gridDim.x * V;
-      if (nb < p.count) lpv_fetch<D, IO>(p.in, nb, p.count, lane, pf);
+      const uint64_t nb = base + nblocks * V;
+      if (nb < sg.count) lpv_fetch<D, IO>(sg.in, nb, sg.count, lane, pf);
 #endif
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1270,17 +1290,17 @@ void tq_encode_lpv(VecArgs p) {
     Q::codes_packed(s_q, x, us, w);
 #pragma unroll
     for (int i = 0; i < NWL; ++i) s_codes[vw * NW + t * NWL + i] = w[i];
-    if (t == 0 && base + vw < p.count) p.scales_out[base + vw] = (float)nrm;
+    if (t == 0 && base + vw < sg.count) sg.scales_out[base + vw] = (float)nrm;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // write the wave's V * NW code words contiguously, in the widest chunks that stay inside one vector
     constexpr int CW = NW % 4 == 0 ? 4 : (NW % 2 == 0 ? 2 : 1);
-    uint32_t* dst = p.codes_out + base * NW;
+    uint32_t* dst = sg.codes_out + base * NW;
 #pragma unroll
     for (int i = 0; i < (V * NW / CW + 63) / 64; ++i) {
       const int q = lane + 64 * i;
-      if (q < V * NW / CW && base + (q * CW) / NW < p.count) {
+      if (q < V * NW / CW && base + (q * CW) / NW < sg.count) {
         if constexpr (CW == 4) *(u32x4*)(dst + 4 * q) = *(const u32x4*)(s_codes + 4 * q);
         else if constexpr (CW == 2) *(u32x2*)(dst + 2 * q) = *(const u32x2*)(s_codes + 2 * q);
         else dst[q] = s_codes[q];
@@ -1288,6 +1308,19 @@ void tq_encode_lpv(VecArgs p) {
     }
     __builtin_amdgcn_wave_barrier();
   }
+}
+
+template <int D, int B, int IO, bool KBIAS>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(PITCH_ENC_WAVES)))
+void tq_encode_lpv(VecArgs p) {
+  lpv_run<D, B, IO, KBIAS>(p, call_segment(p), blockIdx.x, gridDim.x);
+}
+
+template <int D, int B, int IO>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(PITCH_ENC_WAVES)))
+void tq_encode_lpv_batch(VecBatchArgs pb) {
+  const BatchSlot s = batch_slot(pb);
+  lpv_run<D, B, IO, false>(pb.common, s.seg, s.block, s.blocks);
 }
 
 // ----------------------------------------------------------------------------------------------------
@@ -1430,8 +1463,9 @@ void fill_hs_flips(uint32_t seed, uint32_t* out) {
 // bits, the LDS rows of the set's compute lanes, which then read their coordinates into x. neg[i * 4 + k] is
 // the lane mask of the sign of element k of chunk i (fill_hs_flips).
 template <int D, int T, bool KBIAS>
-__device__ __forceinline__ void hs_stage(const VecArgs& p, const u32x4 (&pf)[Hs<D, T>::QPL], uint64_t base, int lane,
-                                         const uint64_t* neg, double* sx, double (&x)[Hs<D, T>::E]) {
+__device__ __forceinline__ void hs_stage(const VecArgs& p, uint64_t count, const u32x4 (&pf)[Hs<D, T>::QPL],
+                                         uint64_t base, int lane, const uint64_t* neg, double* sx,
+                                         double (&x)[Hs<D, T>::E]) {
   using H = Hs<D, T>;
   constexpr int E = H::E;
   const int pp = lane % H::SL, vs = lane / H::SL;
@@ -1446,7 +1480,7 @@ __device__ __forceinline__ void hs_stage(const VecArgs& p, const u32x4 (&pf)[Hs<
       if constexpr (KBIAS) {  // key-bias removal: encode x - o (mechanism_eval.py:113-116)
         float o[4];
         const uint64_t v = base + s * H::VPS + vs;
-        key_bias_offset<D, 4>(p, v < p.count ? v : p.count - 1, 4 * pp + E * i, o);
+        key_bias_offset<D, 4>(p, v < count ? v : count - 1, 4 * pp + E * i, o);
 #pragma unroll
         for (int k = 0; k < 4; ++k) f[k] = f[k] - o[k];
       }
@@ -1513,7 +1547,7 @@ __device__ __forceinline__ void put_code(uint32_t (&w)[NWL], int pos, uint32_t c
 
 template <int D, int T, int B, int NWL>
 __device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w)[NWL]) {
-  constexpr int E = Hs<D, T>::E, NP = E / 2, L = 1 << B;
+  constexpr int E = D / T, NP = E / 2, L = 1 << B;
   constexpr bool kSectors = B <= 5;
   constexpr float kRg = polar_radius_guard<B>();
   fwht_contig<E, 1, double>(x, 0);
@@ -1565,7 +1599,7 @@ __device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w
 // Compute phase of one block: the in-lane stages, the quantisation (TurboQuant: norm and bucket table;
 // PolarQuant: hs_polar_codes) and the stores.
 template <int D, int T, int B, bool POLAR>
-__device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLut8<D, B>::Smem& sq, uint64_t base,
+__device__ __forceinline__ void hs_compute(const EncSeg& sg, const typename TqLut8<D, B>::Smem& sq, uint64_t base,
                                            int lane, double* sx, double (&x)[Hs<D, T>::E]) {
   using H = Hs<D, T>;
   using Q = TqLut8<D, B>;
@@ -1599,14 +1633,14 @@ __device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLu
   // wait for the next block's loads without waiting for these stores (gfx9 counts loads and stores together,
   // in order). A vector past the end was loaded from the last vector (hs_fetch), so its codes and scale equal
   // the last vector's and are written to that vector's place: the same bytes to the same address.
-  const uint64_t vst = base + vw < p.count ? base + vw : p.count - 1;
+  const uint64_t vst = base + vw < sg.count ? base + vw : sg.count - 1;
   // the T lanes of a team write the same scale; cached (a wave writes 64 bytes of scales, half a line, which L2
   // merges with the next wave's)
-  p.scales_out[vst] = nrm;
+  sg.scales_out[vst] = nrm;
   if constexpr (kWhole) {
     // lane (vw, t) owns words t * NWL .. of its vector: the wave's stores are one contiguous run
-    if constexpr (PITCH_HS_NT) store_words_nt(p.codes_out + vst * NW + t * NWL, w);
-    else store_words(p.codes_out + vst * NW + t * NWL, w);
+    if constexpr (PITCH_HS_NT) store_words_nt(sg.codes_out + vst * NW + t * NWL, w);
+    else store_words(sg.codes_out + vst * NW + t * NWL, w);
   } else {
     // E * B = 16 B bits per lane: odd lanes start half-way into a word. Shift their bits up by 16, then
     // the even lane of each pair takes the odd lane's first (shared) word into its last one.
@@ -1635,8 +1669,8 @@ __device__ __forceinline__ void hs_compute(const VecArgs& p, const typename TqLu
     for (int i = 0; i < (NCH + 63) / 64; ++i) {
       const int q = min(lane + 64 * i, NCH - 1);
       const int vq = q / CPV;
-      const uint64_t vd = base + vq < p.count ? base + vq : p.count - 1;
-      uint32_t* dst = p.codes_out + vd * NW + CW * (q - vq * CPV);
+      const uint64_t vd = base + vq < sg.count ? base + vq : sg.count - 1;
+      uint32_t* dst = sg.codes_out + vd * NW + CW * (q - vq * CPV);
       if constexpr (CW == 4) store_v((u32x4*)dst, *(const u32x4*)(sc + 4 * q), PITCH_HS_NT);
       else if constexpr (CW == 2) store_v((u32x2*)dst, *(const u32x2*)(sc + 2 * q), PITCH_HS_NT);
       else store_v(dst, sc[q], PITCH_HS_NT);
@@ -1661,8 +1695,7 @@ constexpr int hs_waves() {
 }
 
 template <int D, int B, bool POLAR, bool KBIAS>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hs_waves<D, POLAR, KBIAS>())))
-void vec_encode_hs(VecArgs p) {
+__device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64_t block, uint64_t nblocks) {
   constexpr int T = hs_team<D>();
   using H = Hs<D, T>;
   constexpr int E = H::E, V = H::V;
@@ -1671,9 +1704,9 @@ void vec_encode_hs(VecArgs p) {
   __shared__ __attribute__((aligned(16))) typename Q::Smem s_q;  // (unused by PolarQuant)
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const float* in = (const float*)p.in;
-  const uint64_t stride = (uint64_t)gridDim.x * H::WAVES * V;
-  uint64_t base = ((uint64_t)blockIdx.x * H::WAVES + wave) * V;
+  const float* in = (const float*)sg.in;
+  const uint64_t stride = nblocks * H::WAVES * V;
+  uint64_t base = (block * H::WAVES + wave) * V;
   // Software pipeline with PFD blocks of loads in flight. The loop is rotated so that each block's loads are
   // waited for in straight-line code after exactly the stores of the block before (two or so operations):
   // an iteration issues the loads of block k + PFD, computes and stores block k, then stages block k + 1.
@@ -1683,38 +1716,269 @@ void vec_encode_hs(VecArgs p) {
   if constexpr (!POLAR) Q::load(s_q, threadIdx.x, 64 * H::WAVES);
   const uint64_t* neg = (const uint64_t*)p.lane_flips;  // fill_hs_flips; kernel arguments, read as scalars
   __syncthreads();
-  if (base >= p.count) return;
+  if (base >= sg.count) return;
   double* sx = s_x[wave];
   u32x4 pfa[H::QPL];
   u32x4 pfb[PFD > 1 ? H::QPL : 1];
   double x[E];
   // every fetch is unconditional, like the stores: a block past the end re-reads the last vector (a cache hit)
-  hs_fetch<D, T>(in, base, p.count, lane, pfa);
-  if constexpr (PFD > 1) hs_fetch<D, T>(in, base + stride, p.count, lane, pfb);
-  hs_stage<D, T, KBIAS>(p, pfa, base, lane, neg, sx, x);
+  hs_fetch<D, T>(in, base, sg.count, lane, pfa);
+  if constexpr (PFD > 1) hs_fetch<D, T>(in, base + stride, sg.count, lane, pfb);
+  hs_stage<D, T, KBIAS>(p, sg.count, pfa, base, lane, neg, sx, x);
   auto step = [&](u32x4 (&refill)[H::QPL], u32x4 (&next)[H::QPL]) {
-    hs_fetch<D, T>(in, base + (uint64_t)PFD * stride, p.count, lane, refill);
+    hs_fetch<D, T>(in, base + (uint64_t)PFD * stride, sg.count, lane, refill);
     __builtin_amdgcn_sched_barrier(0);  // the loads go out before the compute, not interleaved into it
-    hs_compute<D, T, B, POLAR>(p, s_q, base, lane, sx, x);
+    hs_compute<D, T, B, POLAR>(sg, s_q, base, lane, sx, x);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // the next block's staging waits for its loads: keep all of it after the compute
     __builtin_amdgcn_sched_barrier(0);
     base += stride;
-    hs_stage<D, T, KBIAS>(p, next, base, lane, neg, sx, x);  // past the end: staged, never computed
+    hs_stage<D, T, KBIAS>(p, sg.count, next, base, lane, neg, sx, x);  // past the end: staged, never computed
   };
   if constexpr (PFD > 1) {
     while (true) {
       step(pfa, pfb);
-      if (base >= p.count) break;
+      if (base >= sg.count) break;
       step(pfb, pfa);
-      if (base >= p.count) break;
+      if (base >= sg.count) break;
     }
   } else {
-    while (base < p.count) step(pfa, pfa);
+    while (base < sg.count) step(pfa, pfa);
   }
 }
+
+template <int D, int B, bool POLAR, bool KBIAS>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hs_waves<D, POLAR, KBIAS>())))
+void vec_encode_hs(VecArgs p) {
+  hs_run<D, B, POLAR, KBIAS>(p, call_segment(p), blockIdx.x, gridDim.x);
+}
+
+template <int D, int B, bool POLAR>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hs_waves<D, POLAR, false>())))
+void vec_encode_hs_batch(VecBatchArgs pb) {
+  const BatchSlot s = batch_slot(pb);
+  hs_run<D, B, POLAR, false>(pb.common, s.seg, s.block, s.blocks);
+}
+
+// ----------------------------------------------------------------------------------------------------
+// LDS-transposed encoder for float32 vectors at D = 256, 512 and 1024 (both methods). A vector is held by a
+// team of T = D / 32 lanes, twice over:
+// - staging: team lane p loads the D / 32 chunks of CW = 1024 / D consecutive floats at coordinates
+//   CW p + 32 j (j = 0 .. T - 1; each load instruction reads 128 contiguous bytes of every vector), applies the
+//   rotation signs (one v_cndmask with a lane mask each), widens to float64 and runs the butterfly stages on
+//   coordinate bits 5 and above in registers (they select the chunk j);
+// - compute: after an exchange through LDS (row j of a vector = coordinates 32 j .. 32 j + 31), team lane q holds
+//   the 32 contiguous coordinates 32 q + e and runs the stages on bits 0 .. 4 in registers.
+// No butterfly crosses lanes (the team encoder at these sizes exchanges float64 values between lanes at 5 of
+// the 10 stages, two moves and an fma per coordinate and stage), and each lane packs its 32 codes into B whole
+// words. Half of each vector's rows pass through LDS at a time, so a wave needs 8.5 KB of LDS.
+template <int D>
+struct Lt {
+  static constexpr int T = D / 32;          // team lanes per vector
+  static constexpr int V = 64 / T;          // vectors per wave iteration
+  static constexpr int CW = 1024 / D;       // consecutive floats per staged chunk
+  static constexpr int NJ = 32 / CW;        // chunks per staging lane (= T)
+  static constexpr int RS = 34;             // float64 per LDS row: 32 and 2 of padding, so rows are 16 bytes
+                                            // apart modulo 128 and 8 lanes reading 16 bytes each hit distinct banks
+  static constexpr int HR = T / 2;          // rows of a vector staged per pass
+  static constexpr int ROWS = V * HR * RS;  // float64 of LDS per wave
+  static constexpr int WAVES = kBlock / 64;
+  static_assert(D >= 256 && D <= 1024 && NJ == T && HR >= 1, "geometry");
+};
+
+// Lane masks of the rotation signs (host side): bit b of word j * CW + r is set when coordinate
+// CW (b % T) + r + 32 j, the one lane b (and lane b + 32) stages as element r of chunk j, has sign -1.
+template <int D>
+void fill_lt_flips(uint32_t seed, uint32_t* out) {
+  using L = Lt<D>;
+  static_assert(L::NJ * L::CW == 32, "one mask word per staged coordinate of a lane");
+  thread_local uint32_t cached_seed = 0;
+  thread_local bool have = false;
+  thread_local uint32_t cached[32];
+  if (!have || cached_seed != seed) {
+    for (int j = 0; j < L::NJ; ++j)
+      for (int r = 0; r < L::CW; ++r) {
+        uint32_t m = 0u;
+        for (int b = 0; b < 32; ++b)
+          if (sign_is_negative(seed, (uint32_t)(L::CW * (b % L::T) + r + 32 * j))) m |= 1u << b;
+        cached[j * L::CW + r] = m;
+      }
+    cached_seed = seed;
+    have = true;
+  }
+  for (int j = 0; j < 32; ++j) out[j] = cached[j];
+}
+
+// Loads of a wave's block of V vectors (vectors past the end re-read the last one).
+template <int D>
+__device__ __forceinline__ void lt_fetch(const float* in, uint64_t base, uint64_t count, int lane, uint32_t (&pf)[32]) {
+  using L = Lt<D>;
+  const uint64_t v = base + lane / L::T;
+  const float* row = in + (v < count ? v : count - 1) * D + L::CW * (lane % L::T);
+#pragma unroll
+  for (int j = 0; j < L::NJ; ++j) {
+    if constexpr (L::CW == 4) {
+      const u32x4 c = __builtin_nontemporal_load((const u32x4*)(row + 32 * j));
+      pf[4 * j] = c.x, pf[4 * j + 1] = c.y, pf[4 * j + 2] = c.z, pf[4 * j + 3] = c.w;
+    } else if constexpr (L::CW == 2) {
+      const u32x2 c = __builtin_nontemporal_load((const u32x2*)(row + 32 * j));
+      pf[2 * j] = c.x, pf[2 * j + 1] = c.y;
+    } else {
+      pf[j] = __builtin_nontemporal_load((const uint32_t*)(row + 32 * j));
+    }
+  }
+}
+
+// Staging of one block (see Lt): signs, float64, the stages on coordinate bits 5 and above, then two passes
+// through the wave's LDS rows, each for half of every vector's rows, after which lane q of a vector holds its
+// coordinates 32 q .. 32 q + 31 in x.
+template <int D>
+__device__ __forceinline__ void lt_stage(const uint32_t* neg, const uint32_t (&pf)[32], int lane, double* sx,
+                                         double (&x)[32]) {
+  using L = Lt<D>;
+  constexpr int CW = L::CW, NJ = L::NJ, HR = L::HR;
+  double y[NJ][CW];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < CW; ++r) {
+      const uint32_t m = neg[j * CW + r];
+      y[j][r] = (double)neg_lanes(__uint_as_float(pf[j * CW + r]), (uint64_t)m | ((uint64_t)m << 32));
+    }
+#pragma unroll
+  for (int h = 1; h < NJ; h <<= 1)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (!(j & h))
+#pragma unroll
+        for (int r = 0; r < CW; ++r) {
+          const double a = y[j][r], b = y[j | h][r];
+          y[j][r] = a + b;
+          y[j | h][r] = a - b;
+        }
+  const int tl = lane % L::T;
+  double* vrows = sx + (lane / L::T) * HR * L::RS;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+#pragma unroll
+    for (int jj = 0; jj < HR; ++jj) {
+      double* dst = vrows + jj * L::RS + CW * tl;
+      if constexpr (CW == 4) {
+        *(double2*)dst = double2{y[s * HR + jj][0], y[s * HR + jj][1]};
+        *(double2*)(dst + 2) = double2{y[s * HR + jj][2], y[s * HR + jj][3]};
+      } else if constexpr (CW == 2) {
+        *(double2*)dst = double2{y[s * HR + jj][0], y[s * HR + jj][1]};
+      } else {
+        *dst = y[s * HR + jj][0];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (tl / HR == s) {
+      const double* src = vrows + (tl - s * HR) * L::RS;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const double2 v2 = *(const double2*)(src + 2 * k);
+        x[2 * k] = v2.x;
+        x[2 * k + 1] = v2.y;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+// Compute phase of one block: the stages on bits 0 .. 4, the quantisation (TurboQuant: norm and bucket table;
+// PolarQuant: hs_polar_codes) and the stores. As in the staged-stage encoder every store is unconditional: a
+// vector past the end was loaded from the last vector, so its codes and scale are that vector's.
+template <int D, int B, bool POLAR>
+__device__ __forceinline__ void lt_compute(const EncSeg& sg, const typename TqLut8<D, B>::Smem& sq, uint64_t base,
+                                           int lane, double (&x)[32]) {
+  using L = Lt<D>;
+  using Q = TqLut8<D, B>;
+  constexpr int NW = D * B / 32;  // code words per vector; a lane's 32 codes are B of them
+  const int tl = lane % L::T;
+  uint32_t w[B];
+  float nrm;
+  if constexpr (POLAR) {
+    nrm = hs_polar_codes<D, L::T, B, B>(x, w);
+  } else {
+    // ||x||^2 = sum of squares after the staging stages / T (each stage doubles it exactly)
+    double ss[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int e = 0; e < 32; ++e) ss[e & 3] = __builtin_fma(x[e], x[e], ss[e & 3]);
+    double n2 = (ss[0] + ss[1]) + (ss[2] + ss[3]);
+    n2 = team_reduce<L::T>(n2, [](double a, double b) { return a + b; }) * (1.0 / L::T);
+    fwht_contig<32, 1, double>(x, 0);
+    double h;
+    const double g = sqrt_and_half_rsqrt(n2, h);
+    const bool zero = !(n2 > 0.0);
+    nrm = zero ? 0.f : (float)g;
+    // u = H(s * x) / (||x|| sqrt(d)) (pitch_reference.py:96-98); a zero vector is divided by 1
+    const double us = zero ? DimConst<D>::kInvSqrt : (2.0 * h) * DimConst<D>::kInvSqrt;
+    Q::template codes_packed<8>(sq, x, us, lane, w);
+  }
+  const uint64_t v = base + lane / L::T;
+  const uint64_t vst = v < sg.count ? v : sg.count - 1;
+  sg.scales_out[vst] = nrm;
+  store_words_nt(sg.codes_out + vst * NW + tl * B, w);
+}
+
+#ifndef PITCH_LT_WAVES
+#define PITCH_LT_WAVES 2  // waves per SIMD the LDS-transposed encoder's registers must allow
+#endif
+
+template <int D, int B, bool POLAR>
+__device__ __forceinline__ void lt_run(const VecArgs& p, const EncSeg sg, uint64_t block, uint64_t nblocks) {
+  using L = Lt<D>;
+  using Q = TqLut8<D, B>;
+  __shared__ __attribute__((aligned(16))) double s_x[L::WAVES][L::ROWS];
+  __shared__ __attribute__((aligned(16))) typename Q::Smem s_q;  // (unused by PolarQuant)
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const float* in = (const float*)sg.in;
+  const uint64_t stride = nblocks * L::WAVES * L::V;
+  uint64_t base = (block * L::WAVES + wave) * L::V;
+  if constexpr (!POLAR) Q::load(s_q, threadIdx.x, kBlock);
+  const uint32_t* neg = p.lane_flips;  // fill_lt_flips; kernel arguments, read as scalars
+  __syncthreads();
+  if (base >= sg.count) return;
+  double* sx = s_x[wave];
+  uint32_t pf[32];
+  double x[32];
+  // Software pipeline as in the staged-stage encoder: an iteration issues the loads of block k + 1, computes and
+  // stores block k, then stages block k + 1 (past the end: re-reads of the last vector, staged, never computed).
+  lt_fetch<D>(in, base, sg.count, lane, pf);
+  lt_stage<D>(neg, pf, lane, sx, x);
+  while (base < sg.count) {
+    lt_fetch<D>(in, base + stride, sg.count, lane, pf);
+    __builtin_amdgcn_sched_barrier(0);
+    lt_compute<D, B, POLAR>(sg, s_q, base, lane, x);
+    __builtin_amdgcn_sched_barrier(0);
+    base += stride;
+    lt_stage<D>(neg, pf, lane, sx, x);
+  }
+}
+
+template <int D, int B, bool POLAR>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_LT_WAVES)))
+void vec_encode_lt(VecArgs p) {
+  lt_run<D, B, POLAR>(p, call_segment(p), blockIdx.x, gridDim.x);
+}
+
+template <int D, int B, bool POLAR>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_LT_WAVES)))
+void vec_encode_lt_batch(VecBatchArgs pb) {
+  const BatchSlot s = batch_slot(pb);
+  lt_run<D, B, POLAR>(pb.common, s.seg, s.block, s.blocks);
+}
+
+#ifndef PITCH_LT_ENCODER
+#define PITCH_LT_ENCODER 1  // 1: float32 encode at D = 256 .. 1024 uses vec_encode_lt
+#endif
 
 #ifndef PITCH_HS_ENCODER
 #define PITCH_HS_ENCODER 1  // 1: float32 TurboQuant encode at D = 64 / 128 uses vec_encode_hs
@@ -1726,11 +1990,31 @@ void vec_encode_hs(VecArgs p) {
 template <int D>
 constexpr bool use_lpv_encoder() { return D >= 8 && D <= 128; }
 
+// The encoder a call runs; a batched encode runs the same one for each of its segments.
+enum class EncKind { kStaged, kTransposed, kLanePerVector, kTeam };
+template <int D, bool POLAR, int IO, bool KBIAS>
+constexpr EncKind enc_kind() {
+  if (IO == 0 && (POLAR ? PITCH_HS_POLAR : PITCH_HS_ENCODER) && (D == 64 || D == 128)) return EncKind::kStaged;
+  if (IO == 0 && !KBIAS && PITCH_LT_ENCODER && D >= 256) return EncKind::kTransposed;
+  if (!POLAR && use_lpv_encoder<D>()) return EncKind::kLanePerVector;
+  return EncKind::kTeam;
+}
+// Vectors a workgroup of that encoder (without key bias) takes per round.
+template <int D, bool POLAR, int IO>
+constexpr uint32_t enc_vectors_per_block() {
+  constexpr EncKind k = enc_kind<D, POLAR, IO, false>();
+  if constexpr (k == EncKind::kStaged) return Hs<D, hs_team<D>()>::WAVES * Hs<D, hs_team<D>()>::V;
+  else if constexpr (k == EncKind::kTransposed) return Lt<D>::WAVES * Lt<D>::V;
+  else if constexpr (k == EncKind::kLanePerVector) return Lpv<D, IO>::V;
+  else return Geom<D>::VPB;
+}
+
 template <int D, int B, bool POLAR, int IO, bool KBIAS>
 hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   using G = Geom<D>;
   VecArgs a = args;
-  if constexpr (IO == 0 && (POLAR ? PITCH_HS_POLAR : PITCH_HS_ENCODER) && (D == 64 || D == 128)) {
+  constexpr EncKind kEnc = enc_kind<D, POLAR, IO, KBIAS>();
+  if constexpr (kEnc == EncKind::kStaged) {
     if (encode) {
       using H = Hs<D, hs_team<D>()>;
       fill_hs_flips<D, hs_team<D>()>(a.seed, a.lane_flips);
@@ -1757,7 +2041,18 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
       return hipGetLastError();
     }
   }
-  if constexpr (!POLAR && use_lpv_encoder<D>()) {
+  if constexpr (kEnc == EncKind::kTransposed) {
+    if (encode) {
+      using L = Lt<D>;
+      fill_lt_flips<D>(a.seed, a.lane_flips);
+      const uint64_t need = (a.count + L::WAVES * L::V - 1) / (L::WAVES * L::V);
+      const void* k = (const void*)&vec_encode_lt<D, B, POLAR>;
+      const uint64_t grid = persistent_grid(k, need);
+      hipLaunchKernelGGL((vec_encode_lt<D, B, POLAR>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  if constexpr (kEnc == EncKind::kLanePerVector) {
     if (encode) {
       constexpr int V = Lpv<D, IO>::V;
       const uint64_t need = (a.count + V - 1) / V;
@@ -1841,8 +2136,20 @@ hipError_t launch_bits(bool encode, bool polar, const VecArgs& a, hipStream_t s)
 namespace {
 template <int D, int B, bool POLAR>
 hipError_t launch_batch(VecBatchArgs a, hipStream_t s) {
-  fill_lane_flips<D>(a.common.seed, a.common.lane_flips);
-  hipLaunchKernelGGL((vec_encode_batch<D, B, POLAR, PITCH_IO>), dim3(a.block_start[a.items]), dim3(kBlock), 0, s, a);
+  constexpr EncKind k = enc_kind<D, POLAR, PITCH_IO, false>();
+  const dim3 grid(a.block_start[a.items]);
+  if constexpr (k == EncKind::kStaged) {
+    fill_hs_flips<D, hs_team<D>()>(a.common.seed, a.common.lane_flips);
+    hipLaunchKernelGGL((vec_encode_hs_batch<D, B, POLAR>), grid, dim3(kBlock), 0, s, a);
+  } else if constexpr (k == EncKind::kTransposed) {
+    fill_lt_flips<D>(a.common.seed, a.common.lane_flips);
+    hipLaunchKernelGGL((vec_encode_lt_batch<D, B, POLAR>), grid, dim3(kBlock), 0, s, a);
+  } else if constexpr (k == EncKind::kLanePerVector) {
+    hipLaunchKernelGGL((tq_encode_lpv_batch<D, B, PITCH_IO>), grid, dim3(64), 0, s, a);
+  } else {
+    fill_lane_flips<D>(a.common.seed, a.common.lane_flips);
+    hipLaunchKernelGGL((vec_encode_batch<D, B, POLAR, PITCH_IO>), grid, dim3(kBlock), 0, s, a);
+  }
   return hipGetLastError();
 }
 template <int D, int B>
@@ -1851,7 +2158,9 @@ hipError_t launch_batch_bits(bool polar, const VecBatchArgs& a, hipStream_t s) {
 }
 }  // namespace
 
-uint32_t PITCH_CAT(PITCH_CAT(PITCH_CAT(vec_batch_vpb_d, PITCH_DIM), _io), PITCH_IO)() { return Geom<PITCH_DIM>::VPB; }
+uint32_t PITCH_CAT(PITCH_CAT(PITCH_CAT(vec_batch_vpb_d, PITCH_DIM), _io), PITCH_IO)(bool polar) {
+  return polar ? enc_vectors_per_block<PITCH_DIM, true, PITCH_IO>() : enc_vectors_per_block<PITCH_DIM, false, PITCH_IO>();
+}
 
 hipError_t PITCH_CAT(PITCH_CAT(PITCH_CAT(launch_vec_batch_d, PITCH_DIM), _io), PITCH_IO)(bool polar, int bits,
                                                                                     const VecBatchArgs& a,

@@ -1,9 +1,9 @@
 """GPU tests of the batched encode (pitch_enqueue_encode_batch, PITCH.enqueueEncodeBatch, EncodeBatch).
 
-A batch must write exactly what one enqueueEncode per segment writes (codes and scales bit for bit), for every
-method, element type and a spread of dimensions and bit widths, with ragged segment lengths, segments in
-separate buffers and at byte offsets, more segments than one launch takes (32), and a segment long enough to
-loop over its rounds. A batch with one invalid segment launches nothing. The single-call encoders are pinned
+A batch must write exactly what one enqueueEncode per segment writes (codes and scales bit for bit: it runs the
+encoder a single call of its configuration runs), for every method, element type and a spread of dimensions and
+bit widths, with ragged segment lengths, segments in separate buffers and at byte offsets, more segments than one
+launch takes (32), and a segment long enough to loop over its rounds. A batch with one invalid segment launches nothing. The single-call encoders are pinned
 against the oracle elsewhere (test_gpu_parity.py); one case here also checks sampled rows against the oracle
 directly (pitch_reference.py:92-121).
 """
@@ -39,10 +39,15 @@ def _singles(q, segs, cfg, torch):
     return out
 
 
+# Every encoder a single call can run, so every batched form: the staged-stage encoder (float32, d = 64 / 128),
+# the LDS-transposed one (float32, d >= 256; b = 8 has the densest decision edges), the lane-per-vector
+# TurboQuant encoder (float32 d = 8 .. 32, 16-bit d = 64 / 128) and the team encoder (the rest).
 CASES = [("turboQuant", 64, 3, "float32"), ("turboQuant", 128, 4, "float32"), ("polarQuant", 128, 4, "float32"),
-         ("polarQuant", 64, 2, "float16"), ("turboQuant", 128, 8, "bfloat16"), ("turboQuant", 2, 5, "float32"),
-         ("polarQuant", 16, 7, "float32"), ("turboQuant", 256, 3, "float16"), ("turboQuant", 1024, 2, "float32"),
-         ("polarQuant", 512, 6, "bfloat16")]
+         ("polarQuant", 64, 5, "float32"),
+         ("turboQuant", 1024, 2, "float32"), ("turboQuant", 256, 8, "float32"), ("polarQuant", 512, 3, "float32"),
+         ("turboQuant", 32, 3, "float32"), ("turboQuant", 64, 4, "float16"), ("turboQuant", 128, 8, "bfloat16"),
+         ("polarQuant", 64, 2, "float16"), ("turboQuant", 2, 5, "float32"), ("polarQuant", 16, 7, "float32"),
+         ("turboQuant", 256, 3, "float16"), ("polarQuant", 512, 6, "bfloat16")]
 
 
 @pytest.mark.parametrize("method,d,bits,dtype", CASES)
