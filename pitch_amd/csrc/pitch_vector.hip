@@ -1773,16 +1773,20 @@ void vec_encode_hs_batch(VecBatchArgs pb) {
 //   the 32 contiguous coordinates 32 q + e and runs the stages on bits 0 .. 4 in registers.
 // No butterfly crosses lanes (the team encoder at these sizes exchanges float64 values between lanes at 5 of
 // the 10 stages, two moves and an fma per coordinate and stage), and each lane packs its 32 codes into B whole
-// words. Half of each vector's rows pass through LDS at a time, so a wave needs 8.5 KB of LDS.
-template <int D>
+// words. The LDS exchange takes two passes, each for half of every vector's rows (COLS: half of every row's
+// columns, which keeps fewer registers live), so a wave needs 8.5 (9) KB of LDS. Measured at d = 256 .. 1024:
+// TurboQuant is 1-2 % faster with the row split at 2 waves per SIMD (its column split holds 140 VGPRs, 3 waves,
+// and gains nothing from them), PolarQuant 2-4 % faster with the column split at 3 waves.
+template <int D, bool COLS>
 struct Lt {
   static constexpr int T = D / 32;          // team lanes per vector
   static constexpr int V = 64 / T;          // vectors per wave iteration
   static constexpr int CW = 1024 / D;       // consecutive floats per staged chunk
   static constexpr int NJ = 32 / CW;        // chunks per staging lane (= T)
-  static constexpr int RS = 34;             // float64 per LDS row: 32 and 2 of padding, so rows are 16 bytes
-                                            // apart modulo 128 and 8 lanes reading 16 bytes each hit distinct banks
-  static constexpr int HR = T / 2;          // rows of a vector staged per pass
+  // float64 per LDS row of a pass: 32 (16 columns) and 2 of padding, so rows are 16 bytes apart modulo 128 and
+  // 8 lanes reading 16 bytes each hit distinct banks
+  static constexpr int RS = COLS ? 18 : 34;
+  static constexpr int HR = COLS ? T : T / 2;  // rows of a vector staged per pass
   static constexpr int ROWS = V * HR * RS;  // float64 of LDS per wave
   static constexpr int WAVES = kBlock / 64;
   static_assert(D >= 256 && D <= 1024 && NJ == T && HR >= 1, "geometry");
@@ -1792,7 +1796,7 @@ struct Lt {
 // CW (b % T) + r + 32 j, the one lane b (and lane b + 32) stages as element r of chunk j, has sign -1.
 template <int D>
 void fill_lt_flips(uint32_t seed, uint32_t* out) {
-  using L = Lt<D>;
+  using L = Lt<D, false>;
   static_assert(L::NJ * L::CW == 32, "one mask word per staged coordinate of a lane");
   thread_local uint32_t cached_seed = 0;
   thread_local bool have = false;
@@ -1814,7 +1818,7 @@ void fill_lt_flips(uint32_t seed, uint32_t* out) {
 // Loads of a wave's block of V vectors (vectors past the end re-read the last one).
 template <int D>
 __device__ __forceinline__ void lt_fetch(const float* in, uint64_t base, uint64_t count, int lane, uint32_t (&pf)[32]) {
-  using L = Lt<D>;
+  using L = Lt<D, false>;
   const uint64_t v = base + lane / L::T;
   const float* row = in + (v < count ? v : count - 1) * D + L::CW * (lane % L::T);
 #pragma unroll
@@ -1834,10 +1838,10 @@ __device__ __forceinline__ void lt_fetch(const float* in, uint64_t base, uint64_
 // Staging of one block (see Lt): signs, float64, the stages on coordinate bits 5 and above, then two passes
 // through the wave's LDS rows, each for half of every vector's rows, after which lane q of a vector holds its
 // coordinates 32 q .. 32 q + 31 in x.
-template <int D>
+template <int D, bool COLS>
 __device__ __forceinline__ void lt_stage(const uint32_t* neg, const uint32_t (&pf)[32], int lane, double* sx,
                                          double (&x)[32]) {
-  using L = Lt<D>;
+  using L = Lt<D, COLS>;
   constexpr int CW = L::CW, NJ = L::NJ, HR = L::HR;
   double y[NJ][CW];
 #pragma unroll
@@ -1860,6 +1864,41 @@ __device__ __forceinline__ void lt_stage(const uint32_t* neg, const uint32_t (&p
         }
   const int tl = lane % L::T;
   double* vrows = sx + (lane / L::T) * HR * L::RS;
+  if constexpr (COLS) {
+    // pass s: the lanes whose columns CW tl .. CW tl + CW - 1 lie in half s write all their rows, then every
+    // lane reads columns 16 s .. 16 s + 15 of its row
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if ((CW * tl) / 16 == s) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          double* dst = vrows + j * L::RS + CW * tl - 16 * s;
+          if constexpr (CW == 4) {
+            *(double2*)dst = double2{y[j][0], y[j][1]};
+            *(double2*)(dst + 2) = double2{y[j][2], y[j][3]};
+          } else if constexpr (CW == 2) {
+            *(double2*)dst = double2{y[j][0], y[j][1]};
+          } else {
+            *dst = y[j][0];
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const double* src = vrows + tl * L::RS;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const double2 v2 = *(const double2*)(src + 2 * k);
+        x[16 * s + 2 * k] = v2.x;
+        x[16 * s + 2 * k + 1] = v2.y;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    return;
+  }
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
 #pragma unroll
@@ -1898,7 +1937,7 @@ __device__ __forceinline__ void lt_stage(const uint32_t* neg, const uint32_t (&p
 template <int D, int B, bool POLAR>
 __device__ __forceinline__ void lt_compute(const EncSeg& sg, const typename TqLut8<D, B>::Smem& sq, uint64_t base,
                                            int lane, double (&x)[32]) {
-  using L = Lt<D>;
+  using L = Lt<D, false>;
   using Q = TqLut8<D, B>;
   constexpr int NW = D * B / 32;  // code words per vector; a lane's 32 codes are B of them
   const int tl = lane % L::T;
@@ -1928,13 +1967,14 @@ __device__ __forceinline__ void lt_compute(const EncSeg& sg, const typename TqLu
   store_words_nt(sg.codes_out + vst * NW + tl * B, w);
 }
 
-#ifndef PITCH_LT_WAVES
-#define PITCH_LT_WAVES 2  // waves per SIMD the LDS-transposed encoder's registers must allow
-#endif
+// waves per SIMD the LDS-transposed encoder's registers must allow (PolarQuant: a few spills in the float64
+// fallback only)
+template <bool POLAR>
+constexpr int lt_waves() { return POLAR ? 3 : 2; }
 
 template <int D, int B, bool POLAR>
 __device__ __forceinline__ void lt_run(const VecArgs& p, const EncSeg sg, uint64_t block, uint64_t nblocks) {
-  using L = Lt<D>;
+  using L = Lt<D, POLAR>;
   using Q = TqLut8<D, B>;
   __shared__ __attribute__((aligned(16))) double s_x[L::WAVES][L::ROWS];
   __shared__ __attribute__((aligned(16))) typename Q::Smem s_q;  // (unused by PolarQuant)
@@ -1952,25 +1992,25 @@ __device__ __forceinline__ void lt_run(const VecArgs& p, const EncSeg sg, uint64
   // Software pipeline as in the staged-stage encoder: an iteration issues the loads of block k + 1, computes and
   // stores block k, then stages block k + 1 (past the end: re-reads of the last vector, staged, never computed).
   lt_fetch<D>(in, base, sg.count, lane, pf);
-  lt_stage<D>(neg, pf, lane, sx, x);
+  lt_stage<D, POLAR>(neg, pf, lane, sx, x);
   while (base < sg.count) {
     lt_fetch<D>(in, base + stride, sg.count, lane, pf);
     __builtin_amdgcn_sched_barrier(0);
     lt_compute<D, B, POLAR>(sg, s_q, base, lane, x);
     __builtin_amdgcn_sched_barrier(0);
     base += stride;
-    lt_stage<D>(neg, pf, lane, sx, x);
+    lt_stage<D, POLAR>(neg, pf, lane, sx, x);
   }
 }
 
 template <int D, int B, bool POLAR>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_LT_WAVES)))
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(lt_waves<POLAR>())))
 void vec_encode_lt(VecArgs p) {
   lt_run<D, B, POLAR>(p, call_segment(p), blockIdx.x, gridDim.x);
 }
 
 template <int D, int B, bool POLAR>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(PITCH_LT_WAVES)))
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(lt_waves<POLAR>())))
 void vec_encode_lt_batch(VecBatchArgs pb) {
   const BatchSlot s = batch_slot(pb);
   lt_run<D, B, POLAR>(pb.common, s.seg, s.block, s.blocks);
@@ -2004,7 +2044,7 @@ template <int D, bool POLAR, int IO>
 constexpr uint32_t enc_vectors_per_block() {
   constexpr EncKind k = enc_kind<D, POLAR, IO, false>();
   if constexpr (k == EncKind::kStaged) return Hs<D, hs_team<D>()>::WAVES * Hs<D, hs_team<D>()>::V;
-  else if constexpr (k == EncKind::kTransposed) return Lt<D>::WAVES * Lt<D>::V;
+  else if constexpr (k == EncKind::kTransposed) return Lt<D, POLAR>::WAVES * Lt<D, POLAR>::V;
   else if constexpr (k == EncKind::kLanePerVector) return Lpv<D, IO>::V;
   else return Geom<D>::VPB;
 }
@@ -2043,7 +2083,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
   }
   if constexpr (kEnc == EncKind::kTransposed) {
     if (encode) {
-      using L = Lt<D>;
+      using L = Lt<D, POLAR>;
       fill_lt_flips<D>(a.seed, a.lane_flips);
       const uint64_t need = (a.count + L::WAVES * L::V - 1) / (L::WAVES * L::V);
       const void* k = (const void*)&vec_encode_lt<D, B, POLAR>;
