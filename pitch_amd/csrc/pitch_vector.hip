@@ -1815,6 +1815,13 @@ void fill_lt_flips(uint32_t seed, uint32_t* out) {
   for (int j = 0; j < 32; ++j) out[j] = cached[j];
 }
 
+// Non-temporal loads of the input and stores of the codes (each measured 1-2 % faster than the cached form).
+#ifndef PITCH_LT_NTL
+#define PITCH_LT_NTL 1
+#endif
+#ifndef PITCH_LT_NTS
+#define PITCH_LT_NTS 1
+#endif
 // Loads of a wave's block of V vectors (vectors past the end re-read the last one).
 template <int D>
 __device__ __forceinline__ void lt_fetch(const float* in, uint64_t base, uint64_t count, int lane, uint32_t (&pf)[32]) {
@@ -1824,13 +1831,13 @@ __device__ __forceinline__ void lt_fetch(const float* in, uint64_t base, uint64_
 #pragma unroll
   for (int j = 0; j < L::NJ; ++j) {
     if constexpr (L::CW == 4) {
-      const u32x4 c = __builtin_nontemporal_load((const u32x4*)(row + 32 * j));
+      const u32x4 c = PITCH_LT_NTL ? __builtin_nontemporal_load((const u32x4*)(row + 32 * j)) : *(const u32x4*)(row + 32 * j);
       pf[4 * j] = c.x, pf[4 * j + 1] = c.y, pf[4 * j + 2] = c.z, pf[4 * j + 3] = c.w;
     } else if constexpr (L::CW == 2) {
-      const u32x2 c = __builtin_nontemporal_load((const u32x2*)(row + 32 * j));
+      const u32x2 c = PITCH_LT_NTL ? __builtin_nontemporal_load((const u32x2*)(row + 32 * j)) : *(const u32x2*)(row + 32 * j);
       pf[2 * j] = c.x, pf[2 * j + 1] = c.y;
     } else {
-      pf[j] = __builtin_nontemporal_load((const uint32_t*)(row + 32 * j));
+      pf[j] = PITCH_LT_NTL ? __builtin_nontemporal_load((const uint32_t*)(row + 32 * j)) : *(const uint32_t*)(row + 32 * j);
     }
   }
 }
@@ -1964,7 +1971,8 @@ __device__ __forceinline__ void lt_compute(const EncSeg& sg, const typename TqLu
   const uint64_t v = base + lane / L::T;
   const uint64_t vst = v < sg.count ? v : sg.count - 1;
   sg.scales_out[vst] = nrm;
-  store_words_nt(sg.codes_out + vst * NW + tl * B, w);
+  if constexpr (PITCH_LT_NTS) store_words_nt(sg.codes_out + vst * NW + tl * B, w);
+  else store_words(sg.codes_out + vst * NW + tl * B, w);
 }
 
 // waves per SIMD the LDS-transposed encoder's registers must allow (PolarQuant: a few spills in the float64
