@@ -376,12 +376,27 @@ struct TqQuant {
 // largest such value below 2^(k+1). code = c_j + [t > E'_j] comes out of one compare and one add with carry
 // of the entry's low word; its bits above B are cleared by the packing. E'_j exceeds E_j by c_j ulps
 // (2^-31 bucket units at most), which moves the decision by less than 2^-36 in u, far inside the
-// near-boundary band. Small tables are replicated once per lane of a 16-lane LDS access phase (row = 16
-// copies, R = 128 bytes), so the random lookups of a wave never conflict on a bank; larger ones have one copy
-// (R = 8).
+// near-boundary band. Small tables are replicated once per lane of a 32-lane LDS access phase (row = 32
+// copies, R = 256 bytes), so the random lookups of a wave never conflict on a bank; larger ones have as many
+// copies as PITCH_LUT8_REP_MAX bytes hold (R = 8 bytes per copy).
+#ifndef PITCH_LUT8_REP
+#define PITCH_LUT8_REP 32  // copies of a replicated table: lane l reads copy l % REP, so the 32 lanes an LDS cycle
+                           // serves (64 banks of 4 bytes) never share a bank; 16 copies left 2-way conflicts
+                           // (measured 0-8 % slower)
+#endif
 #ifndef PITCH_LUT8_REP_MAX
 #define PITCH_LUT8_REP_MAX 20480  // largest replicated table in bytes
 #endif
+// Copies of a table of `bytes`. The staged-stage encoder (d = 64, 128) keeps 32 or 16 copies when they fit in
+// PITCH_LUT8_REP_MAX bytes and one otherwise: more copies of the larger tables cost it a wave per SIMD (measured 2-7 %
+// slower at d = 64, b = 6 and 8). The transposed encoder (d >= 256), whose LDS allows it, takes as many copies as
+// fit (b = 8 at d = 1024: 2, measured 2 % faster than one).
+constexpr int lut8_copies(int bytes, bool fill) {
+  if (!fill) return PITCH_LUT8_REP * bytes <= PITCH_LUT8_REP_MAX ? PITCH_LUT8_REP : (16 * bytes <= PITCH_LUT8_REP_MAX ? 16 : 1);
+  int r = 1;
+  while (r < PITCH_LUT8_REP && 2 * r * bytes <= PITCH_LUT8_REP_MAX) r *= 2;
+  return r;
+}
 // (a & m) | b in one v_and_or_b32 (the compiler otherwise splits it into an and and an add).
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
   uint32_t r;
@@ -395,7 +410,7 @@ struct TqLut8 {
   static constexpr PitchLutInfo LI = pitch_lut_info(ilog2(D), B);
   static constexpr bool kLut = LI.offset >= 0;
   static constexpr int N = kLut ? LI.entries : 1;
-  static constexpr int REP = (kLut && N * 128 <= PITCH_LUT8_REP_MAX) ? 16 : 1;
+  static constexpr int REP = kLut ? lut8_copies(N * 8, D >= 256) : 1;
   static constexpr int R = 8 * REP;                     // bytes per row
   static constexpr int K = 20 - ilog2(R);               // t in [2^K, 2^(K+1))
   static constexpr double kMagic = double(1 << K) + double(1 << (K - 1)) + LI.off;
