@@ -376,23 +376,26 @@ struct TqQuant {
 // largest such value below 2^(k+1). code = c_j + [t > E'_j] comes out of one compare and one add with carry
 // of the entry's low word; its bits above B are cleared by the packing. E'_j exceeds E_j by c_j ulps
 // (2^-31 bucket units at most), which moves the decision by less than 2^-36 in u, far inside the
-// near-boundary band. Small tables are replicated once per lane of a 32-lane LDS access phase (row = 32
-// copies, R = 256 bytes), so the random lookups of a wave never conflict on a bank; larger ones have as many
-// copies as PITCH_LUT8_REP_MAX bytes hold (R = 8 bytes per copy).
+// near-boundary band. Tables are replicated (lut8_copies; R = 8 bytes per copy) so that the random lookups of a
+// wave conflict on fewer LDS banks.
 #ifndef PITCH_LUT8_REP
-#define PITCH_LUT8_REP 32  // copies of a replicated table: lane l reads copy l % REP, so the 32 lanes an LDS cycle
-                           // serves (64 banks of 4 bytes) never share a bank; 16 copies left 2-way conflicts
-                           // (measured 0-8 % slower)
+#define PITCH_LUT8_REP 32  // most copies of a replicated table: lane l reads copy l % REP, so with 32 the 32 lanes an
+                           // LDS cycle serves (64 banks of 4 bytes) never share a bank
+#endif
+#ifndef PITCH_LUT8_STAGED_REP
+#define PITCH_LUT8_STAGED_REP 16  // copies of the staged-stage encoder's tables (where they fit)
 #endif
 #ifndef PITCH_LUT8_REP_MAX
 #define PITCH_LUT8_REP_MAX 20480  // largest replicated table in bytes
 #endif
-// Copies of a table of `bytes`. The staged-stage encoder (d = 64, 128) keeps 32 or 16 copies when they fit in
-// PITCH_LUT8_REP_MAX bytes and one otherwise: more copies of the larger tables cost it a wave per SIMD (measured 2-7 %
-// slower at d = 64, b = 6 and 8). The transposed encoder (d >= 256), whose LDS allows it, takes as many copies as
-// fit (b = 8 at d = 1024: 2, measured 2 % faster than one).
+// Copies of a table of `bytes`. The staged-stage encoder (d = 64, 128) keeps 16 copies when they fit in
+// PITCH_LUT8_REP_MAX bytes and one otherwise: its staging rows leave LDS conflicts that 32 copies do not remove,
+// building 32 copies per workgroup cost more than the lookups gained at config-2 and config-4 sizes (medians of
+// five runs: -1 to +2.6 %), and more copies of the larger tables cost it a wave per SIMD (2-7 % slower at d = 64,
+// b = 6 and 8). The transposed encoder (d >= 256), whose LDS allows it, takes as many copies as fit, up to 32
+// (bank conflicts 0.39 -> 0.00 of its LDS cycles at d = 1024, b = 3 and 4).
 constexpr int lut8_copies(int bytes, bool fill) {
-  if (!fill) return PITCH_LUT8_REP * bytes <= PITCH_LUT8_REP_MAX ? PITCH_LUT8_REP : (16 * bytes <= PITCH_LUT8_REP_MAX ? 16 : 1);
+  if (!fill) return PITCH_LUT8_STAGED_REP * bytes <= PITCH_LUT8_REP_MAX ? PITCH_LUT8_STAGED_REP : 1;
   int r = 1;
   while (r < PITCH_LUT8_REP && 2 * r * bytes <= PITCH_LUT8_REP_MAX) r *= 2;
   return r;
