@@ -1065,21 +1065,46 @@ void fill_lane_flips(uint32_t seed, uint32_t* out) {
   for (int t = 0; t < 32; ++t) out[t] = cached[t];
 }
 
+// Rotation-sign masks of the streaming decoder (16 coordinates per lane): fill_lane_flips for teams of up to 32
+// lanes; for a team of 64, lane t's 16 bits are bits 16 (t & 1) .. of word t / 2.
+template <int D>
+void fill_stream_flips(uint32_t seed, uint32_t* out) {
+  using G = Geom<D, 16>;
+  if constexpr (G::T <= 32) {
+    fill_lane_flips<D, 16>(seed, out);
+  } else {
+    static_assert(G::T == 64 && G::E == 16, "two lanes per mask word");
+    thread_local uint32_t cached_seed = 0;
+    thread_local bool have = false;
+    thread_local uint32_t cached[32];
+    if (!have || cached_seed != seed) {
+      for (int j = 0; j < 32; ++j) cached[j] = 0u;
+      for (int t = 0; t < 64; ++t)
+        for (int e = 0; e < 16; ++e)
+          if (sign_is_negative(seed, (uint32_t)G::coord(t, e))) cached[t >> 1] |= 1u << (16 * (t & 1) + e);
+      cached_seed = seed;
+      have = true;
+    }
+    for (int j = 0; j < 32; ++j) out[j] = cached[j];
+  }
+}
+
 // ----------------------------------------------------------------------------------------------------
-// Streaming decoder for long float32 calls at D = 128. At a footprint of many GB the persistent decoder above runs
-// at ~5.0 TB/s, while a write stream with the same 10 % of reads reaches ~6 TB/s when the GPU holds 8 workgroups per
-// CU, each wave writes ~8 KB, and each launch gives every workgroup one block (so launches of ~2048 workgroups follow
-// each other; within one long launch the workgroups drift apart and reads and writes interleave at the memory).
-// This kernel is shaped for that: a team of 8 lanes per vector (16 coordinates per lane), two passes of 8 vectors per
-// wave, no output staging (a store instruction writes, for each of 8 vectors, the 128-byte line its team holds), at
-// most 64 VGPRs and a few KB of LDS; the host issues the call as launches of one block per workgroup.
+// Streaming decoder for long float32 calls at D = 128 and 1024. At a footprint of many GB the persistent decoder
+// above runs at ~5.0 TB/s, while a write stream with the same 10 % of reads reaches ~6 TB/s when the GPU holds 8
+// workgroups per CU, each wave writes ~8 KB, and each launch gives every workgroup one block (so launches of ~2048
+// workgroups follow each other; within one long launch the workgroups drift apart and reads and writes interleave at
+// the memory). This kernel is shaped for that: 16 coordinates per lane (a team of 8 lanes per vector at D = 128, the
+// whole wave at D = 1024), two passes per wave (16 or 2 vectors), no output staging (a store instruction writes, for
+// each vector of a pass, the contiguous bytes its team holds: 128 bytes at D = 128, 1 KB at D = 1024), at most 64
+// VGPRs and a few KB of LDS; the host issues the call as launches of one block per workgroup.
 #ifndef PITCH_STREAM_PASSES
 #define PITCH_STREAM_PASSES 2  // vectors per wave of the streaming decoder = passes x 8
 #endif
 #ifndef PITCH_STREAM_NT
 #define PITCH_STREAM_NT 1  // the streaming decoder writes with non-temporal stores
 #endif
-constexpr int kStreamE = 16;     // coordinates per lane at D = 128: teams of 8 lanes
+constexpr int kStreamE = 16;     // coordinates per lane: teams of 8 lanes at D = 128, 64 at D = 1024
 constexpr int kStreamPasses = PITCH_STREAM_PASSES;
 constexpr int kStreamWaves = 8;  // waves per SIMD the kernel is built for (64 VGPRs)
 
@@ -1087,7 +1112,7 @@ template <int D, int B, bool POLAR>
 __global__ __launch_bounds__(kBlock, kStreamWaves) void vec_decode_stream(VecArgs p) {
   using G = Geom<D, kStreamE>;
   using TB = DecTab<B, POLAR, G::W>;
-  static_assert(G::T == 8 && G::W == 4, "full 128-byte lines per team and chunk index");
+  static_assert((G::T == 8 || G::T == 64) && G::W == 4, "full 128-byte lines per team and chunk index");
   constexpr int NW = (D * B + 31) / 32;
   constexpr int CB = G::W * B;            // bits of codes per chunk (<= 32)
   constexpr int P = kStreamPasses;
@@ -1105,7 +1130,9 @@ __global__ __launch_bounds__(kBlock, kStreamWaves) void vec_decode_stream(VecArg
   // table source values and the sign word first, then the coalesced code and scale loads; waiting for the former
   // leaves the latter in flight (loads complete in order)
   const auto tab_src = load_dec_table<D, B, POLAR>();
-  const uint32_t fbits = p.lane_flips[t];
+  // the lane's 16 sign bits: one word per lane for teams of up to 32 lanes, two lanes per word for 64
+  // (fill_stream_flips)
+  const uint32_t fbits = G::T <= 32 ? p.lane_flips[t] : (p.lane_flips[t >> 1] >> (16 * (t & 1))) & 0xFFFFu;
   __builtin_amdgcn_sched_barrier(0);
   uint32_t w[NPL];
   {
@@ -2135,8 +2162,9 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
     const uint64_t grid = persistent_grid(k, need);
     hipLaunchKernelGGL((vec_encode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else {
-    if constexpr (D == 128 && IO == 0 && !KBIAS) {
-      if (a.count >= stream_decode_min_vectors()) {
+    if constexpr ((D == 128 || D == 1024) && IO == 0 && !KBIAS) {
+      // the same output footprint at both sizes (2^22 vectors of d = 128, 2 GB, by default)
+      if (a.count >= stream_decode_min_vectors() * 128 / D) {
         using GS = Geom<D, kStreamE>;
         constexpr uint64_t kVpb = (uint64_t)GS::V * kStreamPasses * (kBlock / 64);  // vectors per workgroup
         const void* ks = (const void*)&vec_decode_stream<D, B, POLAR>;
@@ -2144,7 +2172,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
         // one block per resident workgroup per launch (1.5x, 2x, 3x and 4x as many measured 3-6 % slower)
         const uint64_t grid = persistent_grid(ks, blocks);
         VecArgs b = a;
-        fill_lane_flips<D, kStreamE>(a.seed, b.lane_flips);
+        fill_stream_flips<D>(a.seed, b.lane_flips);
         for (uint64_t b0 = 0; b0 < blocks; b0 += grid) {
           const uint64_t nb = blocks - b0 < grid ? blocks - b0 : grid, v0 = b0 * kVpb;
           b.count = a.count - v0 < nb * kVpb ? a.count - v0 : nb * kVpb;

@@ -1,8 +1,9 @@
-"""GPU parity of the streaming decoder that long float32 calls at d = 128 use (at least 2^22 vectors per call).
+"""GPU parity of the streaming decoder that long float32 calls at d = 128 and 1024 use (at least 2^22 vectors of
+d = 128 per call, or 2^19 of d = 1024: the same 2 GB of output).
 
-Codes are random bytes (at d = 128 every bit width packs into whole words, so any byte pattern is a valid code
-stream) with random positive scales. One call of 2^22 + 4099 vectors (a ragged last launch) per method and bit
-width is checked:
+Codes are random bytes (at d = 128 and 1024 every bit width packs into whole words, so any byte pattern is a valid
+code stream) with random positive scales. One call of the threshold + 4099 vectors (a ragged last launch) per
+dimension, method and bit width is checked:
 * sampled rows against the oracle's decode of the same codes: relative L2 <= 1e-5 (pitch_reference.py:104-107,
   123-129);
 * the first and last 65536 vectors against the persistent decoder (separate calls below the streaming size, through
@@ -17,17 +18,15 @@ from test_gpu_parity import max_rel_diff, REL_L2_BAR
 
 pytestmark = pytest.mark.gpu
 
-N = (1 << 22) + 4099
-D = 128
-
-
+@pytest.mark.parametrize("D", [128, 1024])
 @pytest.mark.parametrize("method", ["turboQuant", "polarQuant"])
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 7, 8])
-def test_stream_decode(q, method, bits):
+def test_stream_decode(q, D, method, bits):
     import torch
     import pitch_amd as P
     dev = q.device
-    print(f"streaming decode {method} b={bits} n={N}", flush=True)
+    N = ((1 << 22) * 128 // D) + 4099
+    print(f"streaming decode d={D} {method} b={bits} n={N}", flush=True)
     cfg = P.QuantConfig(method, D, bits, 0x1234 + bits)
     g = torch.Generator(device=dev).manual_seed(900 + bits + (method == "polarQuant"))
     codes = torch.randint(0, 256, (N * cfg.codeStride,), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
