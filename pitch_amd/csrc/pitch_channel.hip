@@ -218,16 +218,21 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
 #endif
 constexpr int kSlab = 64;        // channels per wave of the decoder (long calls)
 #ifndef PITCH_KIVI_DEC_SLAB32
-#define PITCH_KIVI_DEC_SLAB32 1  // 1: 32-channel decoder slabs for float32 calls of at most 32768 (group, 64-channel) items
+#define PITCH_KIVI_DEC_SLAB32 1  // 1: 32-channel decoder slabs for float32 calls of at most PITCH_KIVI_DEC_SLAB32_MAX
+#endif                           // (group, 64-channel) items
+#ifndef PITCH_KIVI_DEC_SLAB32_MAX
+#define PITCH_KIVI_DEC_SLAB32_MAX 32768
 #endif
 constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
 // Calls of the wave encoder and decoder longer than this many rounds (grid-stride iterations per workgroup) are
 // issued as several launches of this many rounds. At a 17 GB footprint (config 5 keys: 33.5M tokens, d = 128) a
 // single persistent launch reaches 4.4 TB/s encoding and 4.9 TB/s decoding; launches of 2 rounds reach 5.3 and
-// 5.35 TB/s (1 round: 5.0 and 5.4). A launch boundary brings every workgroup back in step; in one long launch they
-// drift apart, and the reads of some interleave with the writes of others at the memory (a probe kernel with the
-// decoder's read/write mix showed the same gain from short launches). Calls of up to this many rounds keep one launch.
-constexpr uint64_t kChanSliceRounds = 2;
+// 5.35 TB/s, of 1 round 5.0 and 5.4 (the same box, one run: encode 5.0 / 5.4, decode 5.42 / 5.36 TB/s for 1 / 2
+// rounds). A launch boundary brings every workgroup back in step; in one long launch they drift apart, and the
+// reads of some interleave with the writes of others at the memory (a probe kernel with the decoder's read/write mix
+// showed the same gain from short launches). Calls of up to this many rounds keep one launch.
+constexpr uint64_t kChanSliceRoundsEnc = 2;
+constexpr uint64_t kChanSliceRoundsDec = 1;
 #ifndef PITCH_KIVI_NT
 #define PITCH_KIVI_NT 1  // the wave encoder reads keys with non-temporal loads
 #endif
@@ -673,7 +678,7 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       // float32 keys: balanced rounds (config 3 is 1.33 rounds at full occupancy); the 16-bit encoders are
       // bound by their arithmetic and keep every resident wave
       const uint64_t grid = persistent_grid(k, (items + 3) / 4, kBlock, PITCH_KIVI_BALANCE && IO == 0);
-      const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRounds);
+      const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRoundsEnc);
       if (rounds && (items + 3) / 4 > grid * rounds && grid * rounds * 4 >= slabs) {
         const uint64_t gpl = grid * rounds * 4 / slabs;  // groups per launch
         constexpr uint64_t ES = IO == 0 ? 4 : 2;
@@ -718,7 +723,7 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       constexpr int SW = decltype(sw_c)::value;
       const uint64_t items = groups * ((a.dim + SW - 1) / SW);
       const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, SW, IO>, (items + 3) / 4);
-      const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRounds);
+      const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRoundsDec);
       if (rounds && (items + 3) / 4 > grid * rounds && grid * rounds * 4 >= slabs) {
         const uint64_t gpl = grid * rounds * 4 / slabs;  // groups per launch
         constexpr uint64_t ES = IO == 0 ? 4 : 2;
@@ -736,7 +741,7 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       }
       hipLaunchKernelGGL((chan_decode_w<B, SW, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
     };
-    if (PITCH_KIVI_DEC_SLAB32 && IO == 0 && items64 <= 32768) go(std::integral_constant<int, 32>{});
+    if (PITCH_KIVI_DEC_SLAB32 && IO == 0 && items64 <= PITCH_KIVI_DEC_SLAB32_MAX) go(std::integral_constant<int, 32>{});
     else go(std::integral_constant<int, kSlab>{});
   } else if (vec4) {
     const uint32_t P = kBlock / (a.dim >> 2);
