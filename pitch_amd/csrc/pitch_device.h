@@ -187,9 +187,10 @@ __device__ __forceinline__ void fwht(F (&v)[Geom<D>::E], int t) {
               PITCH_FMAC_DPP(12, PERM) PITCH_FMAC_DPP(13, PERM) PITCH_FMAC_DPP(14, PERM)                      \
                   PITCH_FMAC_DPP(15, PERM) "s_nop 1\n"
 
+// LM = 8 pairs lane i with i ^ 8 through row_ror:8 (a rotation by half a row).
 template <int LM, int O, int E>
 __device__ __forceinline__ void fmac_dpp16(float (&v)[E], float sg) {
-  static_assert((LM == 1 || LM == 2) && O + 16 <= E, "quad permutes over 16 elements");
+  static_assert((LM == 1 || LM == 2 || LM == 8) && O + 16 <= E, "DPP partners over 16 elements");
 #define PITCH_FMAC_DPP_OPS                                                                                  \
   : "+v"(v[O]), "+v"(v[O + 1]), "+v"(v[O + 2]), "+v"(v[O + 3]), "+v"(v[O + 4]), "+v"(v[O + 5]),             \
     "+v"(v[O + 6]), "+v"(v[O + 7]), "+v"(v[O + 8]), "+v"(v[O + 9]), "+v"(v[O + 10]), "+v"(v[O + 11]),       \
@@ -197,21 +198,45 @@ __device__ __forceinline__ void fmac_dpp16(float (&v)[E], float sg) {
   : "v"(sg)
   if constexpr (LM == 1)
     asm(PITCH_FMAC_DPP16("quad_perm:[1,0,3,2]") PITCH_FMAC_DPP_OPS);
-  else
+  else if constexpr (LM == 2)
     asm(PITCH_FMAC_DPP16("quad_perm:[2,3,0,1]") PITCH_FMAC_DPP_OPS);
+  else
+    asm(PITCH_FMAC_DPP16("row_ror:8") PITCH_FMAC_DPP_OPS);
 #undef PITCH_FMAC_DPP_OPS
 }
 
+// The butterfly at lane distance 4 in two DPP operations per element, without a separate move: lanes 0-3 of each
+// 8 (DPP banks 0 and 2) add the partner read through row_shl:4, lanes 4-7 (banks 1 and 3) take partner - own
+// through row_shr:4 (each operation writes only its banks; both read the inputs, so neither sees the other's
+// result). Low lanes get a + b, high lanes a - b, with the signs of the plain butterfly. Eight elements per block,
+// with the DPP read hazard covered as in fmac_dpp16.
+#define PITCH_BFLY4(O, I)                                                                                       \
+  "v_add_f32_dpp %" #O ", %" #I ", %" #I " row_shl:4 row_mask:0xf bank_mask:0x5\n"                               \
+  "v_sub_f32_dpp %" #O ", %" #I ", %" #I " row_shr:4 row_mask:0xf bank_mask:0xa\n"
+template <int O, int E>
+__device__ __forceinline__ void bfly4_dpp8(float (&v)[E]) {
+  static_assert(O + 8 <= E, "eight elements");
+  float r[8];
+  asm("s_nop 1\n" PITCH_BFLY4(0, 8) PITCH_BFLY4(1, 9) PITCH_BFLY4(2, 10) PITCH_BFLY4(3, 11) PITCH_BFLY4(4, 12)
+          PITCH_BFLY4(5, 13) PITCH_BFLY4(6, 14) PITCH_BFLY4(7, 15) "s_nop 1"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(v[O]), "v"(v[O + 1]), "v"(v[O + 2]), "v"(v[O + 3]), "v"(v[O + 4]), "v"(v[O + 5]), "v"(v[O + 6]),
+        "v"(v[O + 7]));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[O + i] = r[i];
+}
+#undef PITCH_BFLY4
+
 // Lanes of the team whose cross-lane stages fwht_f32_lane_signed runs as v_fmac_f32_dpp (distances 1 and 2,
-// when E is a multiple of 16).
-template <int D, int EE = default_lane_coords(D)>
+// when E is a multiple of 16; with WIDE also 8). These come out negated on the high lane of each pair.
+template <int D, int EE = default_lane_coords(D), bool WIDE = false>
 __host__ __device__ constexpr int dpp_lane_bits() {
-  return (PITCH_DPP_FMAC && Geom<D, EE>::E % 16 == 0) ? (3 & (Geom<D, EE>::T - 1)) : 0;
+  return (PITCH_DPP_FMAC && Geom<D, EE>::E % 16 == 0) ? ((WIDE ? 11 : 3) & (Geom<D, EE>::T - 1)) : 0;
 }
 // Sign bit that lane t's results of fwht_f32_lane_signed carry: (-1)^popcount(t & dpp_lane_bits).
-template <int D, int EE = default_lane_coords(D)>
+template <int D, int EE = default_lane_coords(D), bool WIDE = false>
 __device__ __forceinline__ uint32_t dpp_lane_sign_bit(int t) {
-  return (uint32_t)(__builtin_popcount((unsigned)(t & dpp_lane_bits<D, EE>())) & 1) << 31;
+  return (uint32_t)(__builtin_popcount((unsigned)(t & dpp_lane_bits<D, EE, WIDE>())) & 1) << 31;
 }
 
 // fwht<D, float> with the cross-lane stages at distances 1 and 2 done by fmac_dpp16. The high lane of each
@@ -220,7 +245,9 @@ __device__ __forceinline__ uint32_t dpp_lane_sign_bit(int t) {
 // equal the transform times (-1)^popcount(t & dpp_lane_bits<D>()), bit for bit up to that sign (b - a
 // and -(a - b) round alike; only a zero may come out with the other sign). The first PRE stages (bits
 // below PRE <= log2 W, inside a chunk) are taken as already applied by the caller.
-template <int D, int PRE = 0, int EE = default_lane_coords(D)>
+// With WIDE, the stage at lane distance 8 is a v_fmac_f32_dpp too (row_ror:8), and the one at distance 4 is
+// bfly4_dpp8 (two DPP operations per element, signs as the plain butterfly's).
+template <int D, int PRE = 0, int EE = default_lane_coords(D), bool WIDE = false>
 __device__ __forceinline__ void fwht_f32_lane_signed(float (&v)[EE], int t) {
   using G = Geom<D, EE>;
   static_assert(PRE >= 0 && PRE <= G::LGW, "pre-applied stages lie inside a chunk");
@@ -229,8 +256,10 @@ __device__ __forceinline__ void fwht_f32_lane_signed(float (&v)[EE], int t) {
     if constexpr (bit >= G::LGW && bit < G::LGW + G::LGT) {
       constexpr int lm = 1 << (bit - G::LGW);
       const float sg = (t & lm) ? -1.0f : 1.0f;
-      if constexpr ((dpp_lane_bits<D, EE>() & lm) != 0) {
+      if constexpr ((dpp_lane_bits<D, EE, WIDE>() & lm) != 0) {
         static_for<0, G::E / 16>([&](auto o_c) { fmac_dpp16<lm, 16 * decltype(o_c)::value>(v, sg); });
+      } else if constexpr (WIDE && lm == 4 && PITCH_DPP_FMAC && G::E % 8 == 0) {
+        static_for<0, G::E / 8>([&](auto o_c) { bfly4_dpp8<8 * decltype(o_c)::value>(v); });
       } else {
 #pragma unroll
         for (int e = 0; e < G::E; ++e) v[e] = fma_t(v[e], sg, xchg<lm>(v[e]));

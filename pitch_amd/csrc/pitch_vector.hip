@@ -1157,7 +1157,10 @@ __global__ __launch_bounds__(kBlock, kStreamWaves) void vec_decode_stream(VecArg
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const uint32_t lane_sign = dpp_lane_sign_bit<D, kStreamE>(t);
+  // the butterflies at lane distances 4 and 8 as DPP operations (fwht_f32_lane_signed's WIDE) at D = 1024, where
+  // they measured 2-6 % faster; at D = 128 the same form for distance 4 measured 8 % slower than a DPP move pair
+  constexpr bool kWide = D >= 256;
+  const uint32_t lane_sign = dpp_lane_sign_bit<D, kStreamE, kWide>(t);
   const uint64_t lastv = p.count - 1 - wb;
 #pragma unroll
   for (int j = 0; j < P; ++j) {
@@ -1172,7 +1175,7 @@ __global__ __launch_bounds__(kBlock, kStreamWaves) void vec_decode_stream(VecArg
       decode_chunk<D, B, POLAR>(__builtin_amdgcn_alignbit(row[wh], row[wl], (uint32_t)(pos & 31)), s_tab,
                                 y + k * G::W);
     }
-    fwht_f32_lane_signed<D, TB::PRE, kStreamE>(y, t);
+    fwht_f32_lane_signed<D, TB::PRE, kStreamE, kWide>(y, t);
     const float f = s_scale[wave][lv] * DimConst<D>::kInvSqrtF;
     const uint64_t v = wb + (uint64_t)lv;
 #pragma unroll
