@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from oracle import pitch_oracle as O
-from test_gpu_parity import check_codes, check_scales, max_rel_diff, mean_rel_err, REL_L2_BAR
+from test_gpu_parity import band_mask, check_codes, check_scales, max_rel_diff, mean_rel_err, REL_L2_BAR
 
 pytestmark = pytest.mark.gpu
 METHODS = ["turboQuant", "polarQuant"]
@@ -316,6 +316,33 @@ def test_every_dimension_against_oracle(q, method, d, bits):
     recon = O.DECODERS[method](codes, s32.astype(np.float64), bits, 0x00C0FFEE)
     dec = q.decode(P.CompressedBatch(cfg, O.pack_codes(codes, bits), s32))
     assert max_rel_diff(dec, recon, d) < REL_L2_BAR
+
+
+@pytest.mark.parametrize("method", METHODS)
+@pytest.mark.parametrize("d", [128, 256, 1024])
+@pytest.mark.parametrize("bits", [3, 6])
+def test_extreme_vectors_against_oracle(q, method, d, bits):
+    """Zero vectors, vectors at the largest allowed magnitude, tiny vectors (PolarQuant's rmax far below 1e-30 in
+    the unnormalised transform), a single huge coordinate among small ones and ordinary vectors, in one call: codes
+    equal the oracle's except at near-boundary coordinates, scales within one ulp, decodes finite. A constant
+    vector rotates onto a few distinct values, so a dozen or more of its coordinates can sit within the band of one
+    edge at once: no cap on the count of in-band differences here, unlike the random inputs of check_codes."""
+    import pitch_amd as P
+    rng = np.random.default_rng(d + bits)
+    rows = [np.zeros(d), np.full(d, 1e17), rng.standard_normal(d) * 1e-33, rng.standard_normal(d) * 1e-17,
+            np.where(np.arange(d) == 5, 1e16, rng.standard_normal(d) * 1e-3), -np.full(d, 1e17)]
+    rows += list(rng.standard_normal((10, d)) * np.exp(rng.uniform(-3, 3, (10, 1))))
+    X = np.asarray(rows, np.float32)
+    n = len(X)
+    cfg = P.QuantConfig(method, d, bits, 0x5EED)
+    ours = q.encode(X.reshape(-1), config=cfg)
+    codes, scales = O.ENCODERS[method](X.astype(np.float64), bits, 0x5EED)
+    diff = O.unpack_codes(ours.codes, n, d, bits) != O.unpack_codes(O.pack_codes(codes, bits), n, d, bits)
+    band = band_mask(method, X, None, bits, 0x5EED)
+    assert not (diff & ~band).any(), f"{method} d{d} b{bits}: codes differ away from any boundary"
+    assert not diff[2:5].any() and not diff[6:].any(), "a non-constant vector differs in the band"
+    check_scales(ours.scales, np.asarray(scales, np.float32), "scales")
+    assert np.all(np.isfinite(q.decode(ours)))
 
 
 # ----------------------------------------------------------------------------- per-channel
