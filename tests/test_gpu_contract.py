@@ -325,8 +325,9 @@ def test_extreme_vectors_against_oracle(q, method, d, bits):
     """Zero vectors, vectors at the largest allowed magnitude, tiny vectors (PolarQuant's rmax far below 1e-30 in
     the unnormalised transform), a single huge coordinate among small ones and ordinary vectors, in one call: codes
     equal the oracle's except at near-boundary coordinates, scales within one ulp, decodes finite. A constant
-    vector rotates onto a few distinct values, so a dozen or more of its coordinates can sit within the band of one
-    edge at once: no cap on the count of in-band differences here, unlike the random inputs of check_codes."""
+    vector rotates onto a few distinct values, many of them zeros on TurboQuant's middle edge, exact here and
+    float64 noise of either sign in the specification's divide-first order (pitch_reference.py:96-101): a dozen or
+    more in-band differences at once, so no cap on their count here, unlike the random inputs of check_codes."""
     import pitch_amd as P
     rng = np.random.default_rng(d + bits)
     rows = [np.zeros(d), np.full(d, 1e17), rng.standard_normal(d) * 1e-33, rng.standard_normal(d) * 1e-17,
