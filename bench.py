@@ -182,6 +182,61 @@ def time_copy_fill(torch, timer, src, dst, steps: int = 10) -> dict:
             "fill_gbps": round(nb / ms_fill / 1e6, 1), "fill_ms": round(ms_fill, 4)}
 
 
+class StreamCeiling:
+    """An encoder's bytes with no arithmetic: libpitch_calib.so's pitch_calib_stream reads unit_bytes and writes
+    out_words 4-byte words per unit (vector or key row), with its loads in a chosen access shape (the contiguous
+    piece of a unit that one load instruction reads, the grid, cached or non-temporal). Timed like the codec on
+    the same buffers, it gives the rate any kernel moving those bytes in that shape reaches on this box: the
+    shape the encoder uses, and the best of a small sweep of shapes."""
+
+    def __init__(self, torch):
+        import ctypes
+        self.torch = torch
+        lib = ctypes.CDLL(str(ROOT / "pitch_amd" / "libpitch_calib.so"))
+        fn = lib.pitch_calib_stream
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                       ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+        self.fn = fn
+        self.cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+
+    def _call(self, src, dst, units: int, unit_bytes: int, out_words: int, seg: int, wgs: int, nt: int) -> None:
+        if dst.numel() * dst.element_size() < units * out_words * 4 or src.numel() * src.element_size() < units * unit_bytes:
+            raise ValueError("calibration buffers are smaller than the stream")
+        rc = self.fn(src.data_ptr(), dst.data_ptr(), units, unit_bytes, out_words, seg, wgs, nt,
+                     self.torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError("pitch_calib_stream rejected its arguments")
+
+    def measure(self, timer, pairs, units: int, unit_bytes: int, out_words: int, enc_seg: int, enc_gbps: float,
+                steps: int, warm: int) -> dict:
+        """pairs: (input, output) buffer sets rotated like the encoder's timing. enc_seg: the encoder's load
+        piece; the encoder's grid is 3 workgroups per CU, persistent, non-temporal."""
+        nbytes = units * (unit_bytes + 4 * out_words)
+        rates = {}
+        for seg in (64, 128, 256, 512):
+            if unit_bytes % seg or unit_bytes // seg > 8:
+                continue
+            for wgs in (3 * self.cus, 0):
+                for nt in (1, 0):
+                    ms = timer.time(lambda i: self._call(pairs[i % len(pairs)][0], pairs[i % len(pairs)][1], units,
+                                                         unit_bytes, out_words, seg, wgs, nt), steps, warm)
+                    rates[(seg, wgs, nt)] = nbytes / ms / 1e6
+        enc_shape = rates[(enc_seg, 3 * self.cus, 1)]
+        best = max(rates, key=rates.get)
+        return {"bytes_per_call": nbytes,
+                "encoder_shape": {"load_piece_bytes": enc_seg, "grid": "persistent, 3 workgroups per CU",
+                                  "nontemporal": True, "gbps": round(enc_shape, 1)},
+                "best": {"load_piece_bytes": best[0],
+                         "grid": "persistent, 3 workgroups per CU" if best[1] else "one block per workgroup",
+                         "nontemporal": bool(best[2]), "gbps": round(rates[best], 1),
+                         "pct_peak": round(rates[best] / PEAK_GBPS * 100, 1)},
+                "encoder_frac_of_encoder_shape": round(enc_gbps / enc_shape, 3),
+                "encoder_frac_of_best": round(enc_gbps / rates[best], 3),
+                "all_gbps": {f"piece{k[0]}_{'persistent' if k[1] else 'oneblock'}_{'nt' if k[2] else 'cached'}":
+                             round(v, 1) for k, v in sorted(rates.items())}}
+
+
 def cpu_time(fn, seconds: float) -> tuple[float, int]:
     """Median seconds of fn() over runs for at least `seconds` (3 warm-ups first, at least 5 runs)."""
     for _ in range(3):
@@ -235,6 +290,9 @@ def run_config5_values(torch, q, P, O, W, timer, dev, args) -> tuple[dict, dict]
     out = torch.empty((n, d), dtype=torch.float32, device=dev)
     print("# config 5 V: copy / fill calibration at the same footprint", file=sys.stderr, flush=True)
     calib = time_copy_fill(torch, timer, x, out)
+    print("# config 5 V: encoder-shaped stream calibration at the same footprint", file=sys.stderr, flush=True)
+    enc_ceiling = StreamCeiling(torch).measure(timer, [(x, out)], n, 4 * d, (cfg.codeStride + 4) // 4, 128,
+                                               n * per_vector_bytes(d, b) / ms_enc / 1e6, 3, 1)
     del x
     torch.cuda.empty_cache()
     print("# config 5 V: timing full-cache decode", file=sys.stderr, flush=True)
@@ -277,7 +335,8 @@ def run_config5_values(torch, q, P, O, W, timer, dev, args) -> tuple[dict, dict]
         head["cpu_baseline"] = cpu
     extra = {"cfg5_V_tq_d128_b3_encode_one_call": {"ms": round(ms_enc, 4),
                                                    "gbps": round(nbytes / ms_enc / 1e6, 1),
-                                                   "pct_peak": round(nbytes / ms_enc / 1e6 / PEAK_GBPS * 100, 1)}}
+                                                   "pct_peak": round(nbytes / ms_enc / 1e6 / PEAK_GBPS * 100, 1),
+                                                   "stream_ceiling": enc_ceiling}}
     # per-token append: 8 vectors per layer at codesOffset = (t * 8) * codeStride within each layer's slice
     per_layer = H * T
     xa = torch.randn(L, H, d, device=dev)
@@ -498,6 +557,11 @@ def run_extras(torch, q, P, O, W, timer, dev, args) -> dict:
                                     "encode_pct_peak": round(nb / ms_enc / 1e6 / PEAK_GBPS * 100, 1),
                                     "decode_pct_peak": round(nb / ms_dec / 1e6 / PEAK_GBPS * 100, 1),
                                     "parity_code_diffs_near_boundary": diffs, "parity_decode_max_rel_l2": rel}
+        if b == 4:
+            pairs = [(bf[0], torch.empty(n * 9, dtype=torch.int32, device=dev)) for bf in bufs]
+            out[f"cfg2_tq_d64_b{b}"]["encode_stream_ceiling"] = StreamCeiling(torch).measure(
+                timer, pairs, n, 4 * d, (cfg.codeStride + 4) // 4, 64, nb / ms_enc / 1e6, steps, warm)
+            del pairs
         if b == 4 and not args.no_cpu:
             out[f"cfg2_tq_d64_b{b}"]["cpu_baseline"] = cpu_baseline_vector_decode(
                 O, bufs[0][1][:65536 * cfg.codeStride].cpu().numpy().tobytes(), bufs[0][2][:65536].cpu().numpy(),
@@ -550,6 +614,12 @@ def run_extras(torch, q, P, O, W, timer, dev, args) -> dict:
                                    "encode_pct_peak": round(kb / ms_ke / 1e6 / PEAK_GBPS * 100, 1),
                                    "decode_pct_peak": round(kb / ms_kd / 1e6 / PEAK_GBPS * 100, 1),
                                    "bit_exact_all_heads": True}
+    # the KIVI encoder reads 128-byte row pieces (32 channels of one token) and writes codes plus fp16 ranges:
+    # 256 + 32 + 4 bytes per token at d = 64, b = 4, G = 64
+    pairs = [(kb_[0], torch.empty(8 * nt * 9, dtype=torch.int32, device=dev)) for kb_ in kbufs]
+    out["cfg3_kivi_d64_b4_G64"]["encode_stream_ceiling"] = StreamCeiling(torch).measure(
+        timer, pairs, 8 * nt, 256, 9, 128, kb / ms_ke / 1e6, steps, warm)
+    del pairs
     if not args.no_cpu:
         k0 = keys[0].cpu().numpy()
         t_e, _ = cpu_time(lambda: O.channel_encode(k0, 4, 64), 4.0)
@@ -565,6 +635,8 @@ def run_extras(torch, q, P, O, W, timer, dev, args) -> dict:
     n4 = 28 * 2 * 16384
     keys4 = torch.cat([W.qwen_keys(torch, gen, dev, 2, 16384, 128, first_head=2 * layer).reshape(-1, 128)
                        for layer in range(28)])
+    o4 = torch.empty(n4 * 17, dtype=torch.int32, device=dev)
+    ceiling4 = None
     for method in ("turboQuant", "polarQuant"):
         cfg4 = P.QuantConfig(method, 128, 4)
         c = torch.empty(n4 * cfg4.codeStride, dtype=torch.uint8, device=dev)
@@ -586,6 +658,16 @@ def run_extras(torch, q, P, O, W, timer, dev, args) -> dict:
                                          "decode_pct_peak": round(nb / ms_d / 1e6 / PEAK_GBPS * 100, 1),
                                          "vectors_per_s_decode": round(n4 / ms_d * 1e3, 1),
                                          "parity_code_diffs_near_boundary": diffs, "parity_decode_max_rel_l2": rel}
+        if ceiling4 is None:  # the same bytes for both methods (codeStride 64 at b = 4)
+            ceiling4 = StreamCeiling(torch).measure(timer, [(keys4, o4)], n4, 512, (cfg4.codeStride + 4) // 4, 128,
+                                                    nb / ms_e / 1e6, steps, warm)
+            out[f"cfg4_{method}_d128_b4"]["encode_stream_ceiling"] = ceiling4
+        else:
+            enc = nb / ms_e / 1e6
+            out[f"cfg4_{method}_d128_b4"]["encode_stream_ceiling"] = {
+                "same_as": "cfg4_turboQuant_d128_b4",
+                "encoder_frac_of_encoder_shape": round(enc / ceiling4["encoder_shape"]["gbps"], 3),
+                "encoder_frac_of_best": round(enc / ceiling4["best"]["gbps"], 3)}
         if not args.no_cpu:
             X64 = X4[:4096].astype(np.float64)
             t_e, _ = cpu_time(lambda: O.ENCODERS[method](X64, 4), 3.0)
@@ -596,6 +678,7 @@ def run_extras(torch, q, P, O, W, timer, dev, args) -> dict:
                 "decode_gbps": round(4096 * per_vector_bytes(128, 4) / t_d / 1e9, 4), "cores": 1, "kind": "port",
                 "sample": "oracle encode / decode of 4096 sampled config-4 vectors, 1 thread, extrapolated per vector"}
         del c, s_, o
+    del o4
     x2 = W.gpt2_values(torch, gen, dev)
     out.update(run_io16(torch, q, P, W, timer, gen, dev, args, x2, keys4))
     del x2, keys4

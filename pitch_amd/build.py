@@ -6,6 +6,8 @@ Steps: generate csrc/pitch_tables.inc from data/codebooks.json, compile csrc/pit
 dimension and element type of the uncompressed vectors (-DPITCH_DIM=2..1024, -DPITCH_IO=0/1/2 for
 float32/float16/bfloat16), csrc/pitch_channel.hip once per element type, csrc/pitch_attention.hip once per
 attention dimension (64, 128) and csrc/pitch_abi.cpp, and link the shared library next to this file. Object files go to <repo>/_build/.
+Also builds libpitch_calib.so from csrc/pitch_calib.hip: the measurement kernels bench.py times beside the
+codec (not part of the codec's C ABI).
 """
 from __future__ import annotations
 
@@ -21,6 +23,7 @@ CSRC = PKG / "csrc"
 REPO = PKG.parent
 BUILD = REPO / "_build"
 LIB = PKG / "libpitch_amd.so"
+CALIB_LIB = PKG / "libpitch_calib.so"
 DIMS = [2 ** k for k in range(1, 11)]
 IO_TYPES = [0, 1, 2]   # element type of uncompressed vectors: float32, float16, bfloat16
 ATTENTION_DIMS = [64, 128]
@@ -81,6 +84,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, LIB)
+    tmp = CALIB_LIB.with_suffix(".so.tmp")
+    _run([hipcc, *HIPCC_FLAGS, "-shared", str(CSRC / "pitch_calib.hip"), "-o", str(tmp)])
+    os.replace(tmp, CALIB_LIB)
     return LIB
 
 

@@ -1414,11 +1414,15 @@ constexpr int hs_team() { return D == 64 ? PITCH_HS_T64 : 4; }
 #define PITCH_HS_NT 1  // the staged-stage encoder streams its input in and its codes and scales out non-temporally
 #endif
 
+#ifndef PITCH_HS_NTL
+#define PITCH_HS_NTL PITCH_HS_NT  // the staged-stage encoder's loads alone
+#endif
+
 // One 16-byte load of the staged-stage encoder's input. Non-temporal: an encode reads each input byte once,
 // and keeping the stream out of the caches lets the few writes interleave with it better (measured: +5 % at
 // the same instruction count).
 __device__ __forceinline__ u32x4 hs_load(const float* p) {
-  if constexpr (PITCH_HS_NT) return __builtin_nontemporal_load((const u32x4*)p);
+  if constexpr (PITCH_HS_NTL) return __builtin_nontemporal_load((const u32x4*)p);
   else return *(const u32x4*)p;
 }
 
