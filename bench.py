@@ -286,7 +286,7 @@ def run_config5_values(torch, q, P, O, W, timer, dev, args) -> tuple[dict, dict]
     C = codes.view(n, cfg.codeStride)[it].cpu().numpy().tobytes()
     S = scales[it].cpu().numpy()
     diffs = check_vector_encode(O, "turboQuant", X, C, S, d, b, "config 5 V encode")
-    ms_enc = timer.time(lambda i: q.enqueueEncode(x, codes, scales, n, cfg), 3, 1)
+    ms_enc = timer.time(lambda i: q.enqueueEncode(x, codes, scales, n, cfg), 10, 2)
     out = torch.empty((n, d), dtype=torch.float32, device=dev)
     print("# config 5 V: copy / fill calibration at the same footprint", file=sys.stderr, flush=True)
     calib = time_copy_fill(torch, timer, x, out)

@@ -506,6 +506,19 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
   return cus * kmin;
 }
 
+uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size) {
+  // PITCH_ENC_BLOCKS_PER_WG overrides the blocks per workgroup of long calls (tuning aid); 0 keeps every call
+  // persistent.
+  static const long per_wg = [] {
+    const char* e = std::getenv("PITCH_ENC_BLOCKS_PER_WG");
+    return e ? std::atol(e) : 10L;
+  }();
+  const uint64_t cap = persistent_grid(kernel, blocks_needed, block_size);
+  if (per_wg <= 0 || blocks_needed < 32 * cap) return cap;
+  const uint64_t g = blocks_needed / (uint64_t)per_wg;
+  return g > 0x7FFFFFFFull ? 0x7FFFFFFFull : (g < cap ? cap : g);
+}
+
 }  // namespace pitch
 
 extern "C" {

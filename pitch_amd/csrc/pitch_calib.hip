@@ -11,6 +11,7 @@
 // - workgroups: the grid. Non-zero: a persistent grid of that many 256-thread workgroups striding over the
 //   units (the encoders run 3 workgroups per CU); zero: one block of units per workgroup, all in one launch.
 // - nontemporal: non-temporal loads and stores (the encoders use them), or cached ones.
+// The stores are coalesced: a wave's units write one contiguous run of words, as the encoders' codes do.
 // Every lane's loaded words feed a value that is compared before the stores, so the compiler keeps every load.
 #include <hip/hip_runtime.h>
 
@@ -42,10 +43,14 @@ __global__ __launch_bounds__(kBlock) void calib_stream(const u32x4* __restrict__
 #pragma unroll
     for (int i = 0; i < CPL; ++i) acc ^= c[i].x ^ c[i].y ^ c[i].z ^ c[i].w;
     if (acc == kNever) out[0] = acc;
-    uint32_t* dst = out + u * (uint64_t)out_words;
-    for (uint32_t j = pl; j < out_words; j += L) {
-      if constexpr (NT) __builtin_nontemporal_store(acc + j, dst + j);
-      else dst[j] = acc + j;
+    // the wave's UPW units own one contiguous run of UPW * out_words words (as an encoder's codes): lane l
+    // writes words l, l + 64, ... of it, up to the last unit's end
+    const uint64_t w0 = wb * UPW * (uint64_t)out_words;
+    const uint64_t wend = units * (uint64_t)out_words;
+    const uint64_t run = (uint64_t)UPW * out_words;
+    for (uint64_t j = lane; j < run && w0 + j < wend; j += 64) {
+      if constexpr (NT) __builtin_nontemporal_store(acc + (uint32_t)j, out + w0 + j);
+      else out[w0 + j] = acc + (uint32_t)j;
     }
   }
 }
