@@ -513,8 +513,13 @@ uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size)
     const char* e = std::getenv("PITCH_ENC_BLOCKS_PER_WG");
     return e ? std::atol(e) : 10L;
   }();
+  // PITCH_ENC_MIN_ROUNDS: the resident rounds from which a call is oversubscribed (tuning aid)
+  static const long min_rounds = [] {
+    const char* e = std::getenv("PITCH_ENC_MIN_ROUNDS");
+    return e ? std::atol(e) : 32L;
+  }();
   const uint64_t cap = persistent_grid(kernel, blocks_needed, block_size);
-  if (per_wg <= 0 || blocks_needed < 32 * cap) return cap;
+  if (per_wg <= 0 || blocks_needed < (uint64_t)(min_rounds > 1 ? min_rounds : 1) * cap) return cap;
   const uint64_t g = blocks_needed / (uint64_t)per_wg;
   return g > 0x7FFFFFFFull ? 0x7FFFFFFFull : (g < cap ? cap : g);
 }
