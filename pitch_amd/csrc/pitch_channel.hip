@@ -216,7 +216,10 @@ __global__ __launch_bounds__(kBlock) void chan_encode4(ChanArgs p) {
 #ifndef PITCH_KIVI_WAVES
 #define PITCH_KIVI_WAVES 3  // waves per SIMD the per-channel encoder's register budget allows
 #endif
-constexpr int kSlab = 64;        // channels per wave of the decoder (long calls)
+#ifndef PITCH_KIVI_DEC_SLAB
+#define PITCH_KIVI_DEC_SLAB 64
+#endif
+constexpr int kSlab = PITCH_KIVI_DEC_SLAB;  // channels per wave of the decoder (long calls)
 #ifndef PITCH_KIVI_DEC_SLAB32
 #define PITCH_KIVI_DEC_SLAB32 1  // 1: 32-channel decoder slabs for float32 calls of at most PITCH_KIVI_DEC_SLAB32_MAX
 #endif                           // (group, 64-channel) items
