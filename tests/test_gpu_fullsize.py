@@ -115,6 +115,16 @@ def test_config5_v_share(q):
     per_vector_full(q, "turboQuant", 32 * 131072, 128, 3, 5000, "t5")
 
 
+@pytest.mark.parametrize("method,d,bits", [("polarQuant", 128, 4), ("turboQuant", 64, 4), ("polarQuant", 64, 3),
+                                           ("turboQuant", 64, 3)])
+def test_long_calls_oversubscribed_grid(q, method, d, bits):
+    """The staged encoder runs calls of at least 32 resident rounds as one launch of about 10 blocks per workgroup
+    (encode_grid): 2^21 vectors are 32,768 blocks of 64, past 32 rounds of 768 resident workgroups on a 256-CU
+    device. Sampled rows match the oracle, and the slice per_vector_full encodes through byte offsets (100,003
+    vectors, a persistent grid) gives the same bytes as the long call."""
+    per_vector_full(q, method, 1 << 21, d, bits, 7000 + d + bits, "t5")
+
+
 def test_more_than_2_32_floats_in_one_call(q):
     """count * dim > 2^32 (a documented extension: the reference caps a call below 2^32 elements)."""
     per_vector_full(q, "turboQuant", (1 << 22) + 100, 1024, 4, 6000, "gauss")
