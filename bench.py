@@ -198,6 +198,11 @@ class StreamCeiling:
         fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
                        ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
         self.fn = fn
+        st = lib.pitch_calib_stream_store
+        st.restype = ctypes.c_int
+        st.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                       ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+        self.store_fn = st
         self.cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
 
     def _call(self, src, dst, units: int, unit_bytes: int, out_words: int, seg: int, wgs: int, nt: int) -> None:
@@ -207,6 +212,43 @@ class StreamCeiling:
                      self.torch.cuda.current_stream().cuda_stream)
         if rc != 0:
             raise RuntimeError("pitch_calib_stream rejected its arguments")
+
+    def measure_decoder(self, timer, src, dst, units: int, unit_bytes: int, in_words: int, dec_seg: int,
+                        dec_gbps: float, steps: int, warm: int) -> dict:
+        """The decoders' mirror image (pitch_calib_stream_store): in_words words read (coalesced) and unit_bytes
+        written per unit, in store pieces of 64-512 bytes, as one persistent launch, one launch of one block per
+        workgroup, or launches of one round of 8 workgroups per CU (the config-5 decoders' shape); non-temporal or
+        cached stores. dec_seg: the decoder's store piece."""
+        if (dst.numel() * dst.element_size() < units * unit_bytes or src.numel() * src.element_size() < units * in_words * 4):
+            raise ValueError("calibration buffers are smaller than the stream")
+        nbytes = units * (unit_bytes + 4 * in_words)
+        wgs = 8 * self.cus
+        names = {0: "persistent", 1: "oneblock", 2: "rounds"}
+        rates = {}
+        stream = self.torch.cuda.current_stream().cuda_stream
+
+        def call(seg, mode, nt):
+            if self.store_fn(src.data_ptr(), dst.data_ptr(), units, unit_bytes, in_words, seg, mode, wgs, nt, stream):
+                raise RuntimeError("pitch_calib_stream_store rejected its arguments")
+
+        for seg in (64, 128, 256, 512):
+            if unit_bytes % seg or unit_bytes // seg > 8:
+                continue
+            for mode in (0, 1, 2):
+                for nt in (1, 0):
+                    ms = timer.time(lambda i: call(seg, mode, nt), steps, warm)
+                    rates[(seg, mode, nt)] = nbytes / ms / 1e6
+        shape = rates[(dec_seg, 2, 1)]
+        best = max(rates, key=rates.get)
+        return {"bytes_per_call": nbytes,
+                "decoder_shape": {"store_piece_bytes": dec_seg, "grid": "launches of one round, 8 workgroups per CU",
+                                  "nontemporal": True, "gbps": round(shape, 1)},
+                "best": {"store_piece_bytes": best[0], "grid": names[best[1]], "nontemporal": bool(best[2]),
+                         "gbps": round(rates[best], 1), "pct_peak": round(rates[best] / PEAK_GBPS * 100, 1)},
+                "decoder_frac_of_decoder_shape": round(dec_gbps / shape, 3),
+                "decoder_frac_of_best": round(dec_gbps / rates[best], 3),
+                "all_gbps": {f"piece{k[0]}_{names[k[1]]}_{'nt' if k[2] else 'cached'}": round(v, 1)
+                             for k, v in sorted(rates.items())}}
 
     def measure(self, timer, pairs, units: int, unit_bytes: int, out_words: int, enc_seg: int, enc_gbps: float,
                 steps: int, warm: int) -> dict:
@@ -300,6 +342,11 @@ def run_config5_values(torch, q, P, O, W, timer, dev, args) -> tuple[dict, dict]
     rel = check_vector_decode(O, "turboQuant", C, S, out[it].cpu().numpy(), d, b, "config 5 V decode")
     nbytes = n * per_vector_bytes(d, b)
     gbps = nbytes / (ms * 1e-3) / 1e9
+    print("# config 5 V: decoder-shaped stream calibration at the same footprint", file=sys.stderr, flush=True)
+    src = torch.empty(n * ((cfg.codeStride + 4) // 4), dtype=torch.int32, device=dev)
+    dec_ceiling = StreamCeiling(torch).measure_decoder(timer, src, out, n, 4 * d, (cfg.codeStride + 4) // 4, 512,
+                                                       gbps, 3, 1)
+    del src
     cpu = None if args.no_cpu else cpu_baseline_vector_decode(
         O, codes[:65536 * cfg.codeStride].cpu().numpy().tobytes(), scales[:65536].cpu().numpy(), d, b,
         "config 5 value cache (first 2^16 vectors)")
@@ -330,6 +377,7 @@ def run_config5_values(torch, q, P, O, W, timer, dev, args) -> tuple[dict, dict]
         "parity": {"sampled_rows": int(len(idx)), "encode_code_diffs_near_boundary": diffs,
                    "decode_max_rel_l2": rel},
         "same_footprint_streaming": calib,
+        "decode_stream_ceiling": dec_ceiling,
     }
     if cpu:
         head["cpu_baseline"] = cpu
@@ -409,6 +457,13 @@ def run_config5_keys(torch, q, P, O, W, timer, dev, args) -> dict:
            "decode_pct_peak": round(kb / ms / 1e6 / PEAK_GBPS * 100, 1), "encode_ms": round(ms_enc, 4),
            "encode_gbps": round(kb / ms_enc / 1e6, 1), "encode_pct_peak": round(kb / ms_enc / 1e6 / PEAK_GBPS * 100, 1),
            "parity_groups_bit_exact": len(picks)}
+    # the decoder writes 256-byte row pieces (64 channels of a token) and reads codes plus fp16 ranges:
+    # 512 + 64 + 8 bytes per token at d = 128, b = 4, G = 64
+    print("# config 5 K: decoder-shaped stream calibration at the same footprint", file=sys.stderr, flush=True)
+    src = torch.empty(n * 18, dtype=torch.int32, device=dev)
+    res["decode_stream_ceiling"] = StreamCeiling(torch).measure_decoder(timer, src, out, n, 4 * d, 18, 256,
+                                                                        kb / ms / 1e6, 3, 1)
+    del src
     if not args.no_cpu:
         g0 = 65536 // G
         c0 = codes[:65536 * cfg.codeStride].cpu().numpy().tobytes()
