@@ -504,3 +504,32 @@ def test_attention_key_bias_validation(lib):
     assert "positions" not in _lib.last_error()
     assert call(first=11) == _lib.ERR_INVALID_INPUT and "positions" in _lib.last_error()
     assert call(tb=T * d * 4 - 4) == _lib.ERR_INVALID_INPUT
+
+
+def test_calibration_library_exports_and_rejects_bad_arguments(built_library):
+    """libpitch_calib.so (bench.py's same-traffic streams) is built beside the codec and exports its two entry
+    points; arguments out of range return -1 before any HIP call (null pointers, a unit that is not a whole number
+    of pieces, an unknown piece size or launch mode)."""
+    from pitch_amd.build import CALIB_LIB
+    if not CALIB_LIB.exists():
+        from pitch_amd.build import build
+        build()
+    calib = ctypes.CDLL(str(CALIB_LIB))
+    st, ss = calib.pitch_calib_stream, calib.pitch_calib_stream_store
+    st.restype = ss.restype = ctypes.c_int
+    st.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                   ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+    ss.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                   ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    assert st(None, p, 4, 512, 13, 128, 768, 1, None) == -1
+    assert st(p, None, 4, 512, 13, 128, 768, 1, None) == -1
+    assert st(p, p, 0, 512, 13, 128, 768, 1, None) == -1      # no units
+    assert st(p, p, 4, 500, 13, 128, 768, 1, None) == -1      # not whole pieces
+    assert st(p, p, 4, 96, 13, 96, 768, 1, None) == -1        # unknown piece size
+    assert st(p + 4, p, 4, 512, 13, 128, 768, 1, None) == -1  # input not 16-byte aligned
+    assert ss(None, p, 4, 512, 13, 128, 2, 2048, 1, None) == -1
+    assert ss(p, p, 4, 512, 13, 128, 3, 2048, 1, None) == -1  # unknown launch mode
+    assert ss(p, p + 4, 4, 512, 13, 128, 2, 2048, 1, None) == -1  # output not 16-byte aligned
+    assert ss(p, p, 4, 512, 13, 32, 2, 2048, 1, None) == -1   # unknown piece size
