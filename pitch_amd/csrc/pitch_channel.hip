@@ -236,6 +236,9 @@ constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
 // showed the same gain from short launches). Calls of up to this many rounds keep one launch.
 constexpr uint64_t kChanSliceRoundsEnc = 2;
 constexpr uint64_t kChanSliceRoundsDec = 1;
+#ifndef PITCH_KIVI_ENC_ONE_LAUNCH
+#define PITCH_KIVI_ENC_ONE_LAUNCH 1  // float32 encode calls of 32+ resident rounds: one launch, one item per wave
+#endif
 #ifndef PITCH_KIVI_NT
 #define PITCH_KIVI_NT 1  // the wave encoder reads keys with non-temporal loads
 #endif
@@ -681,6 +684,14 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       // float32 keys: balanced rounds (config 3 is 1.33 rounds at full occupancy); the 16-bit encoders are
       // bound by their arithmetic and keep every resident wave
       const uint64_t grid = persistent_grid(k, (items + 3) / 4, kBlock, PITCH_KIVI_BALANCE && IO == 0);
+      const uint64_t need = (items + 3) / 4;
+      if (PITCH_KIVI_ENC_ONE_LAUNCH && IO == 0 && need >= 32 * grid) {
+        // float32 calls of 32+ resident rounds: one launch of one item per wave, far more workgroups than the CUs
+        // hold (config-5 keys, 341 rounds: 5.52 TB/s against 5.41 for launches of two rounds, three repeats each)
+        const uint64_t g = need < 0x7FFFFFFFull ? need : 0x7FFFFFFFull;
+        hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)g), dim3(kBlock), 0, s, a);
+        return;
+      }
       const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRoundsEnc);
       if (rounds && (items + 3) / 4 > grid * rounds && grid * rounds * 4 >= slabs) {
         const uint64_t gpl = grid * rounds * 4 / slabs;  // groups per launch
