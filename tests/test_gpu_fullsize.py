@@ -181,6 +181,36 @@ def test_config5_k_share(q):
     channel_full(q, 32, 131072, 128, 4, 64, 5001)
 
 
+def test_kivi_long_call_one_launch_matches_per_head_calls(q):
+    """Float32 KIVI encodes of at least 32 resident rounds run one launch of one item per wave: 32 heads x 131,072
+    tokens at d = 128 are 131,072 (group, 64-channel slab) items, 32,768 workgroups, past 32 rounds of 768 on a
+    256-CU device. The long call's codes and ranges equal, byte for byte, those of one call per head (131,072 tokens
+    each, a persistent grid), and sampled groups of a long call match the oracle (channel_full, one_call)."""
+    import torch
+    import pitch_amd as P
+    from pitch_amd import workloads as W
+    heads, tokens, d, bits, G = 32, 131072, 128, 4, 64
+    dev = q.device
+    cfg = P.ChannelQuantConfig(d, bits, G)
+    groups = cfg.groupCount(tokens)
+    gk = torch.Generator(device=dev).manual_seed(5201)
+    x = W.biased_keys(torch, gk, dev, heads, tokens, d).reshape(heads * tokens, d).contiguous()
+    c1 = torch.empty(heads * tokens * cfg.codeStride, dtype=torch.uint8, device=dev)
+    r1 = torch.empty(heads * groups * cfg.rangeStride // 2, dtype=torch.float16, device=dev)
+    c2 = torch.zeros_like(c1)
+    r2 = torch.zeros_like(r1)
+    q.enqueuePerChannelEncode(x, c1, r1, heads * tokens, cfg)
+    for h in range(heads):
+        q.enqueuePerChannelEncode(x, c2, r2, tokens, cfg, inputOffset=h * tokens * d * 4,
+                                  codesOffset=h * tokens * cfg.codeStride, rangesOffset=h * groups * cfg.rangeStride)
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2)
+    assert torch.equal(r1.view(torch.int16), r2.view(torch.int16))
+    del x, c1, r1, c2, r2
+    torch.cuda.empty_cache()
+    channel_full(q, heads, tokens, d, bits, G, 5202, one_call=True)
+
+
 @pytest.mark.parametrize("bits", [2, 3, 8])
 def test_kivi_64_channel_slabs_bit_widths(q, bits):
     """One call of 2^21 + 192 tokens at d = 64: 32,771 (group, 64-channel) items, so the encoder takes its
