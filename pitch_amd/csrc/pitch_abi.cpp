@@ -511,7 +511,7 @@ uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size)
   // persistent.
   static const long per_wg = [] {
     const char* e = std::getenv("PITCH_ENC_BLOCKS_PER_WG");
-    return e ? std::atol(e) : 10L;
+    return e ? std::atol(e) : 8L;
   }();
   // PITCH_ENC_MIN_ROUNDS: the resident rounds from which a call is oversubscribed (tuning aid)
   static const long min_rounds = [] {
