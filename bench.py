@@ -17,9 +17,14 @@ footprint: a plain device copy and a plain fill (the second denominator: the box
 config-5 key cache (KIVI b = 4, G = 64, one call of 33.5M tokens), per-token append latencies, and the oracle's
 CPU decode on a 2^16-vector subset (1 thread), extrapolated per vector.
 
---extras adds BASELINE configs 1-4 (bulk encode and decode, appends, KIVI, d = 128 TurboQuant / PolarQuant),
-single-call latency percentiles, float16/bfloat16 caches, decode-step attention over compressed caches, key-bias
-removal and CPU baselines of configs 1, 3 and 4; --full adds the d = 1024 TurboQuant sweep of config 5.
+After config 5, every other row of the north-star target (bulk encode and full-cache decode of every method at
+d = 64 and 128), each with its parity gate: config 2 (TurboQuant b = 2, 3, 4 and PolarQuant b = 4 at d = 64, and the
+per-step append), config 3 (KIVI d = 64) and config 4 (TurboQuant and PolarQuant at d = 128); `north_star_target`
+lists each row's % of peak beside the 70 % target (--no-rows skips them).
+
+--extras adds BASELINE config 1, the encoder-shaped stream ceilings and CPU baselines of configs 2-4, single-call
+latency percentiles, float16/bfloat16 caches, decode-step attention over compressed caches and key-bias removal;
+--full adds the d = 1024 TurboQuant sweep of config 5.
 """
 from __future__ import annotations
 
@@ -344,7 +349,8 @@ def run_config5_values(torch, q, P, O, W, timer, dev, args) -> tuple[dict, dict]
     gbps = nbytes / (ms * 1e-3) / 1e9
     print("# config 5 V: decoder-shaped stream calibration at the same footprint", file=sys.stderr, flush=True)
     src = torch.empty(n * ((cfg.codeStride + 4) // 4), dtype=torch.int32, device=dev)
-    dec_ceiling = StreamCeiling(torch).measure_decoder(timer, src, out, n, 4 * d, (cfg.codeStride + 4) // 4, 512,
+    # the streaming decoder's store instructions write 128 bytes of each vector (a team of 8 lanes x 16 bytes)
+    dec_ceiling = StreamCeiling(torch).measure_decoder(timer, src, out, n, 4 * d, (cfg.codeStride + 4) // 4, 128,
                                                        gbps, 3, 1)
     del src
     cpu = None if args.no_cpu else cpu_baseline_vector_decode(
@@ -495,6 +501,7 @@ def main() -> int:
     ap.add_argument("--full", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-keys", action="store_true", help="skip the config-5 key cache")
+    ap.add_argument("--no-rows", action="store_true", help="skip configs 2-4 (the target's d = 64 / 128 rows)")
     ap.add_argument("--copy-calib", action="store_true", help="also run a plain 1 GiB device copy (PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -519,6 +526,10 @@ def main() -> int:
     result, extra = run_config5_values(torch, q, P, O, W, timer, dev, args)
     if not args.no_keys:
         extra["cfg5_K_kivi_d128_b4_G64_one_call"] = run_config5_keys(torch, q, P, O, W, timer, dev, args)
+    if not args.no_rows:
+        rows = run_target_rows(torch, q, P, O, W, timer, dev, args)
+        extra.update(rows)
+        result["north_star_target"] = target_summary(rows, result, extra)
     if args.extras or args.full:
         extra.update(run_extras(torch, q, P, O, W, timer, dev, args))
     if args.full:
@@ -535,9 +546,213 @@ def main() -> int:
     return 0
 
 
+# ------------------------------------------------------------------------------- the target's rows (default run)
+def pct(nbytes: int, ms: float) -> float:
+    return round(nbytes / ms / 1e6 / PEAK_GBPS * 100, 1)
+
+
+def codec_row(nbytes: int, n: int, ms_enc: float, ms_dec: float, **parity) -> dict:
+    """encode / decode GB/s, % of the 8 TB/s peak, ms and vectors per second of one bulk call each."""
+    return {"encode_gbps": round(nbytes / ms_enc / 1e6, 1), "decode_gbps": round(nbytes / ms_dec / 1e6, 1),
+            "encode_pct_peak": pct(nbytes, ms_enc), "decode_pct_peak": pct(nbytes, ms_dec),
+            "encode_ms": round(ms_enc, 5), "decode_ms": round(ms_dec, 5),
+            "vectors_per_s_encode": round(n / ms_enc * 1e3, 1), "vectors_per_s_decode": round(n / ms_dec * 1e3, 1),
+            **parity}
+
+
+def run_target_rows(torch, q, P, O, W, timer, dev, args) -> dict:
+    """Every (method, d in {64, 128}, bulk encode / full-cache decode) pair of the north-star target, each in one
+    call over a whole cache with its parity gate (BenchmarkSuite.swift:100-141 times the same pairs):
+    * config 2 (GPT-2 value cache, 393,216 d = 64 vectors): TurboQuant b = 2, 3, 4 and PolarQuant b = 4, over
+      `--sets` rotated buffer sets so that no call finds its inputs in the 256 MB Infinity Cache; the per-step
+      append of 12 vectors;
+    * config 3 (KIVI d = 64, b = 4, G = 64, 8 heads x 32768 tokens in one call), bit-exact on every head;
+    * config 4 (Qwen2.5-1.5B keys, 917,504 d = 128 vectors): TurboQuant and PolarQuant b = 4 on the same tensor.
+    With --extras, the encoder-shaped stream ceilings and the CPU baselines of these rows too."""
+    import numpy as np
+    out = {}
+    steps, warm = max(20, args.steps), 5
+    gen = torch.Generator(device=dev).manual_seed(2)
+    # ---- config 2: GPT-2 value cache, bulk encode and full-cache decode over rotated buffer sets
+    d, n = 64, 32768 * 12
+    print("# config 2: TurboQuant b = 2, 3, 4 and PolarQuant b = 4 at d = 64", file=sys.stderr, flush=True)
+    sets = [W.gpt2_values(torch, gen, dev) for _ in range(args.sets)]
+    x = sets[0]
+    for method, b in (("turboQuant", 2), ("turboQuant", 3), ("turboQuant", 4), ("polarQuant", 4)):
+        cfg = P.QuantConfig(method, d, b)
+        bufs = []
+        for xs in sets:
+            c = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=dev)
+            nm = torch.empty(n, dtype=torch.float32, device=dev)
+            q.enqueueEncode(xs, c, nm, n, cfg)
+            bufs.append((xs, c, nm, torch.empty((n, d), dtype=torch.float32, device=dev)))
+        ms_enc = timer.time(lambda i: q.enqueueEncode(bufs[i % len(bufs)][0], bufs[i % len(bufs)][1],
+                                                      bufs[i % len(bufs)][2], n, cfg), steps, warm)
+        ms_dec = timer.time(lambda i: q.enqueueDecode(bufs[i % len(bufs)][1], bufs[i % len(bufs)][2],
+                                                      bufs[i % len(bufs)][3], n, cfg), steps, warm)
+        idx = sample_rows(n, b, 2048)
+        it = torch.from_numpy(idx).to(dev)
+        C = bufs[0][1].view(n, cfg.codeStride)[it].cpu().numpy().tobytes()
+        S = bufs[0][2][it].cpu().numpy()
+        label = f"config 2 {method} b={b}"
+        diffs = check_vector_encode(O, method, x.view(n, d)[it].cpu().numpy(), C, S, d, b, label)
+        rel = check_vector_decode(O, method, C, S, bufs[0][3][it].cpu().numpy(), d, b, label)
+        nb = n * per_vector_bytes(d, b)
+        key = f"cfg2_{'tq' if method == 'turboQuant' else 'polar'}_d64_b{b}"
+        out[key] = codec_row(nb, n, ms_enc, ms_dec, parity_code_diffs_near_boundary=diffs,
+                             parity_decode_max_rel_l2=rel)
+        if args.extras and method == "turboQuant" and b == 4:
+            pairs = [(bf[0], torch.empty(n * 9, dtype=torch.int32, device=dev)) for bf in bufs]
+            out[key]["encode_stream_ceiling"] = StreamCeiling(torch).measure(
+                timer, pairs, n, 4 * d, (cfg.codeStride + 4) // 4, 64, nb / ms_enc / 1e6, steps, warm)
+            del pairs
+            if not args.no_cpu:
+                out[key]["cpu_baseline"] = cpu_baseline_vector_decode(
+                    O, bufs[0][1][:65536 * cfg.codeStride].cpu().numpy().tobytes(), bufs[0][2][:65536].cpu().numpy(),
+                    d, b, "config 2 value cache (first 2^16 vectors)", 6.0)
+        del bufs
+    del sets
+    # append-encode latency: 12 vectors per step at codesOffset = t*12*cs
+    cfg = P.QuantConfig("turboQuant", d, 3)
+    codes = torch.empty(32768 * 12 * cfg.codeStride, dtype=torch.uint8, device=dev)
+    norms = torch.empty(32768 * 12, dtype=torch.float32, device=dev)
+
+    def app(i):
+        t = i % 32768
+        q.enqueueEncode(x, codes, norms, 12, cfg, inputOffset=t * 12 * d * 4, codesOffset=t * 12 * cfg.codeStride,
+                        scalesOffset=t * 12 * 4)
+
+    ms_app = timer.time(app, 500, 50)
+    out["cfg2_append_encode_12vec"] = {"gpu_us_per_call_backtoback": round(ms_app * 1e3, 2),
+                                       "single_call": timer.single_calls(app)}
+    del x, codes, norms
+    # ---- config 3: KIVI keys, Llama-3.2-1B shape (8 heads x 32768 tokens x 64), G=64, b=4
+    print("# config 3: KIVI d = 64", file=sys.stderr, flush=True)
+    keys = W.biased_keys(torch, gen, dev, 8, 32768, 64)
+    ccfg = P.ChannelQuantConfig(64, 4, 64)
+    nt = 32768
+    kbufs = []
+    for s in range(args.sets):
+        kk = keys if s == 0 else W.biased_keys(torch, gen, dev, 8, 32768, 64, first_head=8 * s)
+        c = torch.empty(8 * nt * ccfg.codeStride, dtype=torch.uint8, device=dev)
+        r = torch.empty(8 * ccfg.groupCount(nt) * 2 * 64, dtype=torch.float16, device=dev)
+        kbufs.append((kk, c, r, torch.empty_like(kk)))
+    # one call over all heads: groups never cross a head (32768 % 64 == 0)
+    ms_ke = timer.time(lambda i: q.enqueuePerChannelEncode(kbufs[i % len(kbufs)][0], kbufs[i % len(kbufs)][1],
+                                                           kbufs[i % len(kbufs)][2], 8 * nt, ccfg), steps, warm)
+    ms_kd = timer.time(lambda i: q.enqueuePerChannelDecode(kbufs[i % len(kbufs)][1], kbufs[i % len(kbufs)][2],
+                                                           kbufs[i % len(kbufs)][3], 8 * nt, ccfg), steps, warm)
+    kb = kivi_bytes(nt, 64, 4, 64, heads=8)
+    # parity gate for KIVI: codes, ranges and decode bit-exact on every head
+    for h in range(8):
+        kh = keys[h].cpu().numpy()
+        codes_ref, ranges_ref = O.channel_encode(kh, 4, 64)
+        ch = kbufs[0][1][h * nt * ccfg.codeStride:(h + 1) * nt * ccfg.codeStride].cpu().numpy().tobytes()
+        g = ccfg.groupCount(nt)
+        rh = kbufs[0][2][h * g * 128:(h + 1) * g * 128].cpu().numpy()
+        dh = kbufs[0][3][h].cpu().numpy()
+        if (ch != O.pack_codes(codes_ref, 4) or not np.array_equal(rh.view(np.uint16),
+                                                                   ranges_ref.reshape(-1).view(np.uint16))
+                or not np.array_equal(dh.view(np.uint32),
+                                      O.channel_decode(codes_ref, ranges_ref, 4, 64).view(np.uint32))):
+            raise SystemExit(f"config 3 KIVI parity failed at head {h}")
+    out["cfg3_kivi_d64_b4_G64"] = codec_row(kb, 8 * nt, ms_ke, ms_kd, bit_exact_all_heads=True)
+    if args.extras:
+        # the KIVI encoder reads 128-byte row pieces (32 channels of one token) and writes codes plus fp16 ranges:
+        # 256 + 32 + 4 bytes per token at d = 64, b = 4, G = 64
+        pairs = [(kb_[0], torch.empty(8 * nt * 9, dtype=torch.int32, device=dev)) for kb_ in kbufs]
+        out["cfg3_kivi_d64_b4_G64"]["encode_stream_ceiling"] = StreamCeiling(torch).measure(
+            timer, pairs, 8 * nt, 256, 9, 128, kb / ms_ke / 1e6, steps, warm)
+        del pairs
+        if not args.no_cpu:
+            k0 = keys[0].cpu().numpy()
+            t_e, _ = cpu_time(lambda: O.channel_encode(k0, 4, 64), 4.0)
+            cr, rr = O.channel_encode(k0, 4, 64)
+            t_d, _ = cpu_time(lambda: O.channel_decode(cr, rr, 4, 64), 4.0)
+            kb1 = kivi_bytes(nt, 64, 4, 64)
+            out["cfg3_kivi_d64_b4_G64"]["cpu_baseline"] = {
+                "encode_gbps": round(kb1 / t_e / 1e9, 4), "decode_gbps": round(kb1 / t_d / 1e9, 4), "cores": 1,
+                "kind": "port", "sample": f"oracle channel_encode / channel_decode of one head (32768 tokens), "
+                                          f"1 thread: {t_e * 1e3:.1f} / {t_d * 1e3:.1f} ms per head"}
+    del kbufs, keys
+    # ---- config 4: Qwen2.5-1.5B shape d=128, 28 L x 2 h x 16384 tokens, TurboQuant and PolarQuant b=4
+    print("# config 4: TurboQuant and PolarQuant b = 4 at d = 128", file=sys.stderr, flush=True)
+    n4 = 28 * 2 * 16384
+    keys4 = torch.cat([W.qwen_keys(torch, gen, dev, 2, 16384, 128, first_head=2 * layer).reshape(-1, 128)
+                       for layer in range(28)])
+    ceiling4 = None
+    for method in ("turboQuant", "polarQuant"):
+        cfg4 = P.QuantConfig(method, 128, 4)
+        c = torch.empty(n4 * cfg4.codeStride, dtype=torch.uint8, device=dev)
+        s_ = torch.empty(n4, dtype=torch.float32, device=dev)
+        o = torch.empty_like(keys4)
+        ms_e = timer.time(lambda i: q.enqueueEncode(keys4, c, s_, n4, cfg4), steps, warm)
+        ms_d = timer.time(lambda i: q.enqueueDecode(c, s_, o, n4, cfg4), steps, warm)
+        idx = sample_rows(n4, 4, 4096)
+        it = torch.from_numpy(idx).to(dev)
+        C = c.view(n4, cfg4.codeStride)[it].cpu().numpy().tobytes()
+        S = s_[it].cpu().numpy()
+        X4 = keys4[it].cpu().numpy()
+        diffs = check_vector_encode(O, method, X4, C, S, 128, 4, f"config 4 {method}")
+        rel = check_vector_decode(O, method, C, S, o[it].cpu().numpy(), 128, 4, f"config 4 {method}")
+        nb = n4 * per_vector_bytes(128, 4)
+        key = f"cfg4_{'tq' if method == 'turboQuant' else 'polar'}_d128_b4"
+        out[key] = codec_row(nb, n4, ms_e, ms_d, parity_code_diffs_near_boundary=diffs, parity_decode_max_rel_l2=rel)
+        if args.extras:
+            if ceiling4 is None:  # the same bytes for both methods (codeStride 64 at b = 4)
+                o4 = torch.empty(n4 * 17, dtype=torch.int32, device=dev)
+                ceiling4 = StreamCeiling(torch).measure(timer, [(keys4, o4)], n4, 512, (cfg4.codeStride + 4) // 4,
+                                                        128, nb / ms_e / 1e6, steps, warm)
+                del o4
+                out[key]["encode_stream_ceiling"] = ceiling4
+            else:
+                enc = nb / ms_e / 1e6
+                out[key]["encode_stream_ceiling"] = {
+                    "same_as": "cfg4_tq_d128_b4",
+                    "encoder_frac_of_encoder_shape": round(enc / ceiling4["encoder_shape"]["gbps"], 3),
+                    "encoder_frac_of_best": round(enc / ceiling4["best"]["gbps"], 3)}
+            if not args.no_cpu:
+                X64 = X4[:4096].astype(np.float64)
+                t_e, _ = cpu_time(lambda: O.ENCODERS[method](X64, 4), 3.0)
+                cc, ss_ = O.ENCODERS[method](X64, 4)
+                t_d, _ = cpu_time(lambda: O.DECODERS[method](cc, np.asarray(ss_, np.float32).astype(np.float64), 4),
+                                  3.0)
+                out[key]["cpu_baseline"] = {
+                    "encode_gbps": round(4096 * per_vector_bytes(128, 4) / t_e / 1e9, 4),
+                    "decode_gbps": round(4096 * per_vector_bytes(128, 4) / t_d / 1e9, 4), "cores": 1, "kind": "port",
+                    "sample": "oracle encode / decode of 4096 sampled config-4 vectors, 1 thread, extrapolated per "
+                              "vector"}
+        del c, s_, o
+    del keys4
+    torch.cuda.empty_cache()
+    return out
+
+
+def target_summary(rows: dict, head: dict, extra: dict) -> dict:
+    """% of the 8 TB/s peak of every bulk encode and full-cache decode the north-star target names (d = 64 and
+    128, every method), beside the target of 70 %."""
+    pcts = {}
+    for key, r in rows.items():
+        if "encode_pct_peak" in r:
+            pcts[f"{key}_encode"] = r["encode_pct_peak"]
+            pcts[f"{key}_decode"] = r["decode_pct_peak"]
+    pcts["cfg5_V_tq_d128_b3_decode"] = head["pct_of_hbm_peak"]
+    enc5 = extra.get("cfg5_V_tq_d128_b3_encode_one_call")
+    if enc5:
+        pcts["cfg5_V_tq_d128_b3_encode"] = enc5["pct_peak"]
+    k5 = extra.get("cfg5_K_kivi_d128_b4_G64_one_call")
+    if k5:
+        pcts["cfg5_K_kivi_d128_b4_encode"] = k5["encode_pct_peak"]
+        pcts["cfg5_K_kivi_d128_b4_decode"] = k5["decode_pct_peak"]
+    below = sorted(k for k, v in pcts.items() if v < 70.0)
+    return {"target_pct": 70.0, "pct_of_peak": pcts, "rows": len(pcts), "rows_at_or_above": len(pcts) - len(below),
+            "below": below, "min_pct": min(pcts.values())}
+
+
+
 # ------------------------------------------------------------------------------------------- --extras
 def run_extras(torch, q, P, O, W, timer, dev, args) -> dict:
-    """BASELINE configs 1-4, single-call latency percentiles, 16-bit caches, attention and key-bias removal."""
+    """BASELINE config 1, single-call latency percentiles, 16-bit caches, attention and key-bias removal."""
     import numpy as np
     out = {}
     steps, warm = max(20, args.steps), 5
@@ -584,157 +799,9 @@ def run_extras(torch, q, P, O, W, timer, dev, args) -> dict:
                 "encode": timer.single_calls(lambda i: q.enqueueEncode(xs, cs_, ss, nb, cfg)),
                 "decode": timer.single_calls(lambda i: q.enqueueDecode(cs_, ss, os_, nb, cfg))}
     out["single_call_tq_b4"] = sc
-    # ---- config 2: GPT-2 value cache, decode at b = 2, 3, 4 and bulk encode, over rotated buffer sets
-    d, n = 64, 32768 * 12
-    x = W.gpt2_values(torch, gen, dev)
-    for b in (2, 3, 4):
-        cfg = P.QuantConfig("turboQuant", d, b)
-        bufs = []
-        for s in range(args.sets):
-            xs = x if s == 0 else W.gpt2_values(torch, gen, dev)
-            c = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=dev)
-            nm = torch.empty(n, dtype=torch.float32, device=dev)
-            q.enqueueEncode(xs, c, nm, n, cfg)
-            bufs.append((xs, c, nm, torch.empty((n, d), dtype=torch.float32, device=dev)))
-        ms_enc = timer.time(lambda i: q.enqueueEncode(bufs[i % len(bufs)][0], bufs[i % len(bufs)][1],
-                                                      bufs[i % len(bufs)][2], n, cfg), steps, warm)
-        ms_dec = timer.time(lambda i: q.enqueueDecode(bufs[i % len(bufs)][1], bufs[i % len(bufs)][2],
-                                                      bufs[i % len(bufs)][3], n, cfg), steps, warm)
-        idx = sample_rows(n, b, 2048)
-        it = torch.from_numpy(idx).to(dev)
-        C = bufs[0][1].view(n, cfg.codeStride)[it].cpu().numpy().tobytes()
-        S = bufs[0][2][it].cpu().numpy()
-        diffs = check_vector_encode(O, "turboQuant", x.view(n, d)[it].cpu().numpy(), C, S, d, b, f"config 2 b={b}")
-        rel = check_vector_decode(O, "turboQuant", C, S, bufs[0][3][it].cpu().numpy(), d, b, f"config 2 b={b}")
-        nb = n * per_vector_bytes(d, b)
-        out[f"cfg2_tq_d64_b{b}"] = {"encode_gbps": round(nb / ms_enc / 1e6, 1), "decode_gbps": round(nb / ms_dec / 1e6, 1),
-                                    "encode_ms": round(ms_enc, 5), "decode_ms": round(ms_dec, 5),
-                                    "encode_pct_peak": round(nb / ms_enc / 1e6 / PEAK_GBPS * 100, 1),
-                                    "decode_pct_peak": round(nb / ms_dec / 1e6 / PEAK_GBPS * 100, 1),
-                                    "parity_code_diffs_near_boundary": diffs, "parity_decode_max_rel_l2": rel}
-        if b == 4:
-            pairs = [(bf[0], torch.empty(n * 9, dtype=torch.int32, device=dev)) for bf in bufs]
-            out[f"cfg2_tq_d64_b{b}"]["encode_stream_ceiling"] = StreamCeiling(torch).measure(
-                timer, pairs, n, 4 * d, (cfg.codeStride + 4) // 4, 64, nb / ms_enc / 1e6, steps, warm)
-            del pairs
-        if b == 4 and not args.no_cpu:
-            out[f"cfg2_tq_d64_b{b}"]["cpu_baseline"] = cpu_baseline_vector_decode(
-                O, bufs[0][1][:65536 * cfg.codeStride].cpu().numpy().tobytes(), bufs[0][2][:65536].cpu().numpy(),
-                d, b, "config 2 value cache (first 2^16 vectors)", 6.0)
-        del bufs
-    # append-encode latency: 12 vectors per step at codesOffset = t*12*cs
-    cfg = P.QuantConfig("turboQuant", d, 3)
-    codes = torch.empty(32768 * 12 * cfg.codeStride, dtype=torch.uint8, device=dev)
-    norms = torch.empty(32768 * 12, dtype=torch.float32, device=dev)
-
-    def app(i):
-        t = i % 32768
-        q.enqueueEncode(x, codes, norms, 12, cfg, inputOffset=t * 12 * d * 4, codesOffset=t * 12 * cfg.codeStride,
-                        scalesOffset=t * 12 * 4)
-
-    ms_app = timer.time(app, 500, 50)
-    out["cfg2_append_encode_12vec"] = {"gpu_us_per_call_backtoback": round(ms_app * 1e3, 2),
-                                       "single_call": timer.single_calls(app)}
-    del x, codes, norms
-    # ---- config 3: KIVI keys, Llama-3.2-1B shape (8 heads x 32768 tokens x 64), G=64, b=4
-    keys = W.biased_keys(torch, gen, dev, 8, 32768, 64)
-    ccfg = P.ChannelQuantConfig(64, 4, 64)
-    nt = 32768
-    kbufs = []
-    for s in range(args.sets):
-        kk = keys if s == 0 else W.biased_keys(torch, gen, dev, 8, 32768, 64, first_head=8 * s)
-        c = torch.empty(8 * nt * ccfg.codeStride, dtype=torch.uint8, device=dev)
-        r = torch.empty(8 * ccfg.groupCount(nt) * 2 * 64, dtype=torch.float16, device=dev)
-        kbufs.append((kk, c, r, torch.empty_like(kk)))
-    # one call over all heads: groups never cross a head (32768 % 64 == 0)
-    ms_ke = timer.time(lambda i: q.enqueuePerChannelEncode(kbufs[i % len(kbufs)][0], kbufs[i % len(kbufs)][1],
-                                                           kbufs[i % len(kbufs)][2], 8 * nt, ccfg), steps, warm)
-    ms_kd = timer.time(lambda i: q.enqueuePerChannelDecode(kbufs[i % len(kbufs)][1], kbufs[i % len(kbufs)][2],
-                                                           kbufs[i % len(kbufs)][3], 8 * nt, ccfg), steps, warm)
-    kb = kivi_bytes(nt, 64, 4, 64, heads=8)
-    # parity gate for KIVI: bit-exact on every head
-    exact = True
-    for h in range(8):
-        kh = keys[h].cpu().numpy()
-        codes_ref, ranges_ref = O.channel_encode(kh, 4, 64)
-        ch = kbufs[0][1][h * nt * ccfg.codeStride:(h + 1) * nt * ccfg.codeStride].cpu().numpy().tobytes()
-        g = ccfg.groupCount(nt)
-        rh = kbufs[0][2][h * g * 128:(h + 1) * g * 128].cpu().numpy()
-        exact &= (ch == O.pack_codes(codes_ref, 4)) and np.array_equal(rh.view(np.uint16),
-                                                                      ranges_ref.reshape(-1).view(np.uint16))
-    if not exact:
-        raise SystemExit("config 3 KIVI parity failed")
-    out["cfg3_kivi_d64_b4_G64"] = {"encode_gbps": round(kb / ms_ke / 1e6, 1), "decode_gbps": round(kb / ms_kd / 1e6, 1),
-                                   "encode_ms": round(ms_ke, 5), "decode_ms": round(ms_kd, 5),
-                                   "encode_pct_peak": round(kb / ms_ke / 1e6 / PEAK_GBPS * 100, 1),
-                                   "decode_pct_peak": round(kb / ms_kd / 1e6 / PEAK_GBPS * 100, 1),
-                                   "bit_exact_all_heads": True}
-    # the KIVI encoder reads 128-byte row pieces (32 channels of one token) and writes codes plus fp16 ranges:
-    # 256 + 32 + 4 bytes per token at d = 64, b = 4, G = 64
-    pairs = [(kb_[0], torch.empty(8 * nt * 9, dtype=torch.int32, device=dev)) for kb_ in kbufs]
-    out["cfg3_kivi_d64_b4_G64"]["encode_stream_ceiling"] = StreamCeiling(torch).measure(
-        timer, pairs, 8 * nt, 256, 9, 128, kb / ms_ke / 1e6, steps, warm)
-    del pairs
-    if not args.no_cpu:
-        k0 = keys[0].cpu().numpy()
-        t_e, _ = cpu_time(lambda: O.channel_encode(k0, 4, 64), 4.0)
-        cr, rr = O.channel_encode(k0, 4, 64)
-        t_d, _ = cpu_time(lambda: O.channel_decode(cr, rr, 4, 64), 4.0)
-        kb1 = kivi_bytes(nt, 64, 4, 64)
-        out["cfg3_kivi_d64_b4_G64"]["cpu_baseline"] = {
-            "encode_gbps": round(kb1 / t_e / 1e9, 4), "decode_gbps": round(kb1 / t_d / 1e9, 4), "cores": 1,
-            "kind": "port", "sample": f"oracle channel_encode / channel_decode of one head (32768 tokens), 1 thread: "
-                                      f"{t_e * 1e3:.1f} / {t_d * 1e3:.1f} ms per head"}
-    del kbufs, keys
-    # ---- config 4: Qwen2.5-1.5B shape d=128, 28 L x 2 h x 16384 tokens, TurboQuant and PolarQuant b=4
-    n4 = 28 * 2 * 16384
+    x2 = W.gpt2_values(torch, gen, dev)
     keys4 = torch.cat([W.qwen_keys(torch, gen, dev, 2, 16384, 128, first_head=2 * layer).reshape(-1, 128)
                        for layer in range(28)])
-    o4 = torch.empty(n4 * 17, dtype=torch.int32, device=dev)
-    ceiling4 = None
-    for method in ("turboQuant", "polarQuant"):
-        cfg4 = P.QuantConfig(method, 128, 4)
-        c = torch.empty(n4 * cfg4.codeStride, dtype=torch.uint8, device=dev)
-        s_ = torch.empty(n4, dtype=torch.float32, device=dev)
-        o = torch.empty_like(keys4)
-        ms_e = timer.time(lambda i: q.enqueueEncode(keys4, c, s_, n4, cfg4), steps, warm)
-        ms_d = timer.time(lambda i: q.enqueueDecode(c, s_, o, n4, cfg4), steps, warm)
-        idx = sample_rows(n4, 4, 4096)
-        it = torch.from_numpy(idx).to(dev)
-        C = c.view(n4, cfg4.codeStride)[it].cpu().numpy().tobytes()
-        S = s_[it].cpu().numpy()
-        X4 = keys4[it].cpu().numpy()
-        diffs = check_vector_encode(O, method, X4, C, S, 128, 4, f"config 4 {method}")
-        rel = check_vector_decode(O, method, C, S, o[it].cpu().numpy(), 128, 4, f"config 4 {method}")
-        nb = n4 * per_vector_bytes(128, 4)
-        out[f"cfg4_{method}_d128_b4"] = {"encode_gbps": round(nb / ms_e / 1e6, 1), "decode_gbps": round(nb / ms_d / 1e6, 1),
-                                         "encode_ms": round(ms_e, 5), "decode_ms": round(ms_d, 5),
-                                         "encode_pct_peak": round(nb / ms_e / 1e6 / PEAK_GBPS * 100, 1),
-                                         "decode_pct_peak": round(nb / ms_d / 1e6 / PEAK_GBPS * 100, 1),
-                                         "vectors_per_s_decode": round(n4 / ms_d * 1e3, 1),
-                                         "parity_code_diffs_near_boundary": diffs, "parity_decode_max_rel_l2": rel}
-        if ceiling4 is None:  # the same bytes for both methods (codeStride 64 at b = 4)
-            ceiling4 = StreamCeiling(torch).measure(timer, [(keys4, o4)], n4, 512, (cfg4.codeStride + 4) // 4, 128,
-                                                    nb / ms_e / 1e6, steps, warm)
-            out[f"cfg4_{method}_d128_b4"]["encode_stream_ceiling"] = ceiling4
-        else:
-            enc = nb / ms_e / 1e6
-            out[f"cfg4_{method}_d128_b4"]["encode_stream_ceiling"] = {
-                "same_as": "cfg4_turboQuant_d128_b4",
-                "encoder_frac_of_encoder_shape": round(enc / ceiling4["encoder_shape"]["gbps"], 3),
-                "encoder_frac_of_best": round(enc / ceiling4["best"]["gbps"], 3)}
-        if not args.no_cpu:
-            X64 = X4[:4096].astype(np.float64)
-            t_e, _ = cpu_time(lambda: O.ENCODERS[method](X64, 4), 3.0)
-            cc, ss_ = O.ENCODERS[method](X64, 4)
-            t_d, _ = cpu_time(lambda: O.DECODERS[method](cc, np.asarray(ss_, np.float32).astype(np.float64), 4), 3.0)
-            out[f"cfg4_{method}_d128_b4"]["cpu_baseline"] = {
-                "encode_gbps": round(4096 * per_vector_bytes(128, 4) / t_e / 1e9, 4),
-                "decode_gbps": round(4096 * per_vector_bytes(128, 4) / t_d / 1e9, 4), "cores": 1, "kind": "port",
-                "sample": "oracle encode / decode of 4096 sampled config-4 vectors, 1 thread, extrapolated per vector"}
-        del c, s_, o
-    del o4
-    x2 = W.gpt2_values(torch, gen, dev)
     out.update(run_io16(torch, q, P, W, timer, gen, dev, args, x2, keys4))
     del x2, keys4
     torch.cuda.empty_cache()

@@ -282,7 +282,9 @@ int pitch_enqueue_attention_decode_key_bias(
  * PITCH_NOALLOC_SCRATCH_BYTES fail with PITCH_ERR_INVALID_INPUT before any work is issued. Every call on a device
  * shares that device's array: calls that overlap on one device (on different streams, or from different threads
  * without ordering) race and must not be issued; calls ordered on one stream are safe. Results are otherwise those
- * of pitch_enqueue_attention_decode on the same arguments. */
+ * of pitch_enqueue_attention_decode on the same arguments. The array's device address is looked up (one
+ * hipGetSymbolAddress, no allocation) by the first call of any pitch_enqueue_* entry point on the device, so a caller
+ * that captures a HIP graph makes that lookup outside the capture by issuing any one call on the device first. */
 int pitch_enqueue_attention_decode_noalloc(const pitch_config_t* key_config, const pitch_config_t* value_config,
                                            const pitch_attention_desc_t* desc, const void* q, uint64_t q_bytes,
                                            uint64_t q_offset, const void* key_codes, uint64_t key_codes_bytes,

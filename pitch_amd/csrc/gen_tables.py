@@ -160,10 +160,11 @@ def main(src: str, dst: str) -> None:
                 info.append("{-1, 0, 0.0, 0.0}")
                 continue
             scale, off, ent = lut
-            # The staged-stage TurboQuant encoder compares in the bucket domain t = u * 2^m + off + 2^k + 2^(k-1)
-            # (k = 13 or 17, t in [2^k, 2^(k+1))) and keeps each entry's code in the low 8 mantissa bits of its
-            # mapped edge: the mapping must be exact and leave those bits zero.
-            for k in (13, 17):
+            # The TurboQuant encoders compare in the bucket domain t = u * 2^m + off + 2^k + 2^(k-1) (k = 17 -
+            # log2 of the table's copies in LDS: 12 ... 17 for 32 ... 1 copies, t in [2^k, 2^(k+1))) and keep each
+            # entry's code in the low 8 mantissa bits of its mapped edge: the mapping must be exact and leave those
+            # bits zero at every k a kernel can compile.
+            for k in range(12, 18):
                 magic = 2.0 ** k + 2.0 ** (k - 1) + off
                 for e_bits, c in ent:
                     e = float(np.uint32(e_bits).view(np.float32))

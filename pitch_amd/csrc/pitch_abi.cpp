@@ -7,6 +7,7 @@
 // The reference's 32-bit limit on count * dim is lifted (64-bit counts and offsets).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -91,12 +92,47 @@ int check_device(const void* ptr, int dev, const char* name) {
   return PITCH_OK;
 }
 
+// Scratch memory of pitch_enqueue_attention_decode_noalloc: the attention workspace for callers that cannot
+// allocate device memory. One copy per device, held until the process ends; every call on a device shares it.
+// Its device address comes from hipGetSymbolAddress (the array's name is only a host-side stand-in), looked up
+// by the first call of any entry point that launches work on the device (current_device), so that a caller who
+// captures a graph after any eager call on the device makes no lookup inside the capture.
+constexpr uint64_t kNoAllocScratchBytes = PITCH_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on device dev, which must be the current device (looked up once per device).
+int scratch_address(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "device %d is out of range", dev);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "scratch memory of device %d is unavailable: %s", dev,
+                    hipGetErrorString(e));
+      }
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return PITCH_OK;
+}
+
+// The current device; the first call on a device also looks up its scratch array (scratch_address).
 int current_device(int* dev) {
   if (hipGetDevice(dev) != hipSuccess) {
     (void)hipGetLastError();
     return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "no HIP device is available");
   }
-  return PITCH_OK;
+  void* unused = nullptr;
+  return scratch_address(*dev, &unused);
 }
 
 bool mul_overflows(uint64_t a, uint64_t b) { return b != 0 && a > UINT64_MAX / b; }
@@ -430,14 +466,12 @@ int device_cu_count() {
 }
 
 uint32_t attention_chunk_tokens(uint64_t tokens, uint32_t kv_heads) {
-  // PITCH_ATTN_CHUNK (64 ... 1024, a power of two) overrides the choice (tuning aid); otherwise the largest
-  // chunk that still gives at least 512 workgroups (two per compute unit), between 128 and 1024 tokens
-  static const uint32_t override_chunk = [] {
-    const char* e = std::getenv("PITCH_ATTN_CHUNK");
-    const int v = e ? std::atoi(e) : 0;
-    return (v >= 64 && v <= 1024 && (v & (v - 1)) == 0) ? (uint32_t)v : 0u;
-  }();
-  if (override_chunk) return override_chunk;
+  // The largest chunk that still gives at least 512 workgroups (two per compute unit), between 128 and 1024
+  // tokens; PITCH_ATTN_CHUNK (a compile-time tuning macro: 64 ... 1024, a power of two) fixes it instead.
+  static_assert(PITCH_ATTN_CHUNK == 0 ||
+                    (PITCH_ATTN_CHUNK >= 64 && PITCH_ATTN_CHUNK <= 1024 && (PITCH_ATTN_CHUNK & (PITCH_ATTN_CHUNK - 1)) == 0),
+                "PITCH_ATTN_CHUNK: 0 or a power of two in 64 ... 1024");
+  if (PITCH_ATTN_CHUNK) return PITCH_ATTN_CHUNK;
   uint32_t chunk = 1024;
   while (chunk > 128 && (tokens + chunk - 1) / chunk * kv_heads < 512) chunk >>= 1;
   return chunk;
@@ -448,34 +482,18 @@ uint64_t attention_workspace_floats(uint32_t dim, uint32_t nqp, uint32_t kv_head
   return (uint64_t)kv_heads * nqp * (3 * dim + tokens + chunks * (2 + dim));
 }
 
-uint64_t slice_rounds(uint64_t dflt) {
-  static const long env = [] {
-    const char* e = std::getenv("PITCH_SLICE_ROUNDS");
-    return e ? std::atol(e) : -1L;
-  }();
-  return env >= 0 ? (uint64_t)env : dflt;
-}
+uint64_t slice_rounds(uint64_t dflt) { return PITCH_SLICE_ROUNDS >= 0 ? (uint64_t)PITCH_SLICE_ROUNDS : dflt; }
 
-uint64_t stream_decode_min_vectors() {
-  static const uint64_t v = [] {
-    const char* e = std::getenv("PITCH_STREAM_MIN_VECTORS");
-    return e ? (uint64_t)std::atoll(e) : (uint64_t)(1u << 22);
-  }();
-  return v;
-}
+uint64_t stream_decode_min_vectors() { return (uint64_t)PITCH_STREAM_MIN_VECTORS; }
 
 uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size, bool balance_rounds) {
   static std::mutex mu;
   static std::unordered_map<const void*, int> occ_cache;
-  // PITCH_BLOCKS_PER_CU overrides the resident 256-thread-block count per CU (tuning aid; smaller blocks
-  // scale it up); 0 or unset = occupancy.
-  static const int override_per_cu = [] {
-    const char* e = std::getenv("PITCH_BLOCKS_PER_CU");
-    return e ? std::atoi(e) : 0;
-  }();
+  // PITCH_BLOCKS_PER_CU (a compile-time tuning macro) fixes the resident 256-thread-block count per CU
+  // (smaller blocks scale it up); 0 = occupancy.
   int occ = 0;
-  if (override_per_cu > 0) {
-    occ = override_per_cu * (256 / block_size);
+  if (PITCH_BLOCKS_PER_CU > 0) {
+    occ = PITCH_BLOCKS_PER_CU * (256 / block_size);
   } else {
     std::lock_guard<std::mutex> lock(mu);
     auto it = occ_cache.find(kernel);
@@ -507,17 +525,9 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
 }
 
 uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size) {
-  // PITCH_ENC_BLOCKS_PER_WG overrides the blocks per workgroup of long calls (tuning aid); 0 keeps every call
-  // persistent.
-  static const long per_wg = [] {
-    const char* e = std::getenv("PITCH_ENC_BLOCKS_PER_WG");
-    return e ? std::atol(e) : 8L;
-  }();
-  // PITCH_ENC_MIN_ROUNDS: the resident rounds from which a call is oversubscribed (tuning aid)
-  static const long min_rounds = [] {
-    const char* e = std::getenv("PITCH_ENC_MIN_ROUNDS");
-    return e ? std::atol(e) : 32L;
-  }();
+  // blocks per workgroup of long calls (PITCH_ENC_BLOCKS_PER_WG; 0 keeps every call persistent) and the resident
+  // rounds from which a call is oversubscribed (PITCH_ENC_MIN_ROUNDS): compile-time tuning macros
+  constexpr long per_wg = PITCH_ENC_BLOCKS_PER_WG, min_rounds = PITCH_ENC_MIN_ROUNDS;
   const uint64_t cap = persistent_grid(kernel, blocks_needed, block_size);
   if (per_wg <= 0 || blocks_needed < (uint64_t)(min_rounds > 1 ? min_rounds : 1) * cap) return cap;
   const uint64_t g = blocks_needed / (uint64_t)per_wg;
@@ -681,34 +691,6 @@ int pitch_attention_workspace_size(const pitch_config_t* key_config, const pitch
 }  // extern "C"
 
 namespace {
-
-// Scratch memory of pitch_enqueue_attention_decode_noalloc: the attention workspace for callers that cannot
-// allocate device memory. One copy per device, held until the process ends; every call on a device shares it.
-// Its device address comes from hipGetSymbolAddress (the array's name is only a host-side stand-in).
-constexpr uint64_t kNoAllocScratchBytes = PITCH_NOALLOC_SCRATCH_BYTES;
-static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
-
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
-
-// The scratch array's address on device dev, which must be the current device (looked up once per device).
-int scratch_address(int dev, void** out) {
-  if (dev < 0 || dev >= kMaxDevices) return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "device %d is out of range", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    void* ptr = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !ptr) {
-      (void)hipGetLastError();
-      return fail(PITCH_ERR_DEVICE_UNAVAILABLE, "scratch memory of device %d is unavailable: %s", dev,
-                  hipGetErrorString(e));
-    }
-    g_scratch_ptr[dev] = ptr;
-  }
-  *out = g_scratch_ptr[dev];
-  return PITCH_OK;
-}
 
 // pitch_enqueue_attention_decode with either a caller's workspace or (workspace == nullptr) the library's scratch.
 int attention_impl(const pitch_config_t* key_config, const pitch_config_t* value_config,

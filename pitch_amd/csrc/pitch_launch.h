@@ -4,6 +4,26 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Launch-shape tuning macros (compile-time; the library reads no environment variables).
+#ifndef PITCH_ATTN_CHUNK
+#define PITCH_ATTN_CHUNK 0  // attention tokens per chunk: 0 = by call size (attention_chunk_tokens)
+#endif
+#ifndef PITCH_SLICE_ROUNDS
+#define PITCH_SLICE_ROUNDS -1  // rounds per launch of every sliced call: -1 = each kernel's own default
+#endif
+#ifndef PITCH_STREAM_MIN_VECTORS
+#define PITCH_STREAM_MIN_VECTORS (1u << 22)  // smallest float32 D = 128 decode run by the streaming decoder
+#endif
+#ifndef PITCH_BLOCKS_PER_CU
+#define PITCH_BLOCKS_PER_CU 0  // resident 256-thread blocks per CU of persistent grids: 0 = occupancy
+#endif
+#ifndef PITCH_ENC_BLOCKS_PER_WG
+#define PITCH_ENC_BLOCKS_PER_WG 8  // blocks per workgroup of long staged encodes: 0 = always persistent
+#endif
+#ifndef PITCH_ENC_MIN_ROUNDS
+#define PITCH_ENC_MIN_ROUNDS 32  // resident rounds from which a staged encode is oversubscribed
+#endif
+
 namespace pitch {
 
 // Arguments of one per-vector encode or decode launch (pointers already advanced by the byte offsets).
@@ -125,11 +145,11 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
 uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256);
 
 // Rounds (grid-stride iterations per workgroup) per launch when a call of more rounds is split into several
-// launches, or 0 for one launch: PITCH_SLICE_ROUNDS when set (tuning aid), else dflt.
+// launches, or 0 for one launch: PITCH_SLICE_ROUNDS when it is 0 or more, else dflt.
 uint64_t slice_rounds(uint64_t dflt);
 
-// Smallest call (vectors) the float32 D = 128 decode issues through the streaming decoder (PITCH_STREAM_MIN_VECTORS
-// when set, a tuning aid).
+// Smallest call (vectors) the float32 D = 128 decode issues through the streaming decoder (PITCH_STREAM_MIN_VECTORS).
+// Both decoders write the same bytes, so the threshold changes only the speed.
 uint64_t stream_decode_min_vectors();
 
 // Per-vector launch for one dimension D and I/O element type IO (0 float32, 1 float16, 2 bfloat16); one

@@ -836,6 +836,21 @@ __device__ __forceinline__ void decode_chunk(uint32_t bits, const float* s_tab, 
   }
 }
 
+// The last step of every per-vector decoder: x = s * (H y) * scale / sqrt(d). y comes from fwht_f32_lane_signed,
+// equal to the transform up to the lane's sign (lane_sign) and, for a zero, up to the sign of that zero, which
+// differs between lane layouts. dec_scale folds the lane's sign into the vector's factor; dec_out multiplies by it
+// with an fma whose addend is +0, which gives every exact zero the sign +0 (RN(-0 + +0) = +0) and every other
+// value RN(y * f), then applies the coordinate's random sign. So each decoder, whatever its lane layout, writes
+// the same bytes for the same codes: a zero of the transform decodes to +0 with the coordinate's sign applied,
+// as the reference's wht(y) * signs gives for a transform zero of +0 (pitch_reference.py:34).
+template <int D>
+__device__ __forceinline__ float dec_scale(float scale, uint32_t lane_sign) {
+  return __uint_as_float(__float_as_uint(scale * DimConst<D>::kInvSqrtF) ^ lane_sign);
+}
+__device__ __forceinline__ float dec_out(float y, float f, uint32_t sign) {
+  return __uint_as_float(__float_as_uint(__builtin_fmaf(y, f, 0.0f)) ^ sign);
+}
+
 #ifndef PITCH_DEC_LDS_STORE
 #define PITCH_DEC_LDS_STORE 1  // decoded vectors are staged in LDS and stored as contiguous wave blocks
 #endif
@@ -874,11 +889,12 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   const int wave = tid >> 6, vw = lane / G::T;  // vector of this lane's team within the wave
 
   const uint32_t fbits = p.lane_flips[t];
-  // the transform's lane sign (fwht_f32_lane_signed) is folded into the random sign flips
+  // the transform's lane sign (fwht_f32_lane_signed) is folded into the scale factor (dec_scale), the random
+  // signs are applied to the scaled values
   const uint32_t lane_sign = dpp_lane_sign_bit<D>(t);
   uint32_t flip[G::E];
 #pragma unroll
-  for (int e = 0; e < G::E; ++e) flip[e] = (((fbits >> e) & 1u) << 31) ^ lane_sign;
+  for (int e = 0; e < G::E; ++e) flip[e] = ((fbits >> e) & 1u) << 31;
   // word index and bit offset of each of this lane's chunks (the next word is read when a chunk straddles)
   int wlo[G::CH], whi[G::CH];
   uint32_t wsh[G::CH];
@@ -946,7 +962,7 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   };
   auto body = [&](const Batch& b, float (&y)[G::E], float scale) {
     const uint64_t v = b.wb + (uint64_t)local_vector(b);
-    const float f = scale * DimConst<D>::kInvSqrtF;
+    const float f = dec_scale<D>(scale, lane_sign);
     if constexpr (kLdsStore) {
       // stage the wave's vectors in LDS, then write them back as contiguous 1 KB wave stores
       float* ws = s_out + (tid >> 6) * kWaveOutFloats;
@@ -955,7 +971,7 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
         float o[G::W];
 #pragma unroll
         for (int r = 0; r < G::W; ++r)
-          o[r] = __uint_as_float(__float_as_uint(y[k * G::W + r] * f) ^ flip[k * G::W + r]);
+          o[r] = dec_out(y[k * G::W + r], f, flip[k * G::W + r]);
         *(float4*)(ws + vw * kVecStride + G::W * (k * G::T + t)) = float4{o[0], o[1], o[2], o[3]};
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -991,7 +1007,7 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
         float o[G::W];
 #pragma unroll
         for (int r = 0; r < G::W; ++r)
-          o[r] = __uint_as_float(__float_as_uint(y[k * G::W + r] * f) ^ flip[k * G::W + r]);
+          o[r] = dec_out(y[k * G::W + r], f, flip[k * G::W + r]);
         if constexpr (KBIAS) {
           float ob[G::W];
           key_bias_offset<D, G::W>(p, v, G::W * (k * G::T + t), ob);
@@ -1176,7 +1192,7 @@ __global__ __launch_bounds__(kBlock, kStreamWaves) void vec_decode_stream(VecArg
                                 y + k * G::W);
     }
     fwht_f32_lane_signed<D, TB::PRE, kStreamE, kWide>(y, t);
-    const float f = s_scale[wave][lv] * DimConst<D>::kInvSqrtF;
+    const float f = dec_scale<D>(s_scale[wave][lv], lane_sign);
     const uint64_t v = wb + (uint64_t)lv;
 #pragma unroll
     for (int k = 0; k < G::CH; ++k) {
@@ -1184,7 +1200,7 @@ __global__ __launch_bounds__(kBlock, kStreamWaves) void vec_decode_stream(VecArg
 #pragma unroll
       for (int r = 0; r < G::W; ++r) {
         const int e = k * G::W + r;
-        o[r] = __uint_as_float(__float_as_uint(y[e] * f) ^ (((fbits >> e) & 1u) << 31) ^ lane_sign);
+        o[r] = dec_out(y[e], f, ((fbits >> e) & 1u) << 31);
       }
       store_elems<0, G::W>(p.out, v * D + G::W * (k * G::T + t), o, PITCH_STREAM_NT);
     }

@@ -7,7 +7,8 @@ dimension, method and bit width is checked:
 * sampled rows against the oracle's decode of the same codes: relative L2 <= 1e-5 (pitch_reference.py:104-107,
   123-129);
 * the first and last 65536 vectors against the persistent decoder (separate calls below the streaming size, through
-  byte offsets): relative L2 <= 1e-6 per vector (both float32, different transform orders);
+  byte offsets): byte for byte, so a slice decoded at an offset equals the same rows of a whole-cache decode (both
+  decoders run the butterflies in the same bit order and give exact zeros the sign +0 before the rotation signs);
 * every output element written (pre-filled with NaN) and finite.
 """
 import numpy as np
@@ -47,8 +48,7 @@ def test_stream_decode(q, D, method, bits):
         part = torch.empty(m, D, device=dev)
         q.enqueueDecode(codes, scales, part, m, cfg, codesOffset=v0 * cfg.codeStride, scalesOffset=v0 * 4)
         torch.cuda.synchronize()
-        a, b = out[v0:v0 + m].double(), part.double()
-        rel = ((a - b).square().sum(1) / b.square().sum(1).clamp_min(1e-300)).sqrt().max()
-        assert float(rel) < 1e-6, (v0, float(rel))
+        differ = int((out[v0:v0 + m].view(torch.int32) != part.view(torch.int32)).sum())
+        assert differ == 0, (v0, differ)
     del codes, scales, out
     torch.cuda.empty_cache()
