@@ -678,16 +678,23 @@ def run_target_rows(torch, q, P, O, W, timer, dev, args) -> dict:
     # ---- config 4: Qwen2.5-1.5B shape d=128, 28 L x 2 h x 16384 tokens, TurboQuant and PolarQuant b=4
     print("# config 4: TurboQuant and PolarQuant b = 4 at d = 128", file=sys.stderr, flush=True)
     n4 = 28 * 2 * 16384
+    # two caches (the second a roll of the first), rotated call by call: a call's 0.53 GB never finds the previous
+    # call's inputs or outputs in the 256 MB Infinity Cache
     keys4 = torch.cat([W.qwen_keys(torch, gen, dev, 2, 16384, 128, first_head=2 * layer).reshape(-1, 128)
                        for layer in range(28)])
+    inputs4 = [keys4, torch.roll(keys4, 4099, 0).contiguous()]
     ceiling4 = None
     for method in ("turboQuant", "polarQuant"):
         cfg4 = P.QuantConfig(method, 128, 4)
-        c = torch.empty(n4 * cfg4.codeStride, dtype=torch.uint8, device=dev)
-        s_ = torch.empty(n4, dtype=torch.float32, device=dev)
-        o = torch.empty_like(keys4)
-        ms_e = timer.time(lambda i: q.enqueueEncode(keys4, c, s_, n4, cfg4), steps, warm)
-        ms_d = timer.time(lambda i: q.enqueueDecode(c, s_, o, n4, cfg4), steps, warm)
+        sets4 = [(xk, torch.empty(n4 * cfg4.codeStride, dtype=torch.uint8, device=dev),
+                  torch.empty(n4, dtype=torch.float32, device=dev), torch.empty_like(keys4)) for xk in inputs4]
+        for xk, c, s_, _ in sets4:
+            q.enqueueEncode(xk, c, s_, n4, cfg4)
+        ms_e = timer.time(lambda i: q.enqueueEncode(sets4[i % 2][0], sets4[i % 2][1], sets4[i % 2][2], n4, cfg4),
+                          steps, warm)
+        ms_d = timer.time(lambda i: q.enqueueDecode(sets4[i % 2][1], sets4[i % 2][2], sets4[i % 2][3], n4, cfg4),
+                          steps, warm)
+        _, c, s_, o = sets4[0]
         idx = sample_rows(n4, 4, 4096)
         it = torch.from_numpy(idx).to(dev)
         C = c.view(n4, cfg4.codeStride)[it].cpu().numpy().tobytes()
@@ -722,10 +729,55 @@ def run_target_rows(torch, q, P, O, W, timer, dev, args) -> dict:
                     "decode_gbps": round(4096 * per_vector_bytes(128, 4) / t_d / 1e9, 4), "cores": 1, "kind": "port",
                     "sample": "oracle encode / decode of 4096 sampled config-4 vectors, 1 thread, extrapolated per "
                               "vector"}
-        del c, s_, o
-    del keys4
+        if method == "turboQuant":
+            out["cfg4_layer_calls_tq_d128_b4"] = run_layer_calls(torch, q, P, timer, sets4[0], cfg4, 28, n4 // 28,
+                                                                 steps, warm)
+        del c, s_, o, sets4
+    del keys4, inputs4
     torch.cuda.empty_cache()
     return out
+
+
+def run_layer_calls(torch, q, P, timer, bufs, cfg, layers: int, per: int, steps: int, warm: int) -> dict:
+    """A model's per-layer calls (README.md:65-76: one enqueueEncode / enqueueDecode per layer's cache): `layers`
+    caches of `per` vectors, laid out one after another in the buffers, encoded and decoded as one call per layer
+    (back to back) and as one batched call over every layer (EncodeBatch / DecodeBatch); the batched calls must write
+    the bytes the per-layer calls write."""
+    x, codes, scales, o = bufs
+    d, cs = cfg.dim, cfg.codeStride
+    nb = layers * per * per_vector_bytes(d, cfg.bits)
+    xs = [x[l * per:(l + 1) * per] for l in range(layers)]
+    cl = [codes[l * per * cs:(l + 1) * per * cs] for l in range(layers)]
+    sl = [scales[l * per:(l + 1) * per] for l in range(layers)]
+    ol = [o[l * per:(l + 1) * per] for l in range(layers)]
+
+    def enc_layers(i):
+        for l in range(layers):
+            q.enqueueEncode(xs[l], cl[l], sl[l], per, cfg)
+
+    def dec_layers(i):
+        for l in range(layers):
+            q.enqueueDecode(cl[l], sl[l], ol[l], per, cfg)
+
+    etab = P.EncodeBatch(q, cfg, xs, cl, sl)
+    dtab = P.DecodeBatch(q, cfg, cl, sl, ol)
+    ms_e = timer.time(enc_layers, steps, warm)
+    ms_d = timer.time(dec_layers, steps, warm)
+    ref_c, ref_s, ref_o = codes.clone(), scales.clone(), o.clone()
+    ms_eb = timer.time(lambda i: etab.enqueue(per), steps, warm)
+    ms_db = timer.time(lambda i: dtab.enqueue(per), steps, warm)
+    torch.cuda.synchronize()
+    if not (torch.equal(codes, ref_c) and torch.equal(scales.view(torch.int32), ref_s.view(torch.int32))
+            and torch.equal(o.view(torch.int32), ref_o.view(torch.int32))):
+        raise SystemExit("layer calls: the batched calls wrote other bytes than the per-layer calls")
+    return {"layers": layers, "vectors_per_layer": per,
+            "encode_per_layer_calls_us": round(ms_e * 1e3, 2), "encode_per_layer_calls_gbps": round(nb / ms_e / 1e6, 1),
+            "encode_one_batched_call_us": round(ms_eb * 1e3, 2),
+            "encode_one_batched_call_gbps": round(nb / ms_eb / 1e6, 1), "encode_one_batched_call_pct_peak": pct(nb, ms_eb),
+            "decode_per_layer_calls_us": round(ms_d * 1e3, 2), "decode_per_layer_calls_gbps": round(nb / ms_d / 1e6, 1),
+            "decode_one_batched_call_us": round(ms_db * 1e3, 2),
+            "decode_one_batched_call_gbps": round(nb / ms_db / 1e6, 1), "decode_one_batched_call_pct_peak": pct(nb, ms_db),
+            "batched_bytes_equal_per_layer_calls": True}
 
 
 def target_summary(rows: dict, head: dict, extra: dict) -> dict:

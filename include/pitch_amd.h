@@ -138,6 +138,27 @@ int pitch_enqueue_decode_io(const pitch_config_t* config, uint32_t io_type, cons
                             uint64_t scales_offset, void* output, uint64_t output_bytes, uint64_t output_offset,
                             uint64_t count, void* stream);
 
+/* One segment of a batched decode: count vectors' codes from codes + codes_offset and scales from scales +
+ * scales_offset, decoded to output + output_offset (byte offsets and sizes as in pitch_enqueue_decode_io). */
+typedef struct pitch_decode_item {
+  const void* codes;
+  uint64_t codes_bytes, codes_offset;
+  const void* scales;
+  uint64_t scales_bytes, scales_offset;
+  void* output;
+  uint64_t output_bytes, output_offset;
+  uint64_t count;
+} pitch_decode_item_t;
+
+/* Decodes n_items independent segments with one configuration and output element type io_type (PITCH_IO_*) in as
+ * few launches as it can (one per 32 segments), writing the same bytes as one pitch_enqueue_decode_io per segment.
+ * Every segment is validated as that call validates it, before anything is launched. For a model's per-layer
+ * decodes (README.md:65-76 decodes each layer's cache with its own PITCH.enqueueDecode, Sources/PITCH/PITCH.swift:
+ * 156-165): a layer of one decode step is a few tens of thousands of vectors, too few to fill the GPU alone, and
+ * one call over every layer's cache runs at the rate of a bulk decode. */
+int pitch_enqueue_decode_batch(const pitch_config_t* config, uint32_t io_type, const pitch_decode_item_t* items,
+                               uint32_t n_items, void* stream);
+
 /* Key-projection bias removal for the per-vector methods (reference/mechanism_eval.py:88-97,113-116: a model
  * whose key projection adds a bias b before RoPE has keys k = R_t W x + R_t b; compressing k - R_t b and adding
  * R_t b back restores the per-vector methods, README.md:28; "not yet built into the kernels", README.md:100).

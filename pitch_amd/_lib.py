@@ -52,6 +52,14 @@ class PitchEncodeItemC(ctypes.Structure):
                 ("count", ctypes.c_uint64)]
 
 
+class PitchDecodeItemC(ctypes.Structure):
+    """pitch_decode_item_t: one segment of pitch_enqueue_decode_batch (ten 64-bit fields)."""
+    _fields_ = [("codes", ctypes.c_void_p), ("codes_bytes", ctypes.c_uint64), ("codes_offset", ctypes.c_uint64),
+                ("scales", ctypes.c_void_p), ("scales_bytes", ctypes.c_uint64), ("scales_offset", ctypes.c_uint64),
+                ("output", ctypes.c_void_p), ("output_bytes", ctypes.c_uint64), ("output_offset", ctypes.c_uint64),
+                ("count", ctypes.c_uint64)]
+
+
 class PitchChannelConfigC(ctypes.Structure):
     _fields_ = [("dim", ctypes.c_uint32), ("bits", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
                 ("reserved", ctypes.c_uint32)]
@@ -77,6 +85,8 @@ SIGNATURES = {
     "pitch_enqueue_encode_io": (_int, [ctypes.POINTER(PitchConfigC), _u32, _vp, _u64, _u64, _vp, _u64, _u64,
                                        _vp, _u64, _u64, _u64, _vp]),
     "pitch_enqueue_encode_batch": (_int, [ctypes.POINTER(PitchConfigC), _u32, ctypes.POINTER(PitchEncodeItemC),
+                                          _u32, _vp]),
+    "pitch_enqueue_decode_batch": (_int, [ctypes.POINTER(PitchConfigC), _u32, ctypes.POINTER(PitchDecodeItemC),
                                           _u32, _vp]),
     "pitch_enqueue_decode_io": (_int, [ctypes.POINTER(PitchConfigC), _u32, _vp, _u64, _u64, _vp, _u64, _u64,
                                        _vp, _u64, _u64, _u64, _vp]),

@@ -752,6 +752,35 @@ class PITCH:
             rc = self._lib.pitch_enqueue_decode_io(ctypes.byref(config._c()), io, *args)
         _raise_for(rc)
 
+    def enqueueDecodeBatch(self, items, config: QuantConfig, stream=None, elementType=None) -> None:
+        """Decodes independent segments with one configuration in one call (pitch_enqueue_decode_batch), writing
+        the same bytes as one enqueueDecode per segment. items: a sequence of (codes, scales, output, count) or
+        (codes, scales, output, count, codesOffset, scalesOffset, outputOffset); every output has the element type
+        elementType, else the first output's, chosen as for enqueueDecode. For a model's per-layer decodes
+        (README.md:65-76 decodes each layer's cache with its own enqueueDecode); DecodeBatch keeps the segment
+        table between calls."""
+        items = list(items)
+        if not items:
+            raise InvalidInput("a batch needs at least one segment")
+        io = _io_type(items[0][2], elementType)
+        arr = (_lib.PitchDecodeItemC * len(items))()
+        for i, it in enumerate(items):
+            if len(it) not in (4, 7):
+                raise InvalidInput("a segment is (codes, scales, output, count[, codesOffset, scalesOffset, "
+                                   "outputOffset])")
+            offs = it[4:] if len(it) == 7 else (0, 0, 0)
+            _check_offsets(*offs)
+            if _io_type(it[2], elementType) != io:
+                raise InvalidInput("every segment's output must have the batch's element type")
+            e = arr[i]
+            e.codes, e.codes_bytes = _buf(it[0], "codes")
+            e.scales, e.scales_bytes = _buf(it[1], "scales")
+            e.output, e.output_bytes = _buf(it[2], "output")
+            e.codes_offset, e.scales_offset, e.output_offset = (int(o) for o in offs)
+            e.count = _count(it[3])
+        _raise_for(self._lib.pitch_enqueue_decode_batch(ctypes.byref(config._c()), io, arr, len(items),
+                                                        _stream_handle(stream, self.device)))
+
     def enqueuePerChannelAppend(self, input, codes, ranges, totalTokens: int, newTokens: int,
                                 config: ChannelQuantConfig, inputOffset: int = 0, codesOffset: int = 0,
                                 rangesOffset: int = 0, stream=None, elementType=None) -> None:
@@ -947,6 +976,49 @@ class EncodeBatch:
         t[:, 8] = scalesOffsets
         p = self._pitch
         _raise_for(p._lib.pitch_enqueue_encode_batch(ctypes.byref(self.config._c()), self._io, self._arr, self._n,
+                                                     _stream_handle(stream, p.device)))
+
+
+class DecodeBatch:
+    """A segment table for pitch_enqueue_decode_batch kept between calls: one segment per (codes, scales, output)
+    buffer triple, e.g. one per layer's cache. Each enqueue sets the segments' counts and byte offsets in place
+    (scalars or one value per segment) and issues one batched decode, so a decode step's per-layer decodes cost
+    one call. The buffers are held for the table's lifetime."""
+
+    def __init__(self, pitch: "PITCH", config: QuantConfig, codes, scales, outputs, elementType=None):
+        self._pitch, self.config = pitch, config
+        self._bufs = (list(codes), list(scales), list(outputs))
+        n = len(self._bufs[0])
+        if n < 1 or len(self._bufs[1]) != n or len(self._bufs[2]) != n:
+            raise InvalidInput("codes, scales and outputs need one buffer per segment")
+        self._io = _io_type(self._bufs[2][0], elementType)
+        if any(_io_type(t, elementType) != self._io for t in self._bufs[2]):
+            raise InvalidInput("every segment's output must have the batch's element type")
+        self._arr = (_lib.PitchDecodeItemC * n)()
+        self._tab = np.frombuffer(self._arr, dtype=np.uint64).reshape(n, 10)  # the C array's fields, in place
+        for i in range(n):
+            e = self._arr[i]
+            e.codes, e.codes_bytes = _buf(self._bufs[0][i], "codes")
+            e.scales, e.scales_bytes = _buf(self._bufs[1][i], "scales")
+            e.output, e.output_bytes = _buf(self._bufs[2][i], "output")
+        self._n = n
+
+    def __len__(self) -> int:
+        return self._n
+
+    def enqueue(self, count, codesOffsets=0, scalesOffsets=0, outputOffsets=0, stream=None) -> None:
+        for name, v in (("count", count), ("offset", codesOffsets), ("offset", scalesOffsets),
+                        ("offset", outputOffsets)):
+            a = np.asarray(v)
+            if a.dtype.kind not in "iu" or (a < (1 if name == "count" else 0)).any():
+                raise InvalidInput(f"{name} {v!r} must be {'at least 1' if name == 'count' else 'non-negative'}")
+        t = self._tab
+        t[:, 9] = count
+        t[:, 2] = codesOffsets
+        t[:, 5] = scalesOffsets
+        t[:, 8] = outputOffsets
+        p = self._pitch
+        _raise_for(p._lib.pitch_enqueue_decode_batch(ctypes.byref(self.config._c()), self._io, self._arr, self._n,
                                                      _stream_handle(stream, p.device)))
 
 

@@ -180,6 +180,21 @@ constexpr VecBatchVpb kVecBatchVpb[10][3] = {
     PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
 #undef PITCH_VEC_ROW
 
+using DecBatchLaunch = hipError_t (*)(bool, int, const pitch::DecBatchArgs&, hipStream_t);
+using DecBatchVpb = uint32_t (*)();
+#define PITCH_VEC_ROW(D) \
+  {pitch::launch_vec_dec_batch_d##D##_io0, pitch::launch_vec_dec_batch_d##D##_io1, pitch::launch_vec_dec_batch_d##D##_io2}
+constexpr DecBatchLaunch kDecBatchLaunch[10][3] = {
+    PITCH_VEC_ROW(2),  PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),   PITCH_VEC_ROW(16),  PITCH_VEC_ROW(32),
+    PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
+#undef PITCH_VEC_ROW
+#define PITCH_VEC_ROW(D) \
+  {pitch::vec_dec_batch_vpb_d##D##_io0, pitch::vec_dec_batch_vpb_d##D##_io1, pitch::vec_dec_batch_vpb_d##D##_io2}
+constexpr DecBatchVpb kDecBatchVpb[10][3] = {
+    PITCH_VEC_ROW(2),  PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),   PITCH_VEC_ROW(16),  PITCH_VEC_ROW(32),
+    PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
+#undef PITCH_VEC_ROW
+
 int dim_index(uint32_t dim) {
   int li = 0;
   while ((2u << li) < dim) ++li;
@@ -313,6 +328,56 @@ int encode_batch_impl(const pitch_config_t* config, uint32_t io, const pitch_enc
     const hipError_t e = kVecBatchLaunch[li][io](config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
                                                 (hipStream_t)stream);
     if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
+  }
+  return ok();
+}
+
+int decode_batch_impl(const pitch_config_t* config, uint32_t io, const pitch_decode_item_t* items, uint32_t n,
+                      void* stream) {
+  PITCH_TRY(validate_config(config));
+  PITCH_TRY(check_io(io));
+  if (n < 1) return fail(PITCH_ERR_INVALID_INPUT, "a batch needs at least one segment");
+  if (!items) return fail(PITCH_ERR_INVALID_INPUT, "segment array is null");
+  const uint32_t dim = config->dim, cs = code_stride_of(dim, config->bits);
+  for (uint32_t i = 0; i < n; ++i) {
+    const pitch_decode_item_t& it = items[i];
+    if (it.count < 1) return fail(PITCH_ERR_INVALID_INPUT, "segment %u: count must be at least 1", i);
+    if (mul_overflows(it.count, (uint64_t)dim * 4u))
+      return fail(PITCH_ERR_INVALID_INPUT, "segment %u: count is too large", i);
+    PITCH_TRY(check_buffer(it.codes, it.codes_bytes, it.codes_offset, it.count * cs, "codes"));
+    PITCH_TRY(check_buffer(it.scales, it.scales_bytes, it.scales_offset, it.count * 4u, "scales"));
+    PITCH_TRY(check_buffer(it.output, it.output_bytes, it.output_offset, it.count * dim * io_bytes(io), "output"));
+  }
+  int dev = 0;
+  PITCH_TRY(current_device(&dev));
+  for (uint32_t i = 0; i < n; ++i) {
+    const pitch_decode_item_t& it = items[i];
+    PITCH_TRY(check_device(it.codes, dev, "codes"));
+    PITCH_TRY(check_device(it.scales, dev, "scales"));
+    PITCH_TRY(check_device(it.output, dev, "output"));
+  }
+  const int li = dim_index(dim);
+  const uint64_t vpb = kDecBatchVpb[li][io]();
+  pitch::DecBatchArgs a{};
+  a.common.seed = config->seed;
+  for (uint32_t i0 = 0; i0 < n; i0 += pitch::kBatchItems) {
+    const uint32_t m = n - i0 < pitch::kBatchItems ? n - i0 : pitch::kBatchItems;
+    a.items = m;
+    uint32_t blocks = 0;
+    for (uint32_t j = 0; j < m; ++j) {
+      const pitch_decode_item_t& it = items[i0 + j];
+      const uint64_t need = (it.count + vpb - 1) / vpb;
+      a.block_start[j] = blocks;
+      blocks += (uint32_t)(need < kBatchMaxBlocks ? need : kBatchMaxBlocks);
+      a.codes_in[j] = at<const uint32_t>(it.codes, it.codes_offset);
+      a.scales_in[j] = at<const float>(it.scales, it.scales_offset);
+      a.out[j] = at<char>(it.output, it.output_offset);
+      a.count[j] = it.count;
+    }
+    a.block_start[m] = blocks;
+    const hipError_t e = kDecBatchLaunch[li][io](config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
+                                                (hipStream_t)stream);
+    if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));
   }
   return ok();
 }
@@ -580,6 +645,11 @@ int pitch_enqueue_encode_io(const pitch_config_t* config, uint32_t io_type, cons
 int pitch_enqueue_encode_batch(const pitch_config_t* config, uint32_t io_type, const pitch_encode_item_t* items,
                                uint32_t n_items, void* stream) {
   return encode_batch_impl(config, io_type, items, n_items, stream);
+}
+
+int pitch_enqueue_decode_batch(const pitch_config_t* config, uint32_t io_type, const pitch_decode_item_t* items,
+                               uint32_t n_items, void* stream) {
+  return decode_batch_impl(config, io_type, items, n_items, stream);
 }
 
 int pitch_enqueue_decode(const pitch_config_t* config, const void* codes, uint64_t codes_bytes,

@@ -862,8 +862,11 @@ __device__ __forceinline__ float dec_out(float y, float f, uint32_t sign) {
 #define PITCH_DEC_WAVES 1  // minimum waves per SIMD requested for the decoders (caps their VGPRs)
 #endif
 
+// The body of every per-vector decode: count vectors from codes_in / scales_in to out (p supplies the sign masks and
+// the key bias), with this workgroup block of nblocks striding over the call.
 template <int D, int B, bool POLAR, int IO, bool KBIAS>
-__global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p) {
+__device__ __forceinline__ void vec_decode_run(const VecArgs& p, const uint32_t* codes_in, const float* scales_in,
+                                               void* out, uint64_t count, uint64_t block, uint64_t nblocks) {
   using G = Geom<D>;
   using TB = DecTab<B, POLAR, G::W>;
   constexpr int NW = (D * B + 31) / 32;
@@ -922,23 +925,23 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   auto fetch = [&](uint64_t base) {
     Batch b;
     const uint64_t nominal = base + (uint64_t)wave * G::V;
-    b.wb = p.count >= (uint64_t)G::V ? (nominal < p.count - G::V ? nominal : p.count - G::V) : 0;
-    const uint32_t* cw = p.codes_in + b.wb * NW;
+    b.wb = count >= (uint64_t)G::V ? (nominal < count - G::V ? nominal : count - G::V) : 0;
+    const uint32_t* cw = codes_in + b.wb * NW;
     // in a call of fewer than V vectors, words past the call's last one read the last word (never used)
-    const uint64_t last = p.count * NW - 1 - b.wb * NW;
+    const uint64_t last = count * NW - 1 - b.wb * NW;
 #pragma unroll
     for (int m = 0; m < NPL; ++m) {
       const uint64_t i = (uint64_t)(lane + 64 * m < kWaveCodeWords ? lane + 64 * m : kWaveCodeWords - 1);
       b.w[m] = cw[i < last ? i : last];
     }
     const uint64_t vs = b.wb + (uint64_t)(lane % G::V);
-    b.scale = p.scales_in[vs < p.count ? vs : p.count - 1];
+    b.scale = scales_in[vs < count ? vs : count - 1];
     return b;
   };
   // the team's vector within the wave's block: vw, or the call's last vector for teams past the end (only in a
   // call of fewer than V vectors)
   auto local_vector = [&](const Batch& b) -> int {
-    const uint64_t lastv = p.count - 1 - b.wb;
+    const uint64_t lastv = count - 1 - b.wb;
     return (uint64_t)vw < lastv ? vw : (int)lastv;
   };
   // stage the batch in LDS, read the lane's chunks back, table lookups and the transform
@@ -992,13 +995,13 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
         }
         if constexpr (KBIAS) {  // key-bias removal: restore x + o (mechanism_eval.py:113-116)
           float ob[K];
-          const uint64_t vv = wbase + vq < p.count ? wbase + vq : p.count - 1;
+          const uint64_t vv = wbase + vq < count ? wbase + vq : count - 1;
           key_bias_offset<D, K>(p, vv, K * cq, ob);
 #pragma unroll
           for (int r = 0; r < K; ++r) o[r] = o[r] + ob[r];
         }
-        const uint64_t vd = wbase + vq < p.count ? wbase + vq : p.count - 1;
-        store_elems<IO, K>(p.out, vd * D + (uint64_t)K * cq, o, PITCH_NT_STORE);
+        const uint64_t vd = wbase + vq < count ? wbase + vq : count - 1;
+        store_elems<IO, K>(out, vd * D + (uint64_t)K * cq, o, PITCH_NT_STORE);
       }
       __builtin_amdgcn_wave_barrier();
     } else {
@@ -1014,7 +1017,7 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
 #pragma unroll
           for (int r = 0; r < G::W; ++r) o[r] = o[r] + ob[r];
         }
-        store_elems<IO, G::W>(p.out, v * D + G::W * (k * G::T + t), o, PITCH_NT_STORE);
+        store_elems<IO, G::W>(out, v * D + G::W * (k * G::T + t), o, PITCH_NT_STORE);
       }
     }
   };
@@ -1022,8 +1025,8 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   // rotated so that each batch is waited for in straight-line code after exactly one iteration's stores and the
   // next batch's loads: fetch A(i), fetch B(i + 1), compute A(i); then fetch A(i + 2), compute B(i + 1),
   // fetch B(i + 3), compute A(i + 2), ...
-  const uint64_t stride = (uint64_t)gridDim.x * G::VPB;
-  uint64_t base = (uint64_t)blockIdx.x * G::VPB;
+  const uint64_t stride = nblocks * G::VPB;
+  uint64_t base = block * G::VPB;
   auto compute = [&](const Batch& b, uint64_t) {
     float y[G::E];
     float scale;
@@ -1042,22 +1045,38 @@ __global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p)
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  if (base >= p.count) return;  // uniform per workgroup; no barrier follows
+  if (base >= count) return;  // uniform per workgroup; no barrier follows
   compute(ba, base);
   for (;;) {
     base += stride;
-    if (base >= p.count) break;
+    if (base >= count) break;
     ba = fetch(base + stride);
     __builtin_amdgcn_sched_barrier(0);
     compute(bb, base);
     __builtin_amdgcn_sched_barrier(0);
     base += stride;
-    if (base >= p.count) break;
+    if (base >= count) break;
     bb = fetch(base + stride);
     __builtin_amdgcn_sched_barrier(0);
     compute(ba, base);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+template <int D, int B, bool POLAR, int IO, bool KBIAS>
+__global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode(VecArgs p) {
+  vec_decode_run<D, B, POLAR, IO, KBIAS>(p, p.codes_in, p.scales_in, p.out, p.count, blockIdx.x, gridDim.x);
+}
+
+// A batch of independent segments with one configuration in one launch (pitch_enqueue_decode_batch): the blocks
+// [block_start[i], block_start[i + 1]) decode segment i with the body of a single call, so a batch writes the bytes
+// the single calls write (the streaming decoder, which long float32 calls take, writes the same bytes as this one).
+template <int D, int B, bool POLAR, int IO>
+__global__ __launch_bounds__(kBlock, PITCH_DEC_WAVES) void vec_decode_batch(DecBatchArgs pb) {
+  uint32_t i = 0;  // uniform: kernel arguments and the block index
+  for (uint32_t j = 1; j < pb.items; ++j) i = pb.block_start[j] <= blockIdx.x ? j : i;
+  vec_decode_run<D, B, POLAR, IO, false>(pb.common, pb.codes_in[i], pb.scales_in[i], pb.out[i], pb.count[i],
+                                         blockIdx.x - pb.block_start[i], pb.block_start[i + 1] - pb.block_start[i]);
 }
 
 // Per-team-lane sign bits for the seed (cached per thread for the last seed).
@@ -2275,7 +2294,36 @@ template <int D, int B>
 hipError_t launch_batch_bits(bool polar, const VecBatchArgs& a, hipStream_t s) {
   return polar ? launch_batch<D, B, true>(a, s) : launch_batch<D, B, false>(a, s);
 }
+template <int D, int B, bool POLAR>
+hipError_t launch_dec_batch(DecBatchArgs a, hipStream_t s) {
+  fill_lane_flips<D>(a.common.seed, a.common.lane_flips);
+  hipLaunchKernelGGL((vec_decode_batch<D, B, POLAR, PITCH_IO>), dim3(a.block_start[a.items]), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+template <int D, int B>
+hipError_t launch_dec_batch_bits(bool polar, const DecBatchArgs& a, hipStream_t s) {
+  return polar ? launch_dec_batch<D, B, true>(a, s) : launch_dec_batch<D, B, false>(a, s);
+}
 }  // namespace
+
+uint32_t PITCH_CAT(PITCH_CAT(PITCH_CAT(vec_dec_batch_vpb_d, PITCH_DIM), _io), PITCH_IO)() {
+  return Geom<PITCH_DIM>::VPB;
+}
+
+hipError_t PITCH_CAT(PITCH_CAT(PITCH_CAT(launch_vec_dec_batch_d, PITCH_DIM), _io), PITCH_IO)(bool polar, int bits,
+                                                                                        const DecBatchArgs& a,
+                                                                                        hipStream_t s) {
+  switch (bits) {
+    case 2: return launch_dec_batch_bits<PITCH_DIM, 2>(polar, a, s);
+    case 3: return launch_dec_batch_bits<PITCH_DIM, 3>(polar, a, s);
+    case 4: return launch_dec_batch_bits<PITCH_DIM, 4>(polar, a, s);
+    case 5: return launch_dec_batch_bits<PITCH_DIM, 5>(polar, a, s);
+    case 6: return launch_dec_batch_bits<PITCH_DIM, 6>(polar, a, s);
+    case 7: return launch_dec_batch_bits<PITCH_DIM, 7>(polar, a, s);
+    case 8: return launch_dec_batch_bits<PITCH_DIM, 8>(polar, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 uint32_t PITCH_CAT(PITCH_CAT(PITCH_CAT(vec_batch_vpb_d, PITCH_DIM), _io), PITCH_IO)(bool polar) {
   return polar ? enc_vectors_per_block<PITCH_DIM, true, PITCH_IO>() : enc_vectors_per_block<PITCH_DIM, false, PITCH_IO>();

@@ -473,6 +473,45 @@ def test_encode_batch_validation(lib):
     assert "segment" not in _lib.last_error() and "needs" not in _lib.last_error()
 
 
+def test_decode_batch_validation(lib):
+    """pitch_enqueue_decode_batch checks every segment as pitch_enqueue_decode checks its buffers (sizes after the
+    offsets, 4-byte offsets, count >= 1), naming the segment, before it looks for a device."""
+    assert ctypes.sizeof(_lib.PitchDecodeItemC) == 80
+    cfg = _lib.PitchConfigC(0, 64, 4, 0)                 # code stride 32 bytes
+    bufs = []
+
+    def items(specs):
+        arr = (_lib.PitchDecodeItemC * len(specs))()
+        for e, (count, cb, sb, ob, offs) in zip(arr, specs):
+            c, s, o = Host(cb), Host(sb), Host(ob)
+            bufs.extend((c, s, o))
+            e.codes, e.codes_bytes, e.codes_offset = c.p, cb, offs[0]
+            e.scales, e.scales_bytes, e.scales_offset = s.p, sb, offs[1]
+            e.output, e.output_bytes, e.output_offset = o.p, ob, offs[2]
+            e.count = count
+        return arr
+
+    good = (3, 3 * 32, 12, 3 * 256, (0, 0, 0))
+    call = lambda arr, n=None, c=cfg, io=0: lib.pitch_enqueue_decode_batch(  # noqa: E731
+        ctypes.byref(c) if c is not None else None, io, arr, len(arr) if n is None else n, None)
+    assert call(items([good, good])) in (_lib.ERR_INVALID_INPUT, _lib.ERR_DEVICE_UNAVAILABLE)
+    assert "segment" not in _lib.last_error()
+    assert call(items([good]), n=0) == _lib.ERR_INVALID_INPUT
+    assert lib.pitch_enqueue_decode_batch(ctypes.byref(cfg), 0, None, 1, None) == _lib.ERR_INVALID_INPUT
+    assert call(items([good]), c=None) == _lib.ERR_INVALID_INPUT
+    assert call(items([good]), c=_lib.PitchConfigC(0, 96, 4, 0)) == _lib.ERR_INVALID_DIMENSION
+    assert call(items([good]), io=3) == _lib.ERR_INVALID_INPUT
+    assert call(items([good, (0, 0, 0, 0, (0, 0, 0))])) == _lib.ERR_INVALID_INPUT
+    assert "segment 1" in _lib.last_error()
+    assert call(items([good, good, (3, 3 * 32, 12, 3 * 256 - 4, (0, 0, 0))])) == _lib.ERR_INVALID_INPUT
+    assert "output" in _lib.last_error()
+    assert call(items([(3, 3 * 32 + 8, 12, 3 * 256, (6, 0, 0))])) == _lib.ERR_INVALID_INPUT   # misaligned
+    assert call(items([(3, 3 * 32, 16, 3 * 256, (0, 8, 0))])) == _lib.ERR_INVALID_INPUT       # 8 bytes left
+    assert call(items([(3, 3 * 32, 12, 3 * 128, (0, 0, 0))]), io=1) in (_lib.ERR_INVALID_INPUT,
+                                                                       _lib.ERR_DEVICE_UNAVAILABLE)
+    assert "segment" not in _lib.last_error() and "needs" not in _lib.last_error()
+
+
 def test_attention_key_bias_validation(lib):
     """The key-bias attention entry: null key bias, a head count other than the call's KV heads and RoPE tables
     too short for first_position + tokens rows are rejected before any device work."""
