@@ -165,7 +165,6 @@ hipError_t launch_vec(uint32_t dim, uint32_t io, bool encode, bool polar, int bi
 }
 
 using VecBatchLaunch = hipError_t (*)(bool, int, const pitch::VecBatchArgs&, hipStream_t);
-using VecBatchVpb = uint32_t (*)(bool);
 
 #define PITCH_VEC_ROW(D) \
   {pitch::launch_vec_batch_d##D##_io0, pitch::launch_vec_batch_d##D##_io1, pitch::launch_vec_batch_d##D##_io2}
@@ -173,24 +172,11 @@ constexpr VecBatchLaunch kVecBatchLaunch[10][3] = {
     PITCH_VEC_ROW(2),  PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),   PITCH_VEC_ROW(16),  PITCH_VEC_ROW(32),
     PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
 #undef PITCH_VEC_ROW
-#define PITCH_VEC_ROW(D) \
-  {pitch::vec_batch_vpb_d##D##_io0, pitch::vec_batch_vpb_d##D##_io1, pitch::vec_batch_vpb_d##D##_io2}
-constexpr VecBatchVpb kVecBatchVpb[10][3] = {
-    PITCH_VEC_ROW(2),  PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),   PITCH_VEC_ROW(16),  PITCH_VEC_ROW(32),
-    PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
-#undef PITCH_VEC_ROW
 
 using DecBatchLaunch = hipError_t (*)(bool, int, const pitch::DecBatchArgs&, hipStream_t);
-using DecBatchVpb = uint32_t (*)();
 #define PITCH_VEC_ROW(D) \
   {pitch::launch_vec_dec_batch_d##D##_io0, pitch::launch_vec_dec_batch_d##D##_io1, pitch::launch_vec_dec_batch_d##D##_io2}
 constexpr DecBatchLaunch kDecBatchLaunch[10][3] = {
-    PITCH_VEC_ROW(2),  PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),   PITCH_VEC_ROW(16),  PITCH_VEC_ROW(32),
-    PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
-#undef PITCH_VEC_ROW
-#define PITCH_VEC_ROW(D) \
-  {pitch::vec_dec_batch_vpb_d##D##_io0, pitch::vec_dec_batch_vpb_d##D##_io1, pitch::vec_dec_batch_vpb_d##D##_io2}
-constexpr DecBatchVpb kDecBatchVpb[10][3] = {
     PITCH_VEC_ROW(2),  PITCH_VEC_ROW(4),   PITCH_VEC_ROW(8),   PITCH_VEC_ROW(16),  PITCH_VEC_ROW(32),
     PITCH_VEC_ROW(64), PITCH_VEC_ROW(128), PITCH_VEC_ROW(256), PITCH_VEC_ROW(512), PITCH_VEC_ROW(1024)};
 #undef PITCH_VEC_ROW
@@ -278,10 +264,6 @@ int encode_impl(const pitch_config_t* config, uint32_t io, const void* input, ui
   return ok();
 }
 
-// Workgroups a batched encode gives one segment: enough for every round of the segment, at most this many
-// (a longer segment loops over its rounds; a batch is meant for short segments).
-constexpr uint64_t kBatchMaxBlocks = 1024;
-
 int encode_batch_impl(const pitch_config_t* config, uint32_t io, const pitch_encode_item_t* items, uint32_t n,
                       void* stream) {
   PITCH_TRY(validate_config(config));
@@ -307,24 +289,18 @@ int encode_batch_impl(const pitch_config_t* config, uint32_t io, const pitch_enc
     PITCH_TRY(check_device(it.scales, dev, "scales"));
   }
   const int li = dim_index(dim);
-  const uint64_t vpb = kVecBatchVpb[li][io](config->method == PITCH_METHOD_POLAR);
   pitch::VecBatchArgs a{};
   a.common.seed = config->seed;
   for (uint32_t i0 = 0; i0 < n; i0 += pitch::kBatchItems) {
     const uint32_t m = n - i0 < pitch::kBatchItems ? n - i0 : pitch::kBatchItems;
-    a.items = m;
-    uint32_t blocks = 0;
+    a.items = m;  // the launcher assigns the segments their workgroups (block_start)
     for (uint32_t j = 0; j < m; ++j) {
       const pitch_encode_item_t& it = items[i0 + j];
-      const uint64_t need = (it.count + vpb - 1) / vpb;
-      a.block_start[j] = blocks;
-      blocks += (uint32_t)(need < kBatchMaxBlocks ? need : kBatchMaxBlocks);
       a.in[j] = at<const char>(it.input, it.input_offset);
       a.codes_out[j] = at<uint32_t>(it.codes, it.codes_offset);
       a.scales_out[j] = at<float>(it.scales, it.scales_offset);
       a.count[j] = it.count;
     }
-    a.block_start[m] = blocks;
     const hipError_t e = kVecBatchLaunch[li][io](config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
                                                 (hipStream_t)stream);
     if (e != hipSuccess) return fail(PITCH_ERR_ENCODING_FAILED, "Encoding failed: %s", hipGetErrorString(e));
@@ -357,24 +333,18 @@ int decode_batch_impl(const pitch_config_t* config, uint32_t io, const pitch_dec
     PITCH_TRY(check_device(it.output, dev, "output"));
   }
   const int li = dim_index(dim);
-  const uint64_t vpb = kDecBatchVpb[li][io]();
   pitch::DecBatchArgs a{};
   a.common.seed = config->seed;
   for (uint32_t i0 = 0; i0 < n; i0 += pitch::kBatchItems) {
     const uint32_t m = n - i0 < pitch::kBatchItems ? n - i0 : pitch::kBatchItems;
-    a.items = m;
-    uint32_t blocks = 0;
+    a.items = m;  // the launcher assigns the segments their workgroups (block_start)
     for (uint32_t j = 0; j < m; ++j) {
       const pitch_decode_item_t& it = items[i0 + j];
-      const uint64_t need = (it.count + vpb - 1) / vpb;
-      a.block_start[j] = blocks;
-      blocks += (uint32_t)(need < kBatchMaxBlocks ? need : kBatchMaxBlocks);
       a.codes_in[j] = at<const uint32_t>(it.codes, it.codes_offset);
       a.scales_in[j] = at<const float>(it.scales, it.scales_offset);
       a.out[j] = at<char>(it.output, it.output_offset);
       a.count[j] = it.count;
     }
-    a.block_start[m] = blocks;
     const hipError_t e = kDecBatchLaunch[li][io](config->method == PITCH_METHOD_POLAR, (int)config->bits, a,
                                                 (hipStream_t)stream);
     if (e != hipSuccess) return fail(PITCH_ERR_DECODING_FAILED, "Decoding failed: %s", hipGetErrorString(e));

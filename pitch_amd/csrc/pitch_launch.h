@@ -50,8 +50,8 @@ struct VecArgs {
 
 // Arguments of one batched encode launch: up to kBatchItems independent segments with one configuration.
 // Segment i (count[i] vectors from in[i] to codes_out[i] / scales_out[i]) is encoded by the workgroups
-// [block_start[i], block_start[i + 1]); block_start[items] is the grid size. common supplies the seed (the
-// launcher fills its lane_flips); its pointers and count are unused.
+// [block_start[i], block_start[i + 1]); block_start[items] is the grid size (the launcher fills block_start).
+// common supplies the seed (the launcher fills its lane_flips); its pointers and count are unused.
 constexpr uint32_t kBatchItems = 32;
 struct VecBatchArgs {
   VecArgs common;
@@ -65,7 +65,8 @@ struct VecBatchArgs {
 
 // Arguments of one batched decode launch: up to kBatchItems independent segments with one configuration. Segment i
 // (count[i] vectors from codes_in[i] / scales_in[i] to out[i]) is decoded by the workgroups [block_start[i],
-// block_start[i + 1]); common supplies the seed (the launcher fills its lane_flips).
+// block_start[i + 1]) (the launcher fills block_start); common supplies the seed (the launcher fills its
+// lane_flips).
 struct DecBatchArgs {
   VecArgs common;
   uint32_t items;
@@ -166,16 +167,13 @@ uint64_t slice_rounds(uint64_t dflt);
 uint64_t stream_decode_min_vectors();
 
 // Per-vector launch for one dimension D and I/O element type IO (0 float32, 1 float16, 2 bfloat16); one
-// object file per (D, IO) defines launch_vec_d<D>_io<IO>, the batched encode launch_vec_batch_d<D>_io<IO>,
-// vec_batch_vpb_d<D>_io<IO>, the vectors each of the batched encode's workgroups takes per round (per method), and
-// the batched decode launch_vec_dec_batch_d<D>_io<IO> with vec_dec_batch_vpb_d<D>_io<IO>, its vectors per workgroup
-// and round.
+// object file per (D, IO) defines launch_vec_d<D>_io<IO>, the batched encode launch_vec_batch_d<D>_io<IO> and the
+// batched decode launch_vec_dec_batch_d<D>_io<IO>. The batched launches fill block_start themselves: the caller
+// sets items and the segments.
 #define PITCH_DECLARE_VEC_LAUNCH_IO(D, IO)                                                                     \
   hipError_t launch_vec_d##D##_io##IO(bool encode, bool polar, int bits, const VecArgs& a, hipStream_t s);      \
   hipError_t launch_vec_batch_d##D##_io##IO(bool polar, int bits, const VecBatchArgs& a, hipStream_t s);        \
-  uint32_t vec_batch_vpb_d##D##_io##IO(bool polar);                                                           \
-  hipError_t launch_vec_dec_batch_d##D##_io##IO(bool polar, int bits, const DecBatchArgs& a, hipStream_t s);    \
-  uint32_t vec_dec_batch_vpb_d##D##_io##IO();
+  hipError_t launch_vec_dec_batch_d##D##_io##IO(bool polar, int bits, const DecBatchArgs& a, hipStream_t s);
 #define PITCH_DECLARE_VEC_LAUNCH(D) \
   PITCH_DECLARE_VEC_LAUNCH_IO(D, 0) PITCH_DECLARE_VEC_LAUNCH_IO(D, 1) PITCH_DECLARE_VEC_LAUNCH_IO(D, 2)
 PITCH_DECLARE_VEC_LAUNCH(2)
