@@ -403,8 +403,17 @@ struct TqQuant {
 // five runs: -1 to +2.6 %), and more copies of the larger tables cost it a wave per SIMD (2-7 % slower at d = 64,
 // b = 6 and 8). The transposed encoder (d >= 256), whose LDS allows it, takes as many copies as fit, up to 32
 // (bank conflicts 0.39 -> 0.00 of its LDS cycles at d = 1024, b = 3 and 4).
-constexpr int lut8_copies(int bytes, bool fill) {
-  if (!fill) return PITCH_LUT8_STAGED_REP * bytes <= PITCH_LUT8_REP_MAX ? PITCH_LUT8_STAGED_REP : 1;
+// The staged-stage encoder's LDS besides its table: the staging rows of its four waves (Hs::WAVES * Hs::ROWS
+// float64, checked in hs_run). Its copies are halved until rows and table fit three workgroups per CU (160 KB):
+// 16 copies of the d = 128, b = 5 table left room for two.
+constexpr int hs_rows_bytes(int D) { return D == 64 ? 41984 : (D == 128 ? 37376 : 0); }
+constexpr int kHsLdsBudget = 54528;
+constexpr int lut8_copies(int bytes, bool fill, int rows_bytes = 0) {
+  if (!fill) {
+    int r = PITCH_LUT8_STAGED_REP * bytes <= PITCH_LUT8_REP_MAX ? PITCH_LUT8_STAGED_REP : 1;
+    while (r > 1 && rows_bytes + r * bytes + 8 > kHsLdsBudget) r /= 2;
+    return r;
+  }
   int r = 1;
   while (r < PITCH_LUT8_REP && 2 * r * bytes <= PITCH_LUT8_REP_MAX) r *= 2;
   return r;
@@ -422,7 +431,7 @@ struct TqLut8 {
   static constexpr PitchLutInfo LI = pitch_lut_info(ilog2(D), B);
   static constexpr bool kLut = LI.offset >= 0;
   static constexpr int N = kLut ? LI.entries : 1;
-  static constexpr int REP = kLut ? lut8_copies(N * 8, D >= 256) : 1;
+  static constexpr int REP = kLut ? lut8_copies(N * 8, D >= 256, hs_rows_bytes(D)) : 1;
   static constexpr int R = 8 * REP;                     // bytes per row
   static constexpr int K = 20 - ilog2(R);               // t in [2^K, 2^(K+1))
   static constexpr double kMagic = double(1 << K) + double(1 << (K - 1)) + LI.off;
@@ -1468,16 +1477,36 @@ __device__ __forceinline__ u32x4 hs_load(const float* p) {
   if constexpr (PITCH_HS_NTL) return __builtin_nontemporal_load((const u32x4*)p);
   else return *(const u32x4*)p;
 }
+// The 16-bit form: the four elements of a staging lane's chunk are 8 bytes.
+__device__ __forceinline__ u32x2 hs_load(const uint16_t* p) {
+  if constexpr (PITCH_HS_NTL) return __builtin_nontemporal_load((const u32x2*)p);
+  else return *(const u32x2*)p;
+}
+// What a staging lane loads per chunk of four elements: 16 bytes of float32, 8 of float16 / bfloat16.
+template <int IO>
+using HsChunk = typename std::conditional<IO == 0, u32x4, u32x2>::type;
+template <int IO>
+using HsElem = typename std::conditional<IO == 0, float, uint16_t>::type;
+// The chunk's four elements as float32 (16-bit ones widened exactly).
+template <int IO>
+__device__ __forceinline__ void hs_chunk_floats(const HsChunk<IO>& c, float (&f)[4]) {
+  if constexpr (IO == 0) {
+    f[0] = __uint_as_float(c.x); f[1] = __uint_as_float(c.y); f[2] = __uint_as_float(c.z); f[3] = __uint_as_float(c.w);
+  } else {
+    widen2<IO>(c.x, f[0], f[1]);
+    widen2<IO>(c.y, f[2], f[3]);
+  }
+}
 
 // Coalesced loads of a wave's block of V vectors: set s, chunk i of lane l is vector base + s * VPS + l / SL
 // at coordinates 4 * (l % SL) + E * i (vectors past the end re-read the last one).
-template <int D, int T>
-__device__ __forceinline__ void hs_fetch(const float* in, uint64_t base, uint64_t count, int lane,
-                                        u32x4 (&pf)[Hs<D, T>::QPL]) {
+template <int D, int T, int IO>
+__device__ __forceinline__ void hs_fetch(const HsElem<IO>* in, uint64_t base, uint64_t count, int lane,
+                                        HsChunk<IO> (&pf)[Hs<D, T>::QPL]) {
   using H = Hs<D, T>;
   const int vl = lane / H::SL, pp = lane % H::SL;
   if (base + H::V <= count) {
-    const float* blk = in + (base + vl) * D + 4 * pp;
+    const HsElem<IO>* blk = in + (base + vl) * D + 4 * pp;
 #pragma unroll
     for (int s = 0; s < H::NSET; ++s)
 #pragma unroll
@@ -1486,7 +1515,7 @@ __device__ __forceinline__ void hs_fetch(const float* in, uint64_t base, uint64_
 #pragma unroll
     for (int s = 0; s < H::NSET; ++s) {
       const uint64_t v = base + s * H::VPS + vl;
-      const float* row = in + (v < count ? v : count - 1) * D + 4 * pp;
+      const HsElem<IO>* row = in + (v < count ? v : count - 1) * D + 4 * pp;
 #pragma unroll
       for (int i = 0; i < T; ++i) pf[s * T + i] = hs_load(row + H::E * i);
     }
@@ -1557,8 +1586,8 @@ void fill_hs_flips(uint32_t seed, uint32_t* out) {
 // Staging of one block (see Hs), one load set at a time: signs, float64, the butterfly stages on the team
 // bits, the LDS rows of the set's compute lanes, which then read their coordinates into x. neg[i * 4 + k] is
 // the lane mask of the sign of element k of chunk i (fill_hs_flips).
-template <int D, int T, bool KBIAS>
-__device__ __forceinline__ void hs_stage(const VecArgs& p, uint64_t count, const u32x4 (&pf)[Hs<D, T>::QPL],
+template <int D, int T, bool KBIAS, int IO>
+__device__ __forceinline__ void hs_stage(const VecArgs& p, uint64_t count, const HsChunk<IO> (&pf)[Hs<D, T>::QPL],
                                          uint64_t base, int lane, const uint64_t* neg, double* sx,
                                          double (&x)[Hs<D, T>::E]) {
   using H = Hs<D, T>;
@@ -1570,8 +1599,8 @@ __device__ __forceinline__ void hs_stage(const VecArgs& p, uint64_t count, const
     double y[T][4];
 #pragma unroll
     for (int i = 0; i < T; ++i) {
-      const u32x4 c = pf[s * T + i];
-      float f[4] = {__uint_as_float(c.x), __uint_as_float(c.y), __uint_as_float(c.z), __uint_as_float(c.w)};
+      float f[4];
+      hs_chunk_floats<IO>(pf[s * T + i], f);
       if constexpr (KBIAS) {  // key-bias removal: encode x - o (mechanism_eval.py:113-116)
         float o[4];
         const uint64_t v = base + s * H::VPS + vs;
@@ -1789,7 +1818,7 @@ constexpr int hs_waves() {
   return POLAR ? PITCH_HS_WAVES_POLAR : (KBIAS ? 2 : (D == 64 ? PITCH_HS_WAVES64 : PITCH_HS_WAVES128));
 }
 
-template <int D, int B, bool POLAR, bool KBIAS>
+template <int D, int B, bool POLAR, bool KBIAS, int IO>
 __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64_t block, uint64_t nblocks) {
   constexpr int T = hs_team<D>();
   using H = Hs<D, T>;
@@ -1797,9 +1826,10 @@ __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64
   using Q = TqLut8<D, B>;
   __shared__ __attribute__((aligned(16))) double s_x[H::WAVES][H::ROWS];
   __shared__ __attribute__((aligned(16))) typename Q::Smem s_q;  // (unused by PolarQuant)
+  static_assert(sizeof(s_x) == hs_rows_bytes(D), "staging rows as the table copies assume");
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const float* in = (const float*)sg.in;
+  const HsElem<IO>* in = (const HsElem<IO>*)sg.in;
   const uint64_t stride = nblocks * H::WAVES * V;
   uint64_t base = (block * H::WAVES + wave) * V;
   // Software pipeline with PFD blocks of loads in flight. The loop is rotated so that each block's loads are
@@ -1813,15 +1843,15 @@ __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64
   __syncthreads();
   if (base >= sg.count) return;
   double* sx = s_x[wave];
-  u32x4 pfa[H::QPL];
-  u32x4 pfb[PFD > 1 ? H::QPL : 1];
+  HsChunk<IO> pfa[H::QPL];
+  HsChunk<IO> pfb[PFD > 1 ? H::QPL : 1];
   double x[E];
   // every fetch is unconditional, like the stores: a block past the end re-reads the last vector (a cache hit)
-  hs_fetch<D, T>(in, base, sg.count, lane, pfa);
-  if constexpr (PFD > 1) hs_fetch<D, T>(in, base + stride, sg.count, lane, pfb);
-  hs_stage<D, T, KBIAS>(p, sg.count, pfa, base, lane, neg, sx, x);
-  auto step = [&](u32x4 (&refill)[H::QPL], u32x4 (&next)[H::QPL]) {
-    hs_fetch<D, T>(in, base + (uint64_t)PFD * stride, sg.count, lane, refill);
+  hs_fetch<D, T, IO>(in, base, sg.count, lane, pfa);
+  if constexpr (PFD > 1) hs_fetch<D, T, IO>(in, base + stride, sg.count, lane, pfb);
+  hs_stage<D, T, KBIAS, IO>(p, sg.count, pfa, base, lane, neg, sx, x);
+  auto step = [&](HsChunk<IO> (&refill)[H::QPL], HsChunk<IO> (&next)[H::QPL]) {
+    hs_fetch<D, T, IO>(in, base + (uint64_t)PFD * stride, sg.count, lane, refill);
     __builtin_amdgcn_sched_barrier(0);  // the loads go out before the compute, not interleaved into it
     hs_compute<D, T, B, POLAR>(sg, s_q, base, lane, sx, x);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1830,7 +1860,7 @@ __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64
     // the next block's staging waits for its loads: keep all of it after the compute
     __builtin_amdgcn_sched_barrier(0);
     base += stride;
-    hs_stage<D, T, KBIAS>(p, sg.count, next, base, lane, neg, sx, x);  // past the end: staged, never computed
+    hs_stage<D, T, KBIAS, IO>(p, sg.count, next, base, lane, neg, sx, x);  // past the end: staged, never computed
   };
   if constexpr (PFD > 1) {
     while (true) {
@@ -1844,17 +1874,17 @@ __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64
   }
 }
 
-template <int D, int B, bool POLAR, bool KBIAS>
+template <int D, int B, bool POLAR, bool KBIAS, int IO>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hs_waves<D, POLAR, KBIAS>())))
 void vec_encode_hs(VecArgs p) {
-  hs_run<D, B, POLAR, KBIAS>(p, call_segment(p), blockIdx.x, gridDim.x);
+  hs_run<D, B, POLAR, KBIAS, IO>(p, call_segment(p), blockIdx.x, gridDim.x);
 }
 
-template <int D, int B, bool POLAR>
+template <int D, int B, bool POLAR, int IO>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hs_waves<D, POLAR, false>())))
 void vec_encode_hs_batch(VecBatchArgs pb) {
   const BatchSlot s = batch_slot(pb);
-  hs_run<D, B, POLAR, false>(pb.common, s.seg, s.block, s.blocks);
+  hs_run<D, B, POLAR, false, IO>(pb.common, s.seg, s.block, s.blocks);
 }
 
 // ----------------------------------------------------------------------------------------------------
@@ -2129,6 +2159,13 @@ void vec_encode_lt_batch(VecBatchArgs pb) {
 #ifndef PITCH_HS_POLAR
 #define PITCH_HS_POLAR 1  // 1: float32 PolarQuant encode at D = 64 / 128 uses vec_encode_hs
 #endif
+// float16 / bfloat16 vectors: the staged-stage encoder (8-byte chunk loads, widened at staging) runs PolarQuant at
+// D = 64 and 128 (measured 18 -> 29 % of peak at D = 64, 17 -> 33 % at 128, against the team encoder) and
+// TurboQuant at D = 128 (40 -> 43 %, against the lane-per-vector encoder); TurboQuant at D = 64 stays on the
+// lane-per-vector encoder (within +-3 % either way).
+#ifndef PITCH_HS_IO16
+#define PITCH_HS_IO16 1
+#endif
 
 template <int D>
 constexpr bool use_lpv_encoder() { return D >= 8 && D <= 128; }
@@ -2137,7 +2174,9 @@ constexpr bool use_lpv_encoder() { return D >= 8 && D <= 128; }
 enum class EncKind { kStaged, kTransposed, kLanePerVector, kTeam };
 template <int D, bool POLAR, int IO, bool KBIAS>
 constexpr EncKind enc_kind() {
-  if (IO == 0 && (POLAR ? PITCH_HS_POLAR : PITCH_HS_ENCODER) && (D == 64 || D == 128)) return EncKind::kStaged;
+  if ((IO == 0 || (PITCH_HS_IO16 && !KBIAS && (POLAR || D == 128))) && (POLAR ? PITCH_HS_POLAR : PITCH_HS_ENCODER) &&
+      (D == 64 || D == 128))
+    return EncKind::kStaged;
   if (IO == 0 && !KBIAS && PITCH_LT_ENCODER && D >= 256) return EncKind::kTransposed;
   if (!POLAR && use_lpv_encoder<D>()) return EncKind::kLanePerVector;
   return EncKind::kTeam;
@@ -2162,7 +2201,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
       using H = Hs<D, hs_team<D>()>;
       fill_hs_flips<D, hs_team<D>()>(a.seed, a.lane_flips);
       const uint64_t need = (a.count + H::WAVES * H::V - 1) / (H::WAVES * H::V);
-      const void* k = (const void*)&vec_encode_hs<D, B, POLAR, KBIAS>;
+      const void* k = (const void*)&vec_encode_hs<D, B, POLAR, KBIAS, IO>;
       const uint64_t grid = encode_grid(k, need, 64 * H::WAVES);
       const uint64_t rounds = KBIAS ? 0 : slice_rounds(0);
       if (rounds && need > grid * rounds) {
@@ -2171,16 +2210,16 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
         for (uint64_t v0 = 0; v0 < a.count; v0 += per) {
           VecArgs b = a;
           b.count = a.count - v0 < per ? a.count - v0 : per;
-          b.in = (const float*)a.in + v0 * D;
+          b.in = (const char*)a.in + v0 * D * Io<IO>::kBytes;
           b.codes_out = a.codes_out + v0 * NW;
           b.scales_out = a.scales_out + v0;
           const uint64_t nb = (b.count + H::WAVES * H::V - 1) / (H::WAVES * H::V);
-          hipLaunchKernelGGL((vec_encode_hs<D, B, POLAR, KBIAS>), dim3((uint32_t)(nb < grid ? nb : grid)),
+          hipLaunchKernelGGL((vec_encode_hs<D, B, POLAR, KBIAS, IO>), dim3((uint32_t)(nb < grid ? nb : grid)),
                              dim3(64 * H::WAVES), 0, s, b);
         }
         return hipGetLastError();
       }
-      hipLaunchKernelGGL((vec_encode_hs<D, B, POLAR, KBIAS>), dim3((uint32_t)grid), dim3(64 * H::WAVES), 0, s, a);
+      hipLaunchKernelGGL((vec_encode_hs<D, B, POLAR, KBIAS, IO>), dim3((uint32_t)grid), dim3(64 * H::WAVES), 0, s, a);
       return hipGetLastError();
     }
   }
@@ -2304,10 +2343,10 @@ hipError_t launch_batch(VecBatchArgs a, hipStream_t s) {
   constexpr EncKind k = enc_kind<D, POLAR, PITCH_IO, false>();
   constexpr uint64_t vpb = enc_vectors_per_block<D, POLAR, PITCH_IO>();
   if constexpr (k == EncKind::kStaged) {
-    const void* kp = (const void*)&vec_encode_hs_batch<D, B, POLAR>;
+    const void* kp = (const void*)&vec_encode_hs_batch<D, B, POLAR, PITCH_IO>;
     const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) { return encode_grid(kp, t, kBlock); }));
     fill_hs_flips<D, hs_team<D>()>(a.common.seed, a.common.lane_flips);
-    hipLaunchKernelGGL((vec_encode_hs_batch<D, B, POLAR>), grid, dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((vec_encode_hs_batch<D, B, POLAR, PITCH_IO>), grid, dim3(kBlock), 0, s, a);
   } else if constexpr (k == EncKind::kTransposed) {
     const void* kp = (const void*)&vec_encode_lt_batch<D, B, POLAR>;
     const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) { return persistent_grid(kp, t); }));

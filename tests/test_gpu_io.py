@@ -74,6 +74,32 @@ def test_per_vector_encode_16bit(q, method, d, bits, io):
 
 
 @pytest.mark.parametrize("io", IO_DTYPES)
+@pytest.mark.parametrize("method,d,bits,n", [("polarQuant", 64, 3, 777), ("polarQuant", 64, 5, 1000),
+                                             ("turboQuant", 128, 3, 1000), ("polarQuant", 128, 5, 777),
+                                             ("polarQuant", 128, 5, (1 << 21) + 45), ("turboQuant", 128, 3, (1 << 21) + 45)])
+def test_staged_encoder_16bit_odd_bits_and_long_calls(q, method, d, bits, n, io):
+    """16-bit vectors through the staged-stage encoder (PolarQuant at d = 64 / 128, TurboQuant at d = 128): odd bit
+    widths (code words shared between lanes at d = 64) and calls of more than 32 resident rounds (the grid of about
+    8 blocks per workgroup) give the bytes of the float32 encode of the widened values, which the float32 parity
+    tests pin against the oracle."""
+    import torch
+    import pitch_amd as P
+    print(f"staged 16-bit {io} {method} d={d} b={bits} n={n}", flush=True)
+    cfg = P.QuantConfig(method, d, bits)
+    x16 = _inputs(n, d, 31 * d + bits, q.device, io)
+    x32 = x16.float().contiguous()
+    c16 = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=q.device)
+    s16 = torch.empty(n, dtype=torch.float32, device=q.device)
+    c32, s32 = torch.empty_like(c16), torch.empty_like(s16)
+    q.enqueueEncode(x16, c16, s16, n, cfg)
+    q.enqueueEncode(x32, c32, s32, n, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(c16, c32) and torch.equal(s16.view(torch.int32), s32.view(torch.int32))
+    del x16, x32, c16, s16, c32, s32
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("io", IO_DTYPES)
 @pytest.mark.parametrize("method,d,bits", PER_VECTOR)
 def test_per_vector_decode_16bit(q, method, d, bits, io):
     import torch
