@@ -43,8 +43,8 @@ PEAK_GBPS = 8000.0
 METRIC = "codec GB/s (fp32 in/out + codes) and % of HBM peak; vectors/s at d=64/128"
 WARMUP_S = 0.25  # minimum warm-up per timed measurement, as the reference's benchmarks (BenchmarkSuite.swift:150-185)
 C5 = dict(layers=32, heads=8, tokens=131072, dim=128)
-HEADLINE_KERNEL = "pitch::vec_decode_stream<128, 3, false>"
-HEADLINE_PROFILE = "profiles/vec_decode_stream_d128_b3_config5.md"
+HEADLINE_KERNEL = "pitch::vec_decode<128, 3, false, 0, false>"
+HEADLINE_PROFILE = "profiles/vec_decode_d128_b3_config5.md"
 
 
 def code_stride(d: int, b: int) -> int:
@@ -219,11 +219,11 @@ class StreamCeiling:
             raise RuntimeError("pitch_calib_stream rejected its arguments")
 
     def measure_decoder(self, timer, src, dst, units: int, unit_bytes: int, in_words: int, dec_seg: int,
-                        dec_gbps: float, steps: int, warm: int) -> dict:
+                        dec_mode: int, dec_gbps: float, steps: int, warm: int) -> dict:
         """The decoders' mirror image (pitch_calib_stream_store): in_words words read (coalesced) and unit_bytes
         written per unit, in store pieces of 64-512 bytes, as one persistent launch, one launch of one block per
         workgroup, or launches of one round of 8 workgroups per CU (the config-5 decoders' shape); non-temporal or
-        cached stores. dec_seg: the decoder's store piece."""
+        cached stores. dec_seg, dec_mode: the decoder's store piece and grid (0, 1, 2 as above)."""
         if (dst.numel() * dst.element_size() < units * unit_bytes or src.numel() * src.element_size() < units * in_words * 4):
             raise ValueError("calibration buffers are smaller than the stream")
         nbytes = units * (unit_bytes + 4 * in_words)
@@ -243,11 +243,11 @@ class StreamCeiling:
                 for nt in (1, 0):
                     ms = timer.time(lambda i: call(seg, mode, nt), steps, warm)
                     rates[(seg, mode, nt)] = nbytes / ms / 1e6
-        shape = rates[(dec_seg, 2, 1)]
+        shape = rates[(dec_seg, dec_mode, 1)]
         best = max(rates, key=rates.get)
         return {"bytes_per_call": nbytes,
-                "decoder_shape": {"store_piece_bytes": dec_seg, "grid": "launches of one round, 8 workgroups per CU",
-                                  "nontemporal": True, "gbps": round(shape, 1)},
+                "decoder_shape": {"store_piece_bytes": dec_seg, "grid": names[dec_mode], "nontemporal": True,
+                                  "gbps": round(shape, 1)},
                 "best": {"store_piece_bytes": best[0], "grid": names[best[1]], "nontemporal": bool(best[2]),
                          "gbps": round(rates[best], 1), "pct_peak": round(rates[best] / PEAK_GBPS * 100, 1)},
                 "decoder_frac_of_decoder_shape": round(dec_gbps / shape, 3),
@@ -349,8 +349,9 @@ def run_config5_values(torch, q, P, O, W, timer, dev, args) -> tuple[dict, dict]
     gbps = nbytes / (ms * 1e-3) / 1e9
     print("# config 5 V: decoder-shaped stream calibration at the same footprint", file=sys.stderr, flush=True)
     src = torch.empty(n * ((cfg.codeStride + 4) // 4), dtype=torch.int32, device=dev)
-    # the streaming decoder's store instructions write 128 bytes of each vector (a team of 8 lanes x 16 bytes)
-    dec_ceiling = StreamCeiling(torch).measure_decoder(timer, src, out, n, 4 * d, (cfg.codeStride + 4) // 4, 128,
+    # the decoder stages a wave's vectors in LDS and writes them whole (each store instruction 1 KB: two 512-byte
+    # vectors), one workgroup per block in one launch
+    dec_ceiling = StreamCeiling(torch).measure_decoder(timer, src, out, n, 4 * d, (cfg.codeStride + 4) // 4, 512, 1,
                                                        gbps, 3, 1)
     del src
     cpu = None if args.no_cpu else cpu_baseline_vector_decode(
@@ -467,7 +468,7 @@ def run_config5_keys(torch, q, P, O, W, timer, dev, args) -> dict:
     # 512 + 64 + 8 bytes per token at d = 128, b = 4, G = 64
     print("# config 5 K: decoder-shaped stream calibration at the same footprint", file=sys.stderr, flush=True)
     src = torch.empty(n * 18, dtype=torch.int32, device=dev)
-    res["decode_stream_ceiling"] = StreamCeiling(torch).measure_decoder(timer, src, out, n, 4 * d, 18, 256,
+    res["decode_stream_ceiling"] = StreamCeiling(torch).measure_decoder(timer, src, out, n, 4 * d, 18, 256, 2,
                                                                         kb / ms / 1e6, 3, 1)
     del src
     if not args.no_cpu:

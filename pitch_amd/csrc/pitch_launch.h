@@ -12,7 +12,7 @@
 #define PITCH_SLICE_ROUNDS -1  // rounds per launch of every sliced call: -1 = each kernel's own default
 #endif
 #ifndef PITCH_STREAM_MIN_VECTORS
-#define PITCH_STREAM_MIN_VECTORS (1u << 22)  // smallest float32 D = 128 decode run by the streaming decoder
+#define PITCH_STREAM_MIN_VECTORS (1u << 19)  // smallest float32 D = 1024 decode run by the streaming decoder
 #endif
 #ifndef PITCH_BLOCKS_PER_CU
 #define PITCH_BLOCKS_PER_CU 0  // resident 256-thread blocks per CU of persistent grids: 0 = occupancy
@@ -162,7 +162,7 @@ uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size 
 // launches, or 0 for one launch: PITCH_SLICE_ROUNDS when it is 0 or more, else dflt.
 uint64_t slice_rounds(uint64_t dflt);
 
-// Smallest call (vectors) the float32 D = 128 decode issues through the streaming decoder (PITCH_STREAM_MIN_VECTORS).
+// Smallest call (vectors) the float32 D = 1024 decode issues through the streaming decoder (PITCH_STREAM_MIN_VECTORS).
 // Both decoders write the same bytes, so the threshold changes only the speed.
 uint64_t stream_decode_min_vectors();
 

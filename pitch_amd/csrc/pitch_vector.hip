@@ -879,6 +879,12 @@ __device__ __forceinline__ float dec_out(float y, float f, uint32_t sign) {
 #ifndef PITCH_DEC_WAVES
 #define PITCH_DEC_WAVES 1  // minimum waves per SIMD requested for the decoders (caps their VGPRs)
 #endif
+#ifndef PITCH_DEC_ONE_PER_WG_MIN
+#define PITCH_DEC_ONE_PER_WG_MIN (64ull << 20)  // float32 decodes writing [MIN, MAX) bytes: one workgroup per block
+#endif
+#ifndef PITCH_DEC_ONE_PER_WG_MAX
+#define PITCH_DEC_ONE_PER_WG_MAX (1ull << 62)
+#endif
 
 // The body of every per-vector decode: count vectors from codes_in / scales_in to out (p supplies the sign masks and
 // the key bias), with this workgroup block of nblocks striding over the call.
@@ -1142,14 +1148,15 @@ void fill_stream_flips(uint32_t seed, uint32_t* out) {
 }
 
 // ----------------------------------------------------------------------------------------------------
-// Streaming decoder for long float32 calls at D = 128 and 1024. At a footprint of many GB the persistent decoder
-// above runs at ~5.0 TB/s, while a write stream with the same 10 % of reads reaches ~6 TB/s when the GPU holds 8
-// workgroups per CU, each wave writes ~8 KB, and each launch gives every workgroup one block (so launches of ~2048
-// workgroups follow each other; within one long launch the workgroups drift apart and reads and writes interleave at
-// the memory). This kernel is shaped for that: 16 coordinates per lane (a team of 8 lanes per vector at D = 128, the
-// whole wave at D = 1024), two passes per wave (16 or 2 vectors), no output staging (a store instruction writes, for
-// each vector of a pass, the contiguous bytes its team holds: 128 bytes at D = 128, 1 KB at D = 1024), at most 64
-// VGPRs and a few KB of LDS; the host issues the call as launches of one block per workgroup.
+// Streaming decoder for long float32 calls at D = 1024 (the layout also serves D = 128, where vec_decode with one
+// workgroup per block is as fast or faster and is used instead). At a footprint of many GB a persistent decoder runs
+// at ~5.0 TB/s, while a write stream with the same 10 % of reads reaches ~6 TB/s when the GPU holds 8 workgroups per
+// CU, each wave writes ~8 KB, and each launch gives every workgroup one block (so launches of ~2048 workgroups follow
+// each other; within one long launch the workgroups drift apart and reads and writes interleave at the memory). This
+// kernel is shaped for that: 16 coordinates per lane (a team of 8 lanes per vector at D = 128, the whole wave at
+// D = 1024), two passes per wave (16 or 2 vectors), no output staging (a store instruction writes, for each vector
+// of a pass, the contiguous bytes its team holds: 128 bytes at D = 128, 1 KB at D = 1024), at most 64 VGPRs and a
+// few KB of LDS; the host issues the call as launches of one block per workgroup.
 #ifndef PITCH_STREAM_PASSES
 #define PITCH_STREAM_PASSES 2  // vectors per wave of the streaming decoder = passes x 8
 #endif
@@ -2253,9 +2260,12 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
     const uint64_t grid = persistent_grid(k, need);
     hipLaunchKernelGGL((vec_encode<D, B, POLAR, IO, KBIAS>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
   } else {
-    if constexpr ((D == 128 || D == 1024) && IO == 0 && !KBIAS) {
-      // the same output footprint at both sizes (2^22 vectors of d = 128, 2 GB, by default)
-      if (a.count >= stream_decode_min_vectors() * 128 / D) {
+    // float32 calls of at least 2^19 vectors at d = 1024 (2 GB of output): the streaming decoder. At d = 128 one
+    // workgroup per block of vec_decode (below) measured as fast as the streaming decoder at 2^25 vectors (config
+    // 5's value cache, 69.6-69.7 against 69.1-69.9 % of peak in interleaved repeats) and 2-7 points faster at
+    // 2^22-2^24 (b = 3, 4, 8 and PolarQuant; b = 2 within 0.5), so d = 128 runs it at every size.
+    if constexpr (D == 1024 && IO == 0 && !KBIAS) {
+      if (a.count >= stream_decode_min_vectors()) {
         using GS = Geom<D, kStreamE>;
         constexpr uint64_t kVpb = (uint64_t)GS::V * kStreamPasses * (kBlock / 64);  // vectors per workgroup
         const void* ks = (const void*)&vec_decode_stream<D, B, POLAR>;
@@ -2276,8 +2286,15 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
       }
     }
     const void* k = (const void*)&vec_decode<D, B, POLAR, IO, KBIAS>;
-    const uint64_t grid = persistent_grid(k, need, kBlock, true);
-    const uint64_t rounds = KBIAS ? 0 : slice_rounds(0);
+    // float32 calls writing 64 MB or more run one workgroup per block (the hardware hands the blocks out as
+    // workgroups finish) instead of a persistent grid. Interleaved repeats on one box, same bytes: config 4 (917,504
+    // vectors at d = 128, 470 MB) 74 -> 84-90 % of peak, d = 64 at 0.4-1.3 GB 75-83 -> 87-90 %, d = 128 at 1-1.5 GB
+    // 64-68 -> 72-73 %, d = 256 and 1024 +3-16 points, 67-200 MB +1-6 points; 100 MB at d = 64 equal.
+    const uint64_t out_bytes = a.count * D * 4;
+    const bool one_per_wg = IO == 0 && out_bytes >= PITCH_DEC_ONE_PER_WG_MIN && out_bytes < PITCH_DEC_ONE_PER_WG_MAX;
+    const uint64_t grid = one_per_wg ? (need < 0x7FFFFFFFull ? need : 0x7FFFFFFFull)
+                                     : persistent_grid(k, need, kBlock, true);
+    const uint64_t rounds = (KBIAS || one_per_wg) ? 0 : slice_rounds(0);
     if (rounds && need > grid * rounds) {
       constexpr int NW = (D * B + 31) / 32;
       const uint64_t per = grid * rounds * G::VPB;  // vectors per launch
