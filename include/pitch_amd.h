@@ -151,7 +151,8 @@ typedef struct pitch_decode_item {
 } pitch_decode_item_t;
 
 /* Decodes n_items independent segments with one configuration and output element type io_type (PITCH_IO_*) in as
- * few launches as it can (one per 32 segments), writing the same bytes as one pitch_enqueue_decode_io per segment.
+ * few launches as it can (one per 32 segments of fewer than 2^18 vectors; a longer segment gets the launch of a
+ * single call), writing the same bytes as one pitch_enqueue_decode_io per segment.
  * Every segment is validated as that call validates it, before anything is launched. For a model's per-layer
  * decodes (README.md:65-76 decodes each layer's cache with its own PITCH.enqueueDecode, Sources/PITCH/PITCH.swift:
  * 156-165): a layer of one decode step is a few tens of thousands of vectors, too few to fill the GPU alone, and

@@ -2,9 +2,9 @@
 
 A batch must write exactly what one enqueueDecode per segment writes, byte for byte, for both methods, every output
 element type and a spread of dimensions and bit widths, with ragged segment lengths, segments in separate buffers
-and at byte offsets, more segments than one launch takes (32), a segment long enough to loop over its rounds, and a
-float32 segment of d = 128 long enough that its single call runs the streaming decoder. A batch with one invalid
-segment launches nothing. The single-call decoders are pinned against the oracle elsewhere (test_gpu_parity.py);
+and at byte offsets, more segments than one launch takes (32), segments on either side of the length from which a
+segment gets a launch of its own (2^18 vectors), mixed with short ones, and a float32 d = 1024 segment long enough
+that its single call runs the streaming decoder. A batch with one invalid segment launches nothing. The single-call decoders are pinned against the oracle elsewhere (test_gpu_parity.py);
 one case here also checks the batch against the oracle's decode directly (pitch_reference.py:104-107, 123-129).
 """
 import numpy as np
@@ -88,12 +88,14 @@ def test_decode_batch_against_oracle(q):
 
 
 def test_decode_batch_long_segments(q):
-    """A segment longer than 1024 workgroups' rounds loops over its rounds; a float32 d = 128 segment of 2^22 + 17
-    vectors (whose single call runs the streaming decoder) decodes to the same bytes in the batch."""
+    """Segments just below and at 2^18 vectors (the batched kernel, and a launch of their own) between short ones; a
+    float32 d = 1024 segment of 2^19 + 17 vectors (whose single call runs the streaming decoder) and a d = 128 one of
+    2^22 + 17 decode to the same bytes in the batch."""
     import torch
     import pitch_amd as P
     dev = q.device
-    for d, bits, counts in ((2, 4, [300_000 + 77, 5]), (128, 3, [(1 << 22) + 17, 100])):
+    for d, bits, counts in ((2, 4, [(1 << 18) - 1, 5, 1 << 18, 77]), (64, 3, [9, (1 << 18) + 3, (1 << 18) - 2]),
+                            (1024, 3, [(1 << 19) + 17, 100]), (128, 3, [(1 << 22) + 17, 100])):
         print(f"decode batch long segments d={d} {counts}", flush=True)
         cfg = P.QuantConfig("turboQuant", d, bits)
         segs = _segments(torch, dev, d, counts, torch.float32, 9 + d, cfg)
