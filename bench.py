@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X KV-cache codec. Headline: BASELINE config 5, the largest single-GPU configuration.
 
-    python bench.py [--steps K] [--warmup W] [--extras] [--full] [--no-cpu] [--copy-calib]
+    python bench.py [--steps K] [--warmup W] [--extras] [--full] [--sweep CSV] [--no-cpu] [--copy-calib]
 
 A step is one full-cache decode of the Llama-3-8B long-context value cache of config 5: 32 layers x 8 KV heads x
 131072 tokens x d = 128 = 33,554,432 vectors (2^32 floats), TurboQuant b = 3, Student-t (nu = 5) values, in ONE
@@ -24,7 +24,9 @@ lists each row's % of peak beside the 70 % target (--no-rows skips them).
 
 --extras adds BASELINE config 1, the encoder-shaped stream ceilings and CPU baselines of configs 2-4, single-call
 latency percentiles, float16/bfloat16 caches, decode-step attention over compressed caches and key-bias removal;
---full adds the d = 1024 TurboQuant sweep of config 5.
+--full adds the d = 1024 TurboQuant sweep of config 5; --sweep CSV runs the reference's per-call throughput sweep
+(both methods, b = 2 / 4 / 8, d = 64 ... 1024, batches of 1 ... 4096 vectors, the GPU-resident and the array API) and
+writes it with the reference's results/throughput.csv columns.
 """
 from __future__ import annotations
 
@@ -503,6 +505,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-keys", action="store_true", help="skip the config-5 key cache")
     ap.add_argument("--no-rows", action="store_true", help="skip configs 2-4 (the target's d = 64 / 128 rows)")
+    ap.add_argument("--sweep", metavar="CSV", help="also run the reference's throughput sweep, writing CSV")
     ap.add_argument("--copy-calib", action="store_true", help="also run a plain 1 GiB device copy (PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -535,6 +538,8 @@ def main() -> int:
         extra.update(run_extras(torch, q, P, O, W, timer, dev, args))
     if args.full:
         extra.update(run_full(torch, q, P, timer, dev))
+    if args.sweep:
+        extra.update(run_sweep(torch, q, P, timer, dev, args.sweep))
     result["extra"] = extra
     if args.copy_calib:
         a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
@@ -801,6 +806,90 @@ def target_summary(rows: dict, head: dict, extra: dict) -> dict:
     return {"target_pct": 70.0, "pct_of_peak": pcts, "rows": len(pcts), "rows_at_or_above": len(pcts) - len(below),
             "below": below, "min_pct": min(pcts.values())}
 
+
+
+# ------------------------------------------------------------------------------------------- --sweep
+SWEEP_COLUMNS = ("method,bits,dim,batch,phase,api,gpu_us_median,gpu_us_p10,gpu_us_p90,wall_us_median,wall_us_p10,"
+                 "wall_us_p90,sustained_gpu_us_per_call,sustained_wall_us_per_call,ns_per_vector_sustained_gpu,"
+                 "input_gb_per_s_sustained_gpu")
+
+
+def run_sweep(torch, q, P, timer, dev, path: str) -> dict:
+    """The reference's throughput sweep (BenchmarkSuite.swift:100-141; its results/throughput.csv has the same
+    columns): both methods, b in {2, 4, 8}, d in {64 .. 1024}, batch in {1, 16, 256, 4096}; for each, the GPU-resident
+    calls (enqueueEncode / enqueueDecode on device buffers) timed one at a time (100 calls: GPU time by HIP events
+    around the call, wall time around launch + synchronisation; median, p10, p90) and back to back (16 calls between
+    two events, 20 times: the median per call; the reference's sustained dispatches), and the array API (encode of a
+    host array, decode of a CompressedBatch to a host array: host copies and the wait included; 30 calls, wall
+    time). Input GB/s counts the fp32 input bytes, as the reference's does. Writes the CSV to `path`."""
+    import numpy as np
+    rows = [SWEEP_COLUMNS]
+    g = lambda v: f"{v:.6g}"
+    pct = lambda v, p: float(np.sort(v)[min(len(v) - 1, int(round((len(v) - 1) * p)))])
+
+    def sustained(fn):
+        # after single_calls' warm-up: 20 times 16 back-to-back calls between two HIP events on the codec's stream
+        per = []
+        for _ in range(20):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(timer.stream)
+            for _ in range(16):
+                fn()
+            b.record(timer.stream)
+            b.synchronize()
+            per.append(a.elapsed_time(b) * 1e-3 / 16)
+        wall = []
+        for _ in range(20):
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            for _ in range(16):
+                fn()
+            torch.cuda.synchronize()
+            wall.append((time.perf_counter() - w0) / 16)
+        return float(np.median(per)), float(np.median(wall))
+
+    def wall_calls(fn, n=30):
+        for _ in range(3):
+            fn()
+        out = []
+        for _ in range(n):
+            w0 = time.perf_counter()
+            fn()
+            out.append(time.perf_counter() - w0)
+        return out
+
+    for dim in (64, 128, 256, 512, 1024):
+        for batch in (1, 16, 256, 4096):
+            x = np.random.default_rng(7).standard_normal((batch, dim)).astype(np.float32)
+            xd = torch.from_numpy(x).to(dev)
+            out = torch.empty_like(xd)
+            nbytes = batch * dim * 4
+            for method in ("turboQuant", "polarQuant"):
+                for bits in (2, 4, 8):
+                    cfg = P.QuantConfig(method, dim, bits)
+                    codes = torch.empty(batch * cfg.codeStride, dtype=torch.uint8, device=dev)
+                    scales = torch.empty(batch, device=dev)
+                    enc = lambda: q.enqueueEncode(xd, codes, scales, batch, cfg)  # noqa: E731
+                    dec = lambda: q.enqueueDecode(codes, scales, out, batch, cfg)  # noqa: E731
+                    for phase, fn in (("encode", enc), ("decode", dec)):
+                        single = timer.single_calls(lambda i: fn())
+                        s_gpu, s_wall = sustained(fn)
+                        rows.append(",".join([method, str(bits), str(dim), str(batch), phase, "gpu_resident",
+                                              g(single["gpu_us"]["median"]), g(single["gpu_us"]["p10"]),
+                                              g(single["gpu_us"]["p90"]), g(single["wall_us"]["median"]),
+                                              g(single["wall_us"]["p10"]), g(single["wall_us"]["p90"]),
+                                              g(s_gpu * 1e6), g(s_wall * 1e6), g(s_gpu * 1e9 / batch),
+                                              g(nbytes / s_gpu / 1e9)]))
+                    compressed = q.encode(x.reshape(-1), config=cfg)
+                    for phase, fn in (("encode", lambda: q.encode(x.reshape(-1), config=cfg)),
+                                      ("decode", lambda: q.decode(compressed))):
+                        w = np.asarray(wall_calls(fn)) * 1e6
+                        rows.append(",".join([method, str(bits), str(dim), str(batch), phase, "array", "", "", "",
+                                              g(pct(w, 0.5)), g(pct(w, 0.1)), g(pct(w, 0.9)), "", "", "", ""]))
+            print(f"# sweep d={dim} batch={batch} done", file=sys.stderr, flush=True)
+    Path(path).write_text("\n".join(rows) + "\n")
+    return {"throughput_sweep": {"csv": path, "rows": len(rows) - 1}}
 
 
 # ------------------------------------------------------------------------------------------- --extras
