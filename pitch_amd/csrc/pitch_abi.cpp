@@ -580,6 +580,21 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
   return cus * kmin;
 }
 
+uint32_t lds_cap_bytes(const void* kernel, int per_cu) {
+  if (per_cu <= 0) return 0;
+  int dev = 0, cu_lds = 0, wg_lds = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cu_lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+      hipDeviceGetAttribute(&wg_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || cu_lds <= 0)
+    return 0;
+  hipFuncAttributes fa{};
+  if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return 0;
+  // more than 1 / (per_cu + 1) of the CU's LDS, in 512-byte allocation granules
+  const uint64_t total = ((uint64_t)cu_lds / (uint64_t)(per_cu + 1) / 512u + 1u) * 512u;
+  if ((uint64_t)fa.sharedSizeBytes >= total || total > (uint64_t)wg_lds) return 0;
+  return (uint32_t)(total - fa.sharedSizeBytes);
+}
+
 uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size) {
   // blocks per workgroup of long calls (PITCH_ENC_BLOCKS_PER_WG; 0 keeps every call persistent) and the resident
   // rounds from which a call is oversubscribed (PITCH_ENC_MIN_ROUNDS): compile-time tuning macros

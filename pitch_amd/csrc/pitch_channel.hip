@@ -241,6 +241,24 @@ constexpr uint64_t kChanSliceRoundsDec = 1;
 // 23 % slower at config 3's, two repeats each).
 #define PITCH_KIVI_DEC_NTS 1
 #endif
+// Long float32 calls of the wave decoder and encoder run one launch of one work item per wave, with far more
+// workgroups than the CUs hold, and with fewer of them resident per CU than the kernels' registers allow: dynamic
+// LDS (lds_cap_bytes) holds the decoder at 4 and the encoder at 2 workgroups per CU. Config 5's keys (33.5M tokens,
+// d = 128, b = 4; interleaved repeats on one box, identical bytes): decode 5.40-5.43 TB/s in launches of one round
+// at the decoder's full 8 per CU; one launch at 3 / 4 / 5 / 6 per CU 5.35-5.41 / 5.81-5.83 / 5.64-5.67 / 5.37-5.39;
+// encode 5.51-5.52 at its full 4 per CU, 5.39-5.41 at 3, 5.70-5.74 at 2.
+#ifndef PITCH_KIVI_DEC_ONE_LAUNCH
+#define PITCH_KIVI_DEC_ONE_LAUNCH 1  // float32 decode calls of PITCH_KIVI_DEC_MIN_ROUNDS+ rounds: one launch
+#endif
+#ifndef PITCH_KIVI_DEC_MIN_ROUNDS
+#define PITCH_KIVI_DEC_MIN_ROUNDS 32  // resident rounds (at full occupancy) from which the one-launch decode runs
+#endif
+#ifndef PITCH_KIVI_DEC_WG_PER_CU
+#define PITCH_KIVI_DEC_WG_PER_CU 4  // resident decoder workgroups per CU in the one-launch mode (0: no cap)
+#endif
+#ifndef PITCH_KIVI_ENC_WG_PER_CU
+#define PITCH_KIVI_ENC_WG_PER_CU 2  // resident encoder workgroups per CU in the one-launch mode (0: no cap)
+#endif
 #ifndef PITCH_KIVI_ENC_ONE_LAUNCH
 #define PITCH_KIVI_ENC_ONE_LAUNCH 1  // float32 encode calls of 32+ resident rounds: one launch, one item per wave
 #endif
@@ -694,7 +712,8 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
         // float32 calls of 32+ resident rounds: one launch of one item per wave, far more workgroups than the CUs
         // hold (config-5 keys, 341 rounds: 5.52 TB/s against 5.41 for launches of two rounds, three repeats each)
         const uint64_t g = need < 0x7FFFFFFFull ? need : 0x7FFFFFFFull;
-        hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)g), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)g), dim3(kBlock),
+                           lds_cap_bytes(k, PITCH_KIVI_ENC_WG_PER_CU), s, a);
         return;
       }
       const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRoundsEnc);
@@ -742,6 +761,15 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       constexpr int SW = decltype(sw_c)::value;
       const uint64_t items = groups * ((a.dim + SW - 1) / SW);
       const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, SW, IO>, (items + 3) / 4);
+      if (IO == 0 && PITCH_KIVI_DEC_ONE_LAUNCH && (items + 3) / 4 >= PITCH_KIVI_DEC_MIN_ROUNDS * grid) {
+        // one launch of one item per wave at a capped residency (above); the kernel's grid-stride loop covers
+        // any items past 2^31 - 1 workgroups
+        const uint64_t need = (items + 3) / 4, g = need < 0x7FFFFFFFull ? need : 0x7FFFFFFFull;
+        const void* k = (const void*)&chan_decode_w<B, SW, IO>;
+        hipLaunchKernelGGL((chan_decode_w<B, SW, IO>), dim3((uint32_t)g), dim3(kBlock),
+                           lds_cap_bytes(k, PITCH_KIVI_DEC_WG_PER_CU), s, a);
+        return;
+      }
       const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRoundsDec);
       if (rounds && (items + 3) / 4 > grid * rounds && grid * rounds * 4 >= slabs) {
         const uint64_t gpl = grid * rounds * 4 / slabs;  // groups per launch

@@ -158,6 +158,11 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
 // lose from it (config 2, 8 rounds: -5 to -15 %), so they stay persistent.
 uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256);
 
+// Dynamic LDS bytes that hold a launch of `kernel` to at most per_cu resident workgroups per CU: enough LDS per
+// workgroup, with the kernel's own, that per_cu + 1 workgroups do not fit in a CU's LDS. 0 when per_cu is 0 or
+// less, when the kernel's own LDS already holds it there, or when the bytes needed exceed a workgroup's maximum.
+uint32_t lds_cap_bytes(const void* kernel, int per_cu);
+
 // Rounds (grid-stride iterations per workgroup) per launch when a call of more rounds is split into several
 // launches, or 0 for one launch: PITCH_SLICE_ROUNDS when it is 0 or more, else dflt.
 uint64_t slice_rounds(uint64_t dflt);

@@ -211,6 +211,38 @@ def test_kivi_long_call_one_launch_matches_per_head_calls(q):
     channel_full(q, heads, tokens, d, bits, G, 5202, one_call=True)
 
 
+@pytest.mark.parametrize("d,bits,n", [(128, 4, (1 << 23) + 37), (64, 3, (1 << 24) + 100)])
+def test_kivi_long_decode_one_launch_matches_slices(q, d, bits, n):
+    """Float32 KIVI decodes of at least 32 resident rounds (about 262,144 (group, 64-channel) items or more) run one
+    launch of one item per wave with a capped residency. The long call's output equals, byte for byte, the decode of
+    the same codes in slices of 2^20 tokens (launches of one round at full residency), the partial last group
+    included. Codes are random bytes and ranges random finite fp16 pairs, so every code value occurs."""
+    import torch
+    import pitch_amd as P
+    G = 64
+    dev = q.device
+    print(f"long KIVI decode d={d} b={bits} tokens={n}", flush=True)
+    cfg = P.ChannelQuantConfig(d, bits, G)
+    groups = cfg.groupCount(n)
+    g = torch.Generator(device=dev).manual_seed(5300 + d + bits)
+    codes = torch.randint(0, 256, (n * cfg.codeStride,), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    lo = torch.randn(groups, 1, d, generator=g, device=dev) * 3
+    hi = lo + torch.rand(groups, 1, d, generator=g, device=dev) * 4
+    ranges = torch.cat([lo, hi], 1).half().reshape(-1)
+    del lo, hi
+    out = torch.full((n, d), float("nan"), dtype=torch.float32, device=dev)
+    ref = torch.full((n, d), float("nan"), dtype=torch.float32, device=dev)
+    q.enqueuePerChannelDecode(codes, ranges, out, n, cfg)
+    per = 1 << 20
+    for t0 in range(0, n, per):
+        m = min(per, n - t0)
+        q.enqueuePerChannelDecode(codes, ranges, ref, m, cfg, codesOffset=t0 * cfg.codeStride,
+                                  rangesOffset=(t0 // G) * cfg.rangeStride, outputOffset=t0 * d * 4)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
+
+
 @pytest.mark.parametrize("bits", [2, 3, 8])
 def test_kivi_64_channel_slabs_bit_widths(q, bits):
     """One call of 2^21 + 192 tokens at d = 64: 32,771 (group, 64-channel) items, so the encoder takes its
