@@ -246,12 +246,16 @@ constexpr uint64_t kChanSliceRoundsDec = 1;
 // LDS (lds_cap_bytes) holds the decoder at 4 and the encoder at 2 workgroups per CU. Config 5's keys (33.5M tokens,
 // d = 128, b = 4; interleaved repeats on one box, identical bytes): decode 5.40-5.43 TB/s in launches of one round
 // at the decoder's full 8 per CU; one launch at 3 / 4 / 5 / 6 per CU 5.35-5.41 / 5.81-5.83 / 5.64-5.67 / 5.37-5.39;
-// encode 5.51-5.52 at its full 4 per CU, 5.39-5.41 at 3, 5.70-5.74 at 2.
+// encode 5.51-5.52 at its full 4 per CU, 5.39-5.41 at 3, 5.70-5.74 at 2. Shorter calls, d = 128, b = 4 (rounds
+// at full occupancy; two repeats, identical bytes): decode 1M tokens (8 rounds of 32-channel slabs) 6.06 -> 6.35-6.40,
+// 2M (8 rounds) 6.50 -> 6.38-6.43, 4M (16 rounds) 5.45-5.48 -> 6.04-6.11; encode 1M (11 rounds) 5.34-5.38 ->
+// 4.99-5.01, 2M (16 rounds) 5.63-5.67 -> 5.98-6.01, config 3 (8 x 32768 tokens at d = 64, 2-4 rounds) 5.25-5.34 ->
+// 4.24-4.29. Hence one launch from 8 rounds for the decoder and from 16 for the encoder.
 #ifndef PITCH_KIVI_DEC_ONE_LAUNCH
 #define PITCH_KIVI_DEC_ONE_LAUNCH 1  // float32 decode calls of PITCH_KIVI_DEC_MIN_ROUNDS+ rounds: one launch
 #endif
 #ifndef PITCH_KIVI_DEC_MIN_ROUNDS
-#define PITCH_KIVI_DEC_MIN_ROUNDS 32  // resident rounds (at full occupancy) from which the one-launch decode runs
+#define PITCH_KIVI_DEC_MIN_ROUNDS 8  // resident rounds (at full occupancy) from which the one-launch decode runs
 #endif
 #ifndef PITCH_KIVI_DEC_WG_PER_CU
 #define PITCH_KIVI_DEC_WG_PER_CU 4  // resident decoder workgroups per CU in the one-launch mode (0: no cap)
@@ -260,7 +264,10 @@ constexpr uint64_t kChanSliceRoundsDec = 1;
 #define PITCH_KIVI_ENC_WG_PER_CU 2  // resident encoder workgroups per CU in the one-launch mode (0: no cap)
 #endif
 #ifndef PITCH_KIVI_ENC_ONE_LAUNCH
-#define PITCH_KIVI_ENC_ONE_LAUNCH 1  // float32 encode calls of 32+ resident rounds: one launch, one item per wave
+#define PITCH_KIVI_ENC_ONE_LAUNCH 1  // float32 encode calls of PITCH_KIVI_ENC_MIN_ROUNDS+ rounds: one launch
+#endif
+#ifndef PITCH_KIVI_ENC_MIN_ROUNDS
+#define PITCH_KIVI_ENC_MIN_ROUNDS 16  // resident rounds (balanced grid) from which the one-launch encode runs
 #endif
 #ifndef PITCH_KIVI_NT
 #define PITCH_KIVI_NT 1  // the wave encoder reads keys with non-temporal loads
@@ -708,9 +715,9 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       // bound by their arithmetic and keep every resident wave
       const uint64_t grid = persistent_grid(k, (items + 3) / 4, kBlock, PITCH_KIVI_BALANCE && IO == 0);
       const uint64_t need = (items + 3) / 4;
-      if (PITCH_KIVI_ENC_ONE_LAUNCH && IO == 0 && need >= 32 * grid) {
-        // float32 calls of 32+ resident rounds: one launch of one item per wave, far more workgroups than the CUs
-        // hold (config-5 keys, 341 rounds: 5.52 TB/s against 5.41 for launches of two rounds, three repeats each)
+      if (PITCH_KIVI_ENC_ONE_LAUNCH && IO == 0 && need >= PITCH_KIVI_ENC_MIN_ROUNDS * grid) {
+        // long float32 calls: one launch of one item per wave, far more workgroups than the CUs hold (config-5 keys,
+        // 341 rounds: 5.52 TB/s against 5.41 for launches of two rounds, three repeats each, before the cap)
         const uint64_t g = need < 0x7FFFFFFFull ? need : 0x7FFFFFFFull;
         hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)g), dim3(kBlock),
                            lds_cap_bytes(k, PITCH_KIVI_ENC_WG_PER_CU), s, a);

@@ -182,8 +182,8 @@ def test_config5_k_share(q):
 
 
 def test_kivi_long_call_one_launch_matches_per_head_calls(q):
-    """Float32 KIVI encodes of at least 32 resident rounds run one launch of one item per wave: 32 heads x 131,072
-    tokens at d = 128 are 131,072 (group, 64-channel slab) items, 32,768 workgroups, past 32 rounds of 768 on a
+    """Float32 KIVI encodes of at least 16 resident rounds run one launch of one item per wave: 32 heads x 131,072
+    tokens at d = 128 are 131,072 (group, 64-channel slab) items, 32,768 workgroups, 32 rounds of 1,024 on a
     256-CU device. The long call's codes and ranges equal, byte for byte, those of one call per head (131,072 tokens
     each, a persistent grid), and sampled groups of a long call match the oracle (channel_full, one_call)."""
     import torch
@@ -213,9 +213,9 @@ def test_kivi_long_call_one_launch_matches_per_head_calls(q):
 
 @pytest.mark.parametrize("d,bits,n", [(128, 4, (1 << 23) + 37), (64, 3, (1 << 24) + 100)])
 def test_kivi_long_decode_one_launch_matches_slices(q, d, bits, n):
-    """Float32 KIVI decodes of at least 32 resident rounds (about 262,144 (group, 64-channel) items or more) run one
+    """Float32 KIVI decodes of at least 8 resident rounds (about 65,536 (group, 64-channel) items or more) run one
     launch of one item per wave with a capped residency. The long call's output equals, byte for byte, the decode of
-    the same codes in slices of 2^20 tokens (launches of one round at full residency), the partial last group
+    the same codes in slices of 2^18 tokens (2 rounds or fewer: one launch at full residency), the partial last group
     included. Codes are random bytes and ranges random finite fp16 pairs, so every code value occurs."""
     import torch
     import pitch_amd as P
@@ -233,7 +233,7 @@ def test_kivi_long_decode_one_launch_matches_slices(q, d, bits, n):
     out = torch.full((n, d), float("nan"), dtype=torch.float32, device=dev)
     ref = torch.full((n, d), float("nan"), dtype=torch.float32, device=dev)
     q.enqueuePerChannelDecode(codes, ranges, out, n, cfg)
-    per = 1 << 20
+    per = 1 << 18
     for t0 in range(0, n, per):
         m = min(per, n - t0)
         q.enqueuePerChannelDecode(codes, ranges, ref, m, cfg, codesOffset=t0 * cfg.codeStride,
