@@ -885,6 +885,19 @@ __device__ __forceinline__ float dec_out(float y, float f, uint32_t sign) {
 #ifndef PITCH_DEC_ONE_PER_WG_MAX
 #define PITCH_DEC_ONE_PER_WG_MAX (1ull << 62)
 #endif
+// Streaming decodes of codes up to PITCH_STREAM_CAP_BITS wide run one launch of every block, held at
+// PITCH_STREAM_WG_PER_CU resident workgroups per CU by dynamic LDS; wider codes run launches of one round at the
+// kernel's full 8 per CU. d = 1024, 2^19 / 2^21 vectors, % of peak in interleaved repeats (identical bytes), rounds
+// -> one launch at 5 per CU: TurboQuant b = 2 66 / 66 -> 72 / 75, b = 3 68 / 65 -> 79 / 74, b = 4 70 / 69 -> 79 / 77,
+// b = 5 70 / 69.5 -> 75 / 69.5, b = 6 70 / 68 -> 76 / 71.5, b = 8 73 / 73.5 -> 69 / 67.5; PolarQuant b = 3 68.5 / 66
+// -> 81 / 74, b = 4 70 / 69.5 -> 80.5 / 77, b = 6 69 / 66.5 -> 73 / 72. One launch at 3, 4, 6, 7 and 8 per CU was
+// slower than at 5 for most widths (b = 8 at 4 per CU: 76 / 72.5).
+#ifndef PITCH_STREAM_WG_PER_CU
+#define PITCH_STREAM_WG_PER_CU 5
+#endif
+#ifndef PITCH_STREAM_CAP_BITS
+#define PITCH_STREAM_CAP_BITS 6
+#endif
 
 // The body of every per-vector decode: count vectors from codes_in / scales_in to out (p supplies the sign masks and
 // the key bias), with this workgroup block of nblocks striding over the call.
@@ -2270,8 +2283,11 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
         constexpr uint64_t kVpb = (uint64_t)GS::V * kStreamPasses * (kBlock / 64);  // vectors per workgroup
         const void* ks = (const void*)&vec_decode_stream<D, B, POLAR>;
         const uint64_t blocks = (a.count + kVpb - 1) / kVpb;
-        // one block per resident workgroup per launch (1.5x, 2x, 3x and 4x as many measured 3-6 % slower)
-        const uint64_t grid = persistent_grid(ks, blocks);
+        // capped one-launch grid (above), else one block per resident workgroup per launch (1.5x, 2x, 3x and 4x as
+        // many measured 3-6 % slower)
+        constexpr int kCap = B <= PITCH_STREAM_CAP_BITS ? PITCH_STREAM_WG_PER_CU : 0;
+        const uint64_t grid = kCap > 0 ? blocks : persistent_grid(ks, blocks);
+        const uint32_t lds = lds_cap_bytes(ks, kCap);
         VecArgs b = a;
         fill_stream_flips<D>(a.seed, b.lane_flips);
         for (uint64_t b0 = 0; b0 < blocks; b0 += grid) {
@@ -2280,7 +2296,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
           b.codes_in = a.codes_in + v0 * ((D * B + 31) / 32);
           b.scales_in = a.scales_in + v0;
           b.out = (float*)a.out + v0 * D;
-          hipLaunchKernelGGL((vec_decode_stream<D, B, POLAR>), dim3((uint32_t)nb), dim3(kBlock), 0, s, b);
+          hipLaunchKernelGGL((vec_decode_stream<D, B, POLAR>), dim3((uint32_t)nb), dim3(kBlock), lds, s, b);
         }
         return hipGetLastError();
       }

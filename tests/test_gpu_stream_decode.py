@@ -1,5 +1,6 @@
-"""GPU parity of the streaming decoder that long float32 calls at d = 128 and 1024 use (at least 2^22 vectors of
-d = 128 per call, or 2^19 of d = 1024: the same 2 GB of output).
+"""GPU parity of long float32 decodes: at d = 1024 the streaming decoder (calls of at least 2^19 vectors; one launch
+held at 5 workgroups per CU for codes of up to 6 bits, launches of one round for 7 and 8), at d = 128 `vec_decode`
+with one workgroup per block (2^22 vectors here: the same 2 GB of output).
 
 Codes are random bytes (at d = 128 and 1024 every bit width packs into whole words, so any byte pattern is a valid
 code stream) with random positive scales. One call of the threshold + 4099 vectors (a ragged last launch) per
