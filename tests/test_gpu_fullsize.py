@@ -243,6 +243,46 @@ def test_kivi_long_decode_one_launch_matches_slices(q, d, bits, n):
     assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
 
 
+@pytest.mark.parametrize("bits", [4, 3])
+def test_kivi_long_encode_one_launch_partial_group(q, bits):
+    """A float32 KIVI encode of 16+ resident rounds (one launch at a capped residency) ending in a partial group:
+    2^22 + 37 tokens at d = 128 are 131,074 (group, 64-channel) items. Codes and ranges equal, byte for byte, those
+    of the same keys encoded in slices of 2^18 tokens (a few rounds, launches of two rounds or one), and the last
+    (37-token) group and the first one match the oracle bit for bit."""
+    import torch
+    import pitch_amd as P
+    from pitch_amd import workloads as W
+    d, G = 128, 64
+    n = (1 << 22) + 37
+    dev = q.device
+    print(f"long KIVI encode d={d} b={bits} tokens={n}", flush=True)
+    cfg = P.ChannelQuantConfig(d, bits, G)
+    groups = cfg.groupCount(n)
+    gk = torch.Generator(device=dev).manual_seed(5400 + bits)
+    x = W.biased_keys(torch, gk, dev, 1, n, d).reshape(n, d).contiguous()
+    c1 = torch.zeros(n * cfg.codeStride, dtype=torch.uint8, device=dev)
+    r1 = torch.full((groups * 2 * d,), float("nan"), dtype=torch.float16, device=dev)
+    c2 = torch.zeros_like(c1)
+    r2 = torch.full_like(r1, float("nan"))
+    q.enqueuePerChannelEncode(x, c1, r1, n, cfg)
+    per = 1 << 18
+    for t0 in range(0, n, per):
+        m = min(per, n - t0)
+        q.enqueuePerChannelEncode(x, c2, r2, m, cfg, inputOffset=t0 * d * 4, codesOffset=t0 * cfg.codeStride,
+                                  rangesOffset=(t0 // G) * cfg.rangeStride)
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2)
+    assert torch.equal(r1.view(torch.int16), r2.view(torch.int16))
+    for g in (0, groups - 1):
+        t0 = g * G
+        m = min(G, n - t0)
+        ref_codes, ref_ranges = O.channel_encode(x[t0:t0 + m].cpu().numpy(), bits, G)
+        got = c1[t0 * cfg.codeStride:(t0 + m) * cfg.codeStride].cpu().numpy().tobytes()
+        assert got == O.pack_codes(ref_codes, bits), g
+        rr = r1.view(groups, 2, d)[g].cpu().numpy()
+        assert np.array_equal(rr.view(np.uint16), np.asarray(ref_ranges, np.float16).reshape(2, d).view(np.uint16)), g
+
+
 @pytest.mark.parametrize("bits", [2, 3, 8])
 def test_kivi_64_channel_slabs_bit_widths(q, bits):
     """One call of 2^21 + 192 tokens at d = 64: 32,771 (group, 64-channel) items, so the encoder takes its
