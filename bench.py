@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X KV-cache codec. Headline: BASELINE config 5, the largest single-GPU configuration.
 
-    python bench.py [--steps K] [--warmup W] [--extras] [--full] [--sweep CSV] [--no-cpu] [--copy-calib]
+    python bench.py [--steps K] [--warmup W] [--extras] [--full] [--sweep CSV] [--sweep-channel CSV] [--no-cpu]
+                    [--copy-calib]
 
 A step is one full-cache decode of the Llama-3-8B long-context value cache of config 5: 32 layers x 8 KV heads x
 131072 tokens x d = 128 = 33,554,432 vectors (2^32 floats), TurboQuant b = 3, Student-t (nu = 5) values, in ONE
@@ -26,7 +27,9 @@ lists each row's % of peak beside the 70 % target (--no-rows skips them).
 latency percentiles, float16/bfloat16 caches, decode-step attention over compressed caches and key-bias removal;
 --full adds the d = 1024 TurboQuant sweep of config 5; --sweep CSV runs the reference's per-call throughput sweep
 (both methods, b = 2 / 4 / 8, d = 64 ... 1024, batches of 1 ... 4096 vectors, the GPU-resident and the array API) and
-writes it with the reference's results/throughput.csv columns.
+writes it with the reference's results/throughput.csv columns; --sweep-channel CSV runs its per-channel sweep (KIVI
+and TurboQuant on the same keys, b = 2 / 4 / 8, d = 64 ... 1024, 64 / 256 / 4096 tokens) with the columns of its
+results/per_channel_throughput.csv.
 """
 from __future__ import annotations
 
@@ -506,6 +509,8 @@ def main() -> int:
     ap.add_argument("--no-keys", action="store_true", help="skip the config-5 key cache")
     ap.add_argument("--no-rows", action="store_true", help="skip configs 2-4 (the target's d = 64 / 128 rows)")
     ap.add_argument("--sweep", metavar="CSV", help="also run the reference's throughput sweep, writing CSV")
+    ap.add_argument("--sweep-channel", metavar="CSV",
+                    help="also run the reference's per-channel sweep (KIVI and TurboQuant), writing CSV")
     ap.add_argument("--copy-calib", action="store_true", help="also run a plain 1 GiB device copy (PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -540,6 +545,8 @@ def main() -> int:
         extra.update(run_full(torch, q, P, timer, dev))
     if args.sweep:
         extra.update(run_sweep(torch, q, P, timer, dev, args.sweep))
+    if args.sweep_channel:
+        extra.update(run_channel_sweep(torch, q, P, timer, dev, args.sweep_channel))
     result["extra"] = extra
     if args.copy_calib:
         a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
@@ -812,42 +819,59 @@ def target_summary(rows: dict, head: dict, extra: dict) -> dict:
 SWEEP_COLUMNS = ("method,bits,dim,batch,phase,api,gpu_us_median,gpu_us_p10,gpu_us_p90,wall_us_median,wall_us_p10,"
                  "wall_us_p90,sustained_gpu_us_per_call,sustained_wall_us_per_call,ns_per_vector_sustained_gpu,"
                  "input_gb_per_s_sustained_gpu")
+CHANNEL_SWEEP_COLUMNS = ("method,bits,dim,tokens,phase,gpu_us_median,wall_us_median,sustained_gpu_us_per_call,"
+                         "sustained_wall_us_per_call,ns_per_token_sustained_gpu")
+
+
+def sustained_calls(torch, timer, fn) -> tuple:
+    """The reference's sustained dispatches (16 calls encoded into one Metal command buffer, PerChannelBenchmark.swift
+    :108-117, BenchmarkSuite.swift:174-183): 16 calls captured once into a HIP graph and the graph replayed 20 times
+    between two HIP events (GPU time per call, median; the calls run back to back on the GPU as the command buffer's
+    dispatches do), and 20 times 16 calls launched from the host between device synchronisations (wall time per
+    call, median). Called after Timer.single_calls' warm-up. The enqueue entry points issue only kernel launches, so
+    they can be captured."""
+    import numpy as np
+    graph, stream = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(16):
+            fn()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    per = []
+    cur = torch.cuda.current_stream()
+    for _ in range(20):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(cur)
+        graph.replay()
+        b.record(cur)
+        b.synchronize()
+        per.append(a.elapsed_time(b) * 1e-3 / 16)
+    wall = []
+    for _ in range(20):
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        for _ in range(16):
+            fn()
+        torch.cuda.synchronize()
+        wall.append((time.perf_counter() - w0) / 16)
+    return float(np.median(per)), float(np.median(wall))
 
 
 def run_sweep(torch, q, P, timer, dev, path: str) -> dict:
     """The reference's throughput sweep (BenchmarkSuite.swift:100-141; its results/throughput.csv has the same
     columns): both methods, b in {2, 4, 8}, d in {64 .. 1024}, batch in {1, 16, 256, 4096}; for each, the GPU-resident
     calls (enqueueEncode / enqueueDecode on device buffers) timed one at a time (100 calls: GPU time by HIP events
-    around the call, wall time around launch + synchronisation; median, p10, p90) and back to back (16 calls between
-    two events, 20 times: the median per call; the reference's sustained dispatches), and the array API (encode of a
+    around the call, wall time around launch + synchronisation; median, p10, p90) and back to back (sustained_calls:
+    16 calls replayed as one HIP graph, as the reference's 16 dispatches in one command buffer, and 16 calls launched
+    from the host for the wall time; medians per call), and the array API (encode of a
     host array, decode of a CompressedBatch to a host array: host copies and the wait included; 30 calls, wall
     time). Input GB/s counts the fp32 input bytes, as the reference's does. Writes the CSV to `path`."""
     import numpy as np
     rows = [SWEEP_COLUMNS]
     g = lambda v: f"{v:.6g}"
     pct = lambda v, p: float(np.sort(v)[min(len(v) - 1, int(round((len(v) - 1) * p)))])
-
-    def sustained(fn):
-        # after single_calls' warm-up: 20 times 16 back-to-back calls between two HIP events on the codec's stream
-        per = []
-        for _ in range(20):
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(timer.stream)
-            for _ in range(16):
-                fn()
-            b.record(timer.stream)
-            b.synchronize()
-            per.append(a.elapsed_time(b) * 1e-3 / 16)
-        wall = []
-        for _ in range(20):
-            torch.cuda.synchronize()
-            w0 = time.perf_counter()
-            for _ in range(16):
-                fn()
-            torch.cuda.synchronize()
-            wall.append((time.perf_counter() - w0) / 16)
-        return float(np.median(per)), float(np.median(wall))
 
     def wall_calls(fn, n=30):
         for _ in range(3):
@@ -874,7 +898,7 @@ def run_sweep(torch, q, P, timer, dev, path: str) -> dict:
                     dec = lambda: q.enqueueDecode(codes, scales, out, batch, cfg)  # noqa: E731
                     for phase, fn in (("encode", enc), ("decode", dec)):
                         single = timer.single_calls(lambda i: fn())
-                        s_gpu, s_wall = sustained(fn)
+                        s_gpu, s_wall = sustained_calls(torch, timer, fn)
                         rows.append(",".join([method, str(bits), str(dim), str(batch), phase, "gpu_resident",
                                               g(single["gpu_us"]["median"]), g(single["gpu_us"]["p10"]),
                                               g(single["gpu_us"]["p90"]), g(single["wall_us"]["median"]),
@@ -890,6 +914,43 @@ def run_sweep(torch, q, P, timer, dev, path: str) -> dict:
             print(f"# sweep d={dim} batch={batch} done", file=sys.stderr, flush=True)
     Path(path).write_text("\n".join(rows) + "\n")
     return {"throughput_sweep": {"csv": path, "rows": len(rows) - 1}}
+
+
+def run_channel_sweep(torch, q, P, timer, dev, path: str) -> dict:
+    """The reference's per-channel sweep (PerChannelBenchmark.swift:24-79; its results/per_channel_throughput.csv has
+    the same columns): d in {64 .. 1024}, tokens in {64, 256, 4096}, b in {2, 4, 8}, N(0, 1) keys (seed 7); per shape
+    and width the per-channel (KIVI, G = 64) encode and decode and the TurboQuant encode and decode of the same keys,
+    each timed one call at a time (100 calls; GPU time by HIP events around the call, wall time around launch and
+    synchronisation; medians) and back to back (sustained_calls: the reference's 16 sustained dispatches as one
+    replayed HIP graph for GPU time, launched from the host for wall time; medians per call). Writes the CSV to
+    `path`."""
+    import numpy as np
+    rows = [CHANNEL_SWEEP_COLUMNS]
+    g = lambda v: f"{v:.6g}"  # noqa: E731
+    for dim in (64, 128, 256, 512, 1024):
+        for tokens in (64, 256, 4096):
+            x = torch.from_numpy(np.random.default_rng(7).standard_normal((tokens, dim)).astype(np.float32)).to(dev)
+            out = torch.empty_like(x)
+            for bits in (2, 4, 8):
+                cc = P.ChannelQuantConfig(dim, bits)
+                codes = torch.empty(tokens * cc.codeStride, dtype=torch.uint8, device=dev)
+                ranges = torch.empty(cc.groupCount(tokens) * cc.rangeStride // 2, dtype=torch.float16, device=dev)
+                tc = P.QuantConfig("turboQuant", dim, bits)
+                tcodes = torch.empty(tokens * tc.codeStride, dtype=torch.uint8, device=dev)
+                tnorms = torch.empty(tokens, device=dev)
+                calls = (("perChannel", "encode", lambda: q.enqueuePerChannelEncode(x, codes, ranges, tokens, cc)),
+                         ("perChannel", "decode", lambda: q.enqueuePerChannelDecode(codes, ranges, out, tokens, cc)),
+                         ("turboQuant", "encode", lambda: q.enqueueEncode(x, tcodes, tnorms, tokens, tc)),
+                         ("turboQuant", "decode", lambda: q.enqueueDecode(tcodes, tnorms, out, tokens, tc)))
+                for method, phase, fn in calls:
+                    single = timer.single_calls(lambda i: fn())
+                    s_gpu, s_wall = sustained_calls(torch, timer, fn)
+                    rows.append(",".join([method, str(bits), str(dim), str(tokens), phase,
+                                          g(single["gpu_us"]["median"]), g(single["wall_us"]["median"]),
+                                          g(s_gpu * 1e6), g(s_wall * 1e6), g(s_gpu * 1e9 / tokens)]))
+            print(f"# channel sweep d={dim} tokens={tokens} done", file=sys.stderr, flush=True)
+    Path(path).write_text("\n".join(rows) + "\n")
+    return {"per_channel_sweep": {"csv": path, "rows": len(rows) - 1}}
 
 
 # ------------------------------------------------------------------------------------------- --extras
