@@ -123,7 +123,9 @@ typedef struct pitch_encode_item {
 int pitch_enqueue_encode_batch(const pitch_config_t* config, uint32_t io_type, const pitch_encode_item_t* items,
                                uint32_t n_items, void* stream);
 
-/* Decodes count vectors into count * dim fp32 values.
+/* Decodes count vectors into count * dim fp32 values. A vector's decoded bytes do not depend on the call: any count,
+ * offset or batch that contains it writes the same bytes (every decode kernel runs the same arithmetic in the same
+ * order; only the grid differs with the call's size).
  * Replaces PITCH.enqueueDecode(codes:codesOffset:scales:scalesOffset:output:outputOffset:count:config:
  * commandBuffer:) (Sources/PITCH/PITCH.swift:156-165 -> Sources/PITCH/Core/Codec.swift:107-140). */
 int pitch_enqueue_decode(const pitch_config_t* config, const void* codes, uint64_t codes_bytes,
