@@ -582,17 +582,41 @@ uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_s
 
 uint32_t lds_cap_bytes(const void* kernel, int per_cu) {
   if (per_cu <= 0) return 0;
-  int dev = 0, cu_lds = 0, wg_lds = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cu_lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
-      hipDeviceGetAttribute(&wg_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || cu_lds <= 0)
-    return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  // cached per (device, kernel, cap): the attributes do not change while the process runs
+  struct Key {
+    int dev;
+    const void* kernel;
+    int per_cu;
+    bool operator==(const Key& o) const { return dev == o.dev && kernel == o.kernel && per_cu == o.per_cu; }
+  };
+  struct KeyHash {
+    size_t operator()(const Key& k) const {
+      return std::hash<const void*>()(k.kernel) ^ ((size_t)k.dev << 8) ^ ((size_t)k.per_cu << 16);
+    }
+  };
+  static std::mutex mu;
+  static std::unordered_map<Key, uint32_t, KeyHash> cache;
+  const Key key{dev, kernel, per_cu};
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  int cu_lds = 0, wg_lds = 0;
   hipFuncAttributes fa{};
-  if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return 0;
-  // more than 1 / (per_cu + 1) of the CU's LDS, in 512-byte allocation granules
-  const uint64_t total = ((uint64_t)cu_lds / (uint64_t)(per_cu + 1) / 512u + 1u) * 512u;
-  if ((uint64_t)fa.sharedSizeBytes >= total || total > (uint64_t)wg_lds) return 0;
-  return (uint32_t)(total - fa.sharedSizeBytes);
+  uint32_t bytes = 0;
+  if (hipDeviceGetAttribute(&cu_lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess &&
+      hipDeviceGetAttribute(&wg_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && cu_lds > 0 &&
+      hipFuncGetAttributes(&fa, kernel) == hipSuccess) {
+    // more than 1 / (per_cu + 1) of the CU's LDS, in 512-byte allocation granules
+    const uint64_t total = ((uint64_t)cu_lds / (uint64_t)(per_cu + 1) / 512u + 1u) * 512u;
+    if ((uint64_t)fa.sharedSizeBytes < total && total <= (uint64_t)wg_lds) bytes = (uint32_t)(total - fa.sharedSizeBytes);
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  cache[key] = bytes;
+  return bytes;
 }
 
 uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size) {
