@@ -211,6 +211,55 @@ __device__ __forceinline__ uint32_t sector_code(float c, float a, bool& ok) {
   return n & (uint32_t)(L - 1);
 }
 
+// sector_code's octant reflections as one LDS byte lookup: the first-octant count n (bits [0, NB)), |c| > |a| (bit
+// NB), a < 0 (bit NB + 1) and c < 0 (bit NB + 2) index a table of the codes the reflections give; entries of n above
+// the boundary count K are never read. The 16 - 64 byte table sits in 4 - 16 banks, so a wave's lookups never
+// conflict (lanes reading one dword are served by a broadcast).
+#ifndef PITCH_POLAR_OCT_TAB
+#define PITCH_POLAR_OCT_TAB 1  // PolarQuant's staged and transposed encoders take their angle codes from the table
+#endif
+template <int B>
+struct OctTab {
+  static constexpr int K = polar_sector_bounds<B>();
+  static constexpr int NB = K == 1 ? 1 : (K == 2 ? 2 : 3);
+  static constexpr int N = 1 << (NB + 3);
+};
+typedef __attribute__((address_space(3))) const uint8_t lds_u8_t;
+
+template <int B>
+__device__ __forceinline__ void octant_table_build(uint8_t* tab, int tid, int nthreads) {
+  using O = OctTab<B>;
+  constexpr uint32_t L = 1u << B;
+  for (int i = tid; i < O::N; i += nthreads) {
+    uint32_t n = (uint32_t)i & ((1u << O::NB) - 1u);
+    n = ((i >> O::NB) & 1) ? L / 4 - n : n;
+    n = ((i >> (O::NB + 1)) & 1) ? L / 2 - n : n;
+    n = ((i >> (O::NB + 2)) & 1) ? L - n : n;
+    tab[i] = (uint8_t)(n & (L - 1));
+  }
+}
+
+template <int B>
+__device__ __forceinline__ uint32_t sector_code_tab(float c, float a, bool& ok, lds_u8_t* tab) {
+  using O = OctTab<B>;
+  static_assert(B >= 2 && B <= 5 && O::K <= 4, "sector boundaries of the first octant");
+  const float ax = __builtin_fabsf(a), ay = __builtin_fabsf(c);
+  const float mx = __builtin_fmaxf(ax, ay), mn = __builtin_fminf(ax, ay);
+  const float gm = kSectorGuard * mx;
+  bool good = mx >= 1e-30f;
+  uint32_t n = 0;
+#pragma unroll
+  for (int j = 0; j < O::K; ++j) {
+    const float dj = __builtin_fmaf(mx, -pitch_sector_tan[B - 2][j], mn);
+    n += dj > 0.f ? 1u : 0u;
+    good = good && __builtin_fabsf(dj) > gm;
+  }
+  ok = ok && good;
+  const uint32_t idx = n | (ay > ax ? 1u << O::NB : 0u) | ((__float_as_uint(a) >> 31) << (O::NB + 1)) |
+                       ((__float_as_uint(c) >> 31) << (O::NB + 2));
+  return tab[idx];
+}
+
 // y / sqrt(D) rounded as the reference's division (pitch_reference.py:33).
 template <int D>
 __device__ __forceinline__ double div_sqrt_d(double y) {
@@ -1690,7 +1739,7 @@ __device__ __forceinline__ void put_code(uint32_t (&w)[NWL], int pos, uint32_t c
 }
 
 template <int D, int T, int B, int NWL>
-__device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w)[NWL]) {
+__device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w)[NWL], lds_u8_t* otab) {
   constexpr int E = D / T, NP = E / 2, L = 1 << B;
   constexpr bool kSectors = B <= 5;
   constexpr float kRg = polar_radius_guard<B>();
@@ -1716,7 +1765,8 @@ __device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w
     const uint32_t cr = guarded_code_shifted(__builtin_fmaf(rf, sr, 0.5f - kRg), kRg, ok);
     uint32_t ca;
     if constexpr (kSectors) {
-      ca = sector_code<B>(cf, af, ok);
+      if constexpr (PITCH_POLAR_OCT_TAB) ca = sector_code_tab<B>(cf, af, ok, otab);
+      else ca = sector_code<B>(cf, af, ok);
     } else {  // a pair at the origin gives a NaN angle (0 * 1/0), which fails the guard
       ca = guarded_code_shifted(angle_sectors<B>(cf, af) + (0.5f - kPolarGuard), kPolarGuard, ok) &
            (uint32_t)(L - 1);
@@ -1756,7 +1806,7 @@ __device__ __forceinline__ void hs_compute(const EncSeg& sg, const typename TqLu
   uint32_t w[NWL];
   float nrm;
   if constexpr (POLAR) {
-    nrm = hs_polar_codes<D, T, B, NWL>(x, w);
+    nrm = hs_polar_codes<D, T, B, NWL>(x, w, (lds_u8_t*)sq.tab);
   } else {
     // ||x||^2 = sum of squares after the team-bit stages / T (each stage doubles it exactly)
     double ss[4] = {0.0, 0.0, 0.0, 0.0};
@@ -1847,6 +1897,7 @@ __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64
   __shared__ __attribute__((aligned(16))) double s_x[H::WAVES][H::ROWS];
   __shared__ __attribute__((aligned(16))) typename Q::Smem s_q;  // (unused by PolarQuant)
   static_assert(sizeof(s_x) == hs_rows_bytes(D), "staging rows as the table copies assume");
+  static_assert(!POLAR || sizeof(s_q) >= (size_t)OctTab<B>::N, "the octant table fits the bucket table's space");
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const HsElem<IO>* in = (const HsElem<IO>*)sg.in;
@@ -1859,6 +1910,7 @@ __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64
   constexpr int PFD = hs_pfd<D, B, KBIAS>();
   static_assert(PFD == 1 || PFD == 2, "prefetch depth");
   if constexpr (!POLAR) Q::load(s_q, threadIdx.x, 64 * H::WAVES);
+  else if constexpr (B <= 5 && PITCH_POLAR_OCT_TAB) octant_table_build<B>((uint8_t*)s_q.tab, threadIdx.x, 64 * H::WAVES);
   const uint64_t* neg = (const uint64_t*)p.lane_flips;  // fill_hs_flips; kernel arguments, read as scalars
   __syncthreads();
   if (base >= sg.count) return;
@@ -2096,7 +2148,7 @@ __device__ __forceinline__ void lt_compute(const EncSeg& sg, const typename TqLu
   uint32_t w[B];
   float nrm;
   if constexpr (POLAR) {
-    nrm = hs_polar_codes<D, L::T, B, B>(x, w);
+    nrm = hs_polar_codes<D, L::T, B, B>(x, w, (lds_u8_t*)sq.tab);
   } else {
     // ||x||^2 = sum of squares after the staging stages / T (each stage doubles it exactly)
     double ss[4] = {0.0, 0.0, 0.0, 0.0};
@@ -2135,7 +2187,9 @@ __device__ __forceinline__ void lt_run(const VecArgs& p, const EncSeg sg, uint64
   const float* in = (const float*)sg.in;
   const uint64_t stride = nblocks * L::WAVES * L::V;
   uint64_t base = (block * L::WAVES + wave) * L::V;
+  static_assert(!POLAR || sizeof(s_q) >= (size_t)OctTab<B>::N, "the octant table fits the bucket table's space");
   if constexpr (!POLAR) Q::load(s_q, threadIdx.x, kBlock);
+  else if constexpr (B <= 5 && PITCH_POLAR_OCT_TAB) octant_table_build<B>((uint8_t*)s_q.tab, threadIdx.x, kBlock);
   const uint32_t* neg = p.lane_flips;  // fill_lt_flips; kernel arguments, read as scalars
   __syncthreads();
   if (base >= sg.count) return;
