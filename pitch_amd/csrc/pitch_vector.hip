@@ -934,6 +934,9 @@ __device__ __forceinline__ float dec_out(float y, float f, uint32_t sign) {
 #ifndef PITCH_DEC_ONE_PER_WG_MAX
 #define PITCH_DEC_ONE_PER_WG_MAX (1ull << 62)
 #endif
+#ifndef PITCH_DEC_WAVE_BASE
+#define PITCH_DEC_WAVE_BASE 1  // calls of at least one wave's vectors store from a wave-uniform base
+#endif
 // Streaming decodes of codes up to PITCH_STREAM_CAP_BITS wide run one launch of every block, held at
 // PITCH_STREAM_WG_PER_CU resident workgroups per CU by dynamic LDS; wider codes run launches of one round at the
 // kernel's full 8 per CU. d = 1024, 2^19 / 2^21 vectors, % of peak in interleaved repeats (identical bytes), rounds
@@ -1069,6 +1072,36 @@ __device__ __forceinline__ void vec_decode_run(const VecArgs& p, const uint32_t*
       const uint64_t wbase = b.wb;  // first vector of this wave
       constexpr int K = Io<IO>::kPerChunk;  // elements per 16-byte store
       static_assert((G::V * D) % (64 * K) == 0, "whole 16-byte stores per lane");
+      if constexpr (PITCH_DEC_WAVE_BASE && !KBIAS) {
+        // The wave's output is one contiguous run from its first vector: a wave-uniform base and the lane's 16-byte
+        // offsets. Fetch clamps the first vector to count - V, so the run lies inside the call except in a call of
+        // fewer than V vectors, whose chunks past the end are not stored.
+        const uint64_t wb_u = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(wbase >> 32)) << 32) |
+                              __builtin_amdgcn_readfirstlane((uint32_t)wbase);
+        const uint64_t left = count - wb_u;  // vectors of the call from the wave's first one on
+        char* wout = (char*)out + wb_u * (uint64_t)D * Io<IO>::kBytes;
+        // 16-byte chunk q = lane + 64 m of the wave's output: LDS row q / CPV at chunk q % CPV, written to byte 16 q;
+        // both are the lane's base plus a constant per m
+        constexpr int CPV = D / K;  // 16-byte chunks per vector
+        static_assert(CPV <= 64 ? 64 % CPV == 0 : CPV % 64 == 0, "chunks per vector divide or are divided by 64");
+        const float* lp = CPV <= 64 ? ws + (lane / CPV) * kVecStride + K * (lane % CPV) : ws + K * lane;
+        char* sp = wout + 16 * lane;
+#pragma unroll
+        for (int m = 0; m < G::V * D / K / 64; ++m) {
+          const int off = CPV <= 64 ? m * (64 / CPV) * kVecStride
+                                    : (m / (CPV / 64)) * kVecStride + 64 * K * (m % (CPV / 64));
+          const int vq = CPV <= 64 ? lane / CPV + m * (64 / CPV) : m / (CPV / 64);  // the chunk's vector
+          float o[K];
+#pragma unroll
+          for (int h = 0; h < K / 4; ++h) {
+            const float4 val = *(const float4*)(lp + off + 4 * h);
+            o[4 * h] = val.x; o[4 * h + 1] = val.y; o[4 * h + 2] = val.z; o[4 * h + 3] = val.w;
+          }
+          if ((uint64_t)vq < left) store_elems<IO, K>(sp + 1024 * m, 0, o, PITCH_NT_STORE);
+        }
+        __builtin_amdgcn_wave_barrier();
+        return;
+      }
 #pragma unroll
       for (int m = 0; m < G::V * D / K / 64; ++m) {
         const int q = lane + 64 * m;          // 16-byte chunk of the wave's output block
