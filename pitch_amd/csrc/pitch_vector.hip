@@ -552,29 +552,30 @@ struct TqLut8 {
     }
   }
 
-  // Codes of x[0..NX) packed into words as they are produced: code e at bits [e*B, e*B + B) of w. When B
-  // divides 32 each code is shifted in from the top of its word (v_alignbit), which also drops the raw
-  // value's bits above B; otherwise the code is masked and or-ed in.
+  // Codes of x[0..NX) packed into words as they are produced: code e at bits [e*B, e*B + B) of w. Each word
+  // is a shift register: v_alignbit(raw, w, s) shifts w down by s and brings the low s bits of raw in at the
+  // top (raw's bits above s are dropped), so a word ends up holding the last 32 bits shifted into it, the
+  // earliest at bit 0. A code that straddles two words is shifted into both: its low 32 - sh bits end the
+  // first, and all B bits go into the second, whose remaining codes push the low ones out again. When the
+  // codes end part-way into the last word, they sit in its top bits and one shift moves them down. One
+  // instruction per code, where masking and or-ing takes two.
   template <int QB, int NX, int NWORDS>
   __device__ static void codes_packed(const Smem& sm, const double (&x)[NX], double us, int lane,
                                       uint32_t (&w)[NWORDS]) {
-    if constexpr (32 % B == 0) {
+    static_assert(NWORDS * 32 >= NX * B, "room for every code");
 #pragma unroll
-      for (int i = 0; i < NWORDS; ++i) w[i] = 0u;
-      for_codes<QB>(sm, x, us, lane, [&](int e, uint32_t raw) {
-        const int wi = (e * B) >> 5;
+    for (int i = 0; i < NWORDS; ++i) w[i] = 0u;
+    for_codes<QB>(sm, x, us, lane, [&](int e, uint32_t raw) {
+      const int pos = e * B, wi = pos >> 5, sh = pos & 31;
+      if (sh + B > 32) {
+        w[wi] = __builtin_amdgcn_alignbit(raw, w[wi], 32 - sh);
+        w[wi + 1] = __builtin_amdgcn_alignbit(raw, w[wi + 1], B);
+      } else {
         w[wi] = __builtin_amdgcn_alignbit(raw, w[wi], B);
-      });
-    } else {
-#pragma unroll
-      for (int i = 0; i < NWORDS; ++i) w[i] = 0u;
-      for_codes<QB>(sm, x, us, lane, [&](int e, uint32_t raw) {
-        const uint32_t cd = raw & (uint32_t)(L - 1);
-        const int pos = e * B, wi = pos >> 5, sh = pos & 31;
-        w[wi] |= cd << sh;
-        if (sh + B > 32) w[wi + 1] |= cd >> (32 - sh);
-      });
-    }
+      }
+    });
+    constexpr int kRem = (NX * B) & 31;
+    if constexpr (kRem != 0) w[(NX * B) >> 5] >>= 32 - kRem;
   }
 };
 
