@@ -211,18 +211,25 @@ __device__ __forceinline__ uint32_t sector_code(float c, float a, bool& ok) {
   return n & (uint32_t)(L - 1);
 }
 
-// sector_code's octant reflections as one LDS byte lookup: the first-octant count n (bits [0, NB)), |c| > |a| (bit
-// NB), a < 0 (bit NB + 1) and c < 0 (bit NB + 2) index a table of the codes the reflections give; entries of n above
-// the boundary count K are never read. The 16 - 64 byte table sits in 4 - 16 banks, so a wave's lookups never
-// conflict (lanes reading one dword are served by a broadcast).
+// sector_code as one LDS byte lookup indexed by sign bits: bit 0 the sign of c, bit 1 the sign of a, bit 2 the
+// sign of |a| - |c| (set exactly when |c| > |a|: the difference of distinct floats is nonzero, of equal ones +0),
+// bits 3 .. K + 2 the signs of d_{K-1} .. d_0. Each bit is appended with one v_alignbit(idx, x, 31) =
+// (idx << 1) | (x >> 31). The table holds, for every index, the code the octant reflections give to the
+// first-octant count n = the number of clear d_j sign bits. An accepted pair has every |d_j| above the guard,
+// so no d_j is zero and a clear sign bit means d_j > 0. The guard is gm = fma(mx, 2e-6, 1e-36): for mx < 1e-36
+// it exceeds mx >= |d_j| and rejects the pair (the origin included); above, the products mx tan_j (tan_j >=
+// 0.098) are normal floats and d_j errs by under 2.4e-7 mx + 2^-149 (2^-150 for each subnormal rounding of mn
+// and of the fused result), a third of gm at most. The staged encoders take the float32 path only for vectors
+// whose largest radius is at least 1e-15, where a pair below 1e-30 has radius code 0 however its square rounds.
+// The 16 - 128 byte table sits in at most 32 banks, so a wave's lookups never conflict (lanes reading one dword
+// are served by a broadcast).
 #ifndef PITCH_POLAR_OCT_TAB
 #define PITCH_POLAR_OCT_TAB 1  // PolarQuant's staged and transposed encoders take their angle codes from the table
 #endif
 template <int B>
 struct OctTab {
   static constexpr int K = polar_sector_bounds<B>();
-  static constexpr int NB = K == 1 ? 1 : (K == 2 ? 2 : 3);
-  static constexpr int N = 1 << (NB + 3);
+  static constexpr int N = K <= 4 ? 1 << (K + 3) : 1;  // b > 5 takes no table
 };
 typedef __attribute__((address_space(3))) const uint8_t lds_u8_t;
 
@@ -231,10 +238,12 @@ __device__ __forceinline__ void octant_table_build(uint8_t* tab, int tid, int nt
   using O = OctTab<B>;
   constexpr uint32_t L = 1u << B;
   for (int i = tid; i < O::N; i += nthreads) {
-    uint32_t n = (uint32_t)i & ((1u << O::NB) - 1u);
-    n = ((i >> O::NB) & 1) ? L / 4 - n : n;
-    n = ((i >> (O::NB + 1)) & 1) ? L / 2 - n : n;
-    n = ((i >> (O::NB + 2)) & 1) ? L - n : n;
+    uint32_t n = 0;
+#pragma unroll
+    for (int j = 0; j < O::K; ++j) n += ((i >> (3 + j)) & 1) ? 0u : 1u;
+    n = ((i >> 2) & 1) ? L / 4 - n : n;
+    n = ((i >> 1) & 1) ? L / 2 - n : n;
+    n = (i & 1) ? L - n : n;
     tab[i] = (uint8_t)(n & (L - 1));
   }
 }
@@ -245,18 +254,19 @@ __device__ __forceinline__ uint32_t sector_code_tab(float c, float a, bool& ok, 
   static_assert(B >= 2 && B <= 5 && O::K <= 4, "sector boundaries of the first octant");
   const float ax = __builtin_fabsf(a), ay = __builtin_fabsf(c);
   const float mx = __builtin_fmaxf(ax, ay), mn = __builtin_fminf(ax, ay);
-  const float gm = kSectorGuard * mx;
-  bool good = mx >= 1e-30f;
-  uint32_t n = 0;
+  const float gm = __builtin_fmaf(mx, kSectorGuard, 1e-36f);
+  bool good = true;
+  uint32_t idx = 0;
 #pragma unroll
   for (int j = 0; j < O::K; ++j) {
     const float dj = __builtin_fmaf(mx, -pitch_sector_tan[B - 2][j], mn);
-    n += dj > 0.f ? 1u : 0u;
+    idx = j == 0 ? __float_as_uint(dj) >> 31 : __builtin_amdgcn_alignbit(idx, __float_as_uint(dj), 31);
     good = good && __builtin_fabsf(dj) > gm;
   }
   ok = ok && good;
-  const uint32_t idx = n | (ay > ax ? 1u << O::NB : 0u) | ((__float_as_uint(a) >> 31) << (O::NB + 1)) |
-                       ((__float_as_uint(c) >> 31) << (O::NB + 2));
+  idx = __builtin_amdgcn_alignbit(idx, __float_as_uint(ax - ay), 31);
+  idx = __builtin_amdgcn_alignbit(idx, __float_as_uint(a), 31);
+  idx = __builtin_amdgcn_alignbit(idx, __float_as_uint(c), 31);
   return tab[idx];
 }
 
@@ -1757,9 +1767,13 @@ __device__ __forceinline__ void hs_stage(const VecArgs& p, uint64_t count, const
 // unnormalised transform and only rmax is scaled. Each pair is decided in float32 on the unscaled pair (the
 // angle is scale-invariant; the radius is multiplied by (2^B - 1) / rmax): the radius behind
 // polar_radius_guard, the angle by sector_code at B <= 5 and by angle_sectors behind kPolarGuard above. A pair
-// that fails a guard, and every pair of a vector whose rmax lies outside [1e-30, 1e30] (where the unscaled
-// float32 pair could lose precision), is decided afterwards by the float64 path in the reference's order, in
-// one block per lane that the waves enter only when one of their lanes has such a pair.
+// that fails a guard, and every pair of a vector whose rmax lies outside [1e-15, 1e18], is decided afterwards by
+// the float64 path in the reference's order, in one block per lane that the waves enter only when one of their
+// lanes has such a pair. The range keeps the float32 squared radius a^2 + c^2 exact to its rounding: near a
+// radius boundary (r >= rmax / (2 (2^B - 1))) a subnormal square's absolute rounding error (2^-150 each) moves t
+// by at most (2^B - 1)^2 2^-149 / rmax^2, under 1e-10 for rmax >= 1e-15 (for rmax near 1e-25 the squares
+// underflow and every radius would read 0), and r <= rmax <= 1e18 keeps r^2 <= 1e36 below float32's largest
+// value.
 template <int B, int NWL>
 __device__ __forceinline__ void put_code(uint32_t (&w)[NWL], int pos, uint32_t cd, bool clear) {
   const int wi = pos >> 5, sh = pos & 31;
@@ -1784,7 +1798,7 @@ __device__ __forceinline__ float hs_polar_codes(double (&x)[D / T], uint32_t (&w
   m = team_reduce<T>(m, [](double a, double b) { return __builtin_fmax(a, b); });
   const double rmax = __builtin_sqrt(m);  // = the largest radius: sqrt is monotone
   const double safe = rmax > 0.0 ? rmax : 1.0;
-  const bool inrange = rmax > 1e-30 && rmax < 1e30;
+  const bool inrange = rmax >= 1e-15 && rmax <= 1e18;
   const float sr = (float)(double(L - 1) / safe);
 #pragma unroll
   for (int i = 0; i < NWL; ++i) w[i] = 0u;

@@ -346,6 +346,31 @@ def test_extreme_vectors_against_oracle(q, method, d, bits):
     assert np.all(np.isfinite(q.decode(ours)))
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_polar_magnitudes_against_oracle(q, d, bits):
+    """PolarQuant vectors scaled from 1e-29 up to the largest allowed magnitude (1e17, PITCH.swift:172-181), five
+    of each scale, in one call: codes equal the oracle's except at near-boundary coordinates, scales within one
+    ulp. The staged encoders (float32 input at d = 64 and 128; d >= 256) decide codes in float32 on the
+    unnormalised pairs, whose squared radius loses its precision below a largest radius of about 1e-18 (near
+    1e-25 it underflows to 0 and every radius would read code 0) and overflows above about 1.8e19; vectors
+    outside the fast path's range take the float64 path."""
+    import pitch_amd as P
+    rng = np.random.default_rng(31 * d + bits)
+    scales_in = np.repeat([1e-29, 1e-25, 1e-21, 1e-19, 1e-17, 1e-16, 1e-3, 1e15, 3e16], 5)
+    X = np.clip(rng.standard_normal((len(scales_in), d)) * scales_in[:, None], -1e17, 1e17).astype(np.float32)
+    n = len(X)
+    cfg = P.QuantConfig("polarQuant", d, bits, 0x5EED)
+    print(f"polar magnitudes d{d} b{bits}", flush=True)
+    ours = q.encode(X.reshape(-1), config=cfg)
+    codes, scales = O.polar_encode(X.astype(np.float64), bits, 0x5EED)
+    diff = O.unpack_codes(ours.codes, n, d, bits) != O.unpack_codes(O.pack_codes(codes, bits), n, d, bits)
+    band = band_mask("polarQuant", X, None, bits, 0x5EED)
+    bad = (diff & ~band).any(1)
+    assert not bad.any(), f"d{d} b{bits}: codes differ away from any boundary at scales {sorted(set(scales_in[bad]))}"
+    check_scales(ours.scales, np.asarray(scales, np.float32), "scales")
+
+
 # ----------------------------------------------------------------------------- per-channel
 @pytest.mark.parametrize("d", [64, 96, 128])
 def test_channel_error_within_half_a_step(q, d):
