@@ -507,18 +507,31 @@ struct TqLut8 {
     double edge64[kLut ? 1 : L];
   };
 
-  __device__ static void load(Smem& sm, int tid, int nthreads) {
+  // The table set-up of a workgroup of NT threads. Each thread's global loads go out together (the index is
+  // clamped instead of tested, so no load sits in a branch) and are waited for once.
+  template <int NT>
+  __device__ static void load(Smem& sm, int tid) {
     if constexpr (kLut) {
-      for (int i = tid; i < N * REP; i += nthreads) {
-        const int j = i / REP;
-        const float e = __uint_as_float(pitch_lut_tab[2 * (LI.offset + j)]);
-        const uint32_t c = pitch_lut_tab[2 * (LI.offset + j) + 1];
-        const uint64_t bits = __builtin_isinf(e) ? kTop : (uint64_t)__double_as_longlong(__builtin_fma((double)e, LI.scale, kMagic));
-        sm.tab[i] = bits | c;
+      constexpr int kIt = (N * REP + NT - 1) / NT;
+      uint32_t e_bits[kIt], c[kIt];
+#pragma unroll
+      for (int k = 0; k < kIt; ++k) {
+        const int j = min(tid + k * NT, N * REP - 1) / REP;
+        e_bits[k] = pitch_lut_tab[2 * (LI.offset + j)];
+        c[k] = pitch_lut_tab[2 * (LI.offset + j) + 1];
+      }
+#pragma unroll
+      for (int k = 0; k < kIt; ++k) {
+        const int i = tid + k * NT;
+        if (i < N * REP) {
+          const float e = __uint_as_float(e_bits[k]);
+          const uint64_t bits = __builtin_isinf(e) ? kTop : (uint64_t)__double_as_longlong(__builtin_fma((double)e, LI.scale, kMagic));
+          sm.tab[i] = bits | c[k];
+        }
       }
     } else {
       constexpr int off = pitch_codebook_offset(ilog2(D), B);
-      for (int i = tid; i < L; i += nthreads) sm.edge64[i] = (double)pitch_edge_tab[off + i];
+      for (int i = tid; i < L; i += NT) sm.edge64[i] = (double)pitch_edge_tab[off + i];
     }
   }
 
@@ -1954,21 +1967,23 @@ __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64
   // Software pipeline with PFD blocks of loads in flight. The loop is rotated so that each block's loads are
   // waited for in straight-line code after exactly the stores of the block before (two or so operations):
   // an iteration issues the loads of block k + PFD, computes and stores block k, then stages block k + 1.
-  // The waves' first loads are issued after the table set-up, so no other load is pending at that point.
+  // The waves' first loads go out before the table set-up, whose loads queue behind them: one load latency
+  // before the first block instead of the table's and then the block's.
   constexpr int PFD = hs_pfd<D, B, KBIAS>();
   static_assert(PFD == 1 || PFD == 2, "prefetch depth");
-  if constexpr (!POLAR) Q::load(s_q, threadIdx.x, 64 * H::WAVES);
+  HsChunk<IO> pfa[H::QPL];
+  HsChunk<IO> pfb[PFD > 1 ? H::QPL : 1];
+  // every fetch is unconditional, like the stores: a block past the end re-reads the last vector (a cache hit;
+  // every call has at least one vector), also in a wave that has no block and leaves after the barrier
+  hs_fetch<D, T, IO>(in, base, sg.count, lane, pfa);
+  if constexpr (PFD > 1) hs_fetch<D, T, IO>(in, base + stride, sg.count, lane, pfb);
+  if constexpr (!POLAR) Q::template load<64 * H::WAVES>(s_q, threadIdx.x);
   else if constexpr (B <= 5 && PITCH_POLAR_OCT_TAB) octant_table_build<B>((uint8_t*)s_q.tab, threadIdx.x, 64 * H::WAVES);
   const uint64_t* neg = (const uint64_t*)p.lane_flips;  // fill_hs_flips; kernel arguments, read as scalars
   __syncthreads();
   if (base >= sg.count) return;
   double* sx = s_x[wave];
-  HsChunk<IO> pfa[H::QPL];
-  HsChunk<IO> pfb[PFD > 1 ? H::QPL : 1];
   double x[E];
-  // every fetch is unconditional, like the stores: a block past the end re-reads the last vector (a cache hit)
-  hs_fetch<D, T, IO>(in, base, sg.count, lane, pfa);
-  if constexpr (PFD > 1) hs_fetch<D, T, IO>(in, base + stride, sg.count, lane, pfb);
   hs_stage<D, T, KBIAS, IO>(p, sg.count, pfa, base, lane, neg, sx, x);
   auto step = [&](HsChunk<IO> (&refill)[H::QPL], HsChunk<IO> (&next)[H::QPL]) {
     hs_fetch<D, T, IO>(in, base + (uint64_t)PFD * stride, sg.count, lane, refill);
@@ -2236,17 +2251,18 @@ __device__ __forceinline__ void lt_run(const VecArgs& p, const EncSeg sg, uint64
   const uint64_t stride = nblocks * L::WAVES * L::V;
   uint64_t base = (block * L::WAVES + wave) * L::V;
   static_assert(!POLAR || sizeof(s_q) >= (size_t)OctTab<B>::N, "the octant table fits the bucket table's space");
-  if constexpr (!POLAR) Q::load(s_q, threadIdx.x, kBlock);
+  // Software pipeline as in the staged-stage encoder: an iteration issues the loads of block k + 1, computes and
+  // stores block k, then stages block k + 1 (past the end: re-reads of the last vector, staged, never computed).
+  // The first block's loads go out before the table set-up, as there.
+  uint32_t pf[32];
+  lt_fetch<D>(in, base, sg.count, lane, pf);
+  if constexpr (!POLAR) Q::template load<kBlock>(s_q, threadIdx.x);
   else if constexpr (B <= 5 && PITCH_POLAR_OCT_TAB) octant_table_build<B>((uint8_t*)s_q.tab, threadIdx.x, kBlock);
   const uint32_t* neg = p.lane_flips;  // fill_lt_flips; kernel arguments, read as scalars
   __syncthreads();
   if (base >= sg.count) return;
   double* sx = s_x[wave];
-  uint32_t pf[32];
   double x[32];
-  // Software pipeline as in the staged-stage encoder: an iteration issues the loads of block k + 1, computes and
-  // stores block k, then stages block k + 1 (past the end: re-reads of the last vector, staged, never computed).
-  lt_fetch<D>(in, base, sg.count, lane, pf);
   lt_stage<D, POLAR>(neg, pf, lane, sx, x);
   while (base < sg.count) {
     lt_fetch<D>(in, base + stride, sg.count, lane, pf);
