@@ -1424,6 +1424,34 @@ __device__ __forceinline__ void chunk_floats(const u32x4& w, float (&f)[Io<IO>::
   }
 }
 
+#ifndef PITCH_ENC_FAIR
+#define PITCH_ENC_FAIR 1  // persistent encoders raise a wave's issue priority with its share of blocks still to do
+#endif
+// A SIMD issues from its oldest wave first. With a fixed share of blocks per wave, the first-dispatched workgroups
+// of a persistent encoder ran ahead and finished early, and the rest ended the call with fewer resident waves to
+// hide their latency (a config-2 encode: every wave started within 0.4 us and ended between 11 and 23 us). In a
+// persistent launch (on) each wave therefore sets its priority (s_setprio 0 .. 3) from the fraction of its blocks
+// still to do, so the waves behind are issued first and a SIMD's waves finish together. An oversubscribed launch,
+// where the hardware starts new workgroups as others finish, keeps the default priority (measured 1-1.5 % slower
+// with it). Both arguments are wave-uniform.
+struct FairPriority {
+  bool on;
+  uint32_t total, left;
+  __device__ FairPriority(bool on_, uint64_t blocks)
+      : on(on_), total(blocks < 1 ? 1u : (blocks > 0xFFFFFFu ? 0xFFFFFFu : (uint32_t)blocks)), left(total) {}
+  // before each block
+  __device__ __forceinline__ void next() {
+    if (PITCH_ENC_FAIR && on) {
+      const uint32_t level = __builtin_amdgcn_readfirstlane((left * 4u) / total);
+      if (level >= 3) __builtin_amdgcn_s_setprio(3);
+      else if (level == 2) __builtin_amdgcn_s_setprio(2);
+      else if (level == 1) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+      left = left > 0 ? left - 1 : 0;
+    }
+  }
+};
+
 template <int D, int B, int IO, bool KBIAS>
 __device__ __forceinline__ void lpv_run(const VecArgs& p, const EncSeg sg, uint64_t block, uint64_t nblocks) {
   using Lp = Lpv<D, IO>;
@@ -1456,7 +1484,9 @@ __device__ __forceinline__ void lpv_run(const VecArgs& p, const EncSeg sg, uint6
   for (int r = 0; r < K; ++r)
     smask[r] = sign_is_negative(p.seed, (uint32_t)(K * (lane % Lp::QPV) + r)) ? 0x80000000u : 0u;
   __syncthreads();
+  FairPriority fair(p.fair != 0, block * V < sg.count ? (sg.count - block * V + nblocks * V - 1) / (nblocks * V) : 0);
   for (uint64_t base = block * V; base < sg.count; base += nblocks * V) {
+    fair.next();
     // stage the wave's block of V vectors in LDS with coalesced loads
     {
 #if !PITCH_ENC_PREFETCH
@@ -1949,34 +1979,6 @@ constexpr int hs_waves() {
   return POLAR ? PITCH_HS_WAVES_POLAR : (KBIAS ? 2 : (D == 64 ? PITCH_HS_WAVES64 : PITCH_HS_WAVES128));
 }
 
-#ifndef PITCH_ENC_FAIR
-#define PITCH_ENC_FAIR 1  // persistent encoders raise a wave's issue priority with its share of blocks still to do
-#endif
-// A SIMD issues from its oldest wave first. With a fixed share of blocks per wave, the first-dispatched workgroups
-// of a persistent encoder ran ahead and finished early, and the rest ended the call with fewer resident waves to
-// hide their latency (a config-2 encode: every wave started within 0.4 us and ended between 11 and 23 us). In a
-// persistent launch (on) each wave therefore sets its priority (s_setprio 0 .. 3) from the fraction of its blocks
-// still to do, so the waves behind are issued first and a SIMD's waves finish together. An oversubscribed launch,
-// where the hardware starts new workgroups as others finish, keeps the default priority (measured 1-1.5 % slower
-// with it). Both arguments are wave-uniform.
-struct FairPriority {
-  bool on;
-  uint32_t total, left;
-  __device__ FairPriority(bool on_, uint64_t blocks)
-      : on(on_), total(blocks < 1 ? 1u : (blocks > 0xFFFFFFu ? 0xFFFFFFu : (uint32_t)blocks)), left(total) {}
-  // before each block
-  __device__ __forceinline__ void next() {
-    if (PITCH_ENC_FAIR && on) {
-      const uint32_t level = __builtin_amdgcn_readfirstlane((left * 4u) / total);
-      if (level >= 3) __builtin_amdgcn_s_setprio(3);
-      else if (level == 2) __builtin_amdgcn_s_setprio(2);
-      else if (level == 1) __builtin_amdgcn_s_setprio(1);
-      else __builtin_amdgcn_s_setprio(0);
-      left = left > 0 ? left - 1 : 0;
-    }
-  }
-};
-
 template <int D, int B, bool POLAR, bool KBIAS, int IO>
 __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64_t block, uint64_t nblocks) {
   constexpr int T = hs_team<D>();
@@ -2414,6 +2416,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
       const uint64_t need = (a.count + V - 1) / V;
       const void* k = (const void*)&tq_encode_lpv<D, B, IO, KBIAS>;
       const uint64_t grid = persistent_grid(k, need, 64);
+      a.fair = 1u;
       hipLaunchKernelGGL((tq_encode_lpv<D, B, IO, KBIAS>), dim3((uint32_t)grid), dim3(64), 0, s, a);
       return hipGetLastError();
     }
