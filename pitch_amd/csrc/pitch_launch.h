@@ -21,7 +21,10 @@
 #define PITCH_ENC_BLOCKS_PER_WG 8  // blocks per workgroup of long staged encodes: 0 = always persistent
 #endif
 #ifndef PITCH_ENC_MIN_ROUNDS
-#define PITCH_ENC_MIN_ROUNDS 32  // resident rounds from which a staged encode is oversubscribed
+// resident rounds from which a staged encode is oversubscribed. With the persistent launch's fair wave priority
+// the persistent grid won at 32 and 48 rounds (d = 64: +3 points) and the oversubscribed one from 64 rounds up
+// (d = 64 and 128: +1-5 points), equal at 56 (d = 128)
+#define PITCH_ENC_MIN_ROUNDS 56
 #endif
 
 namespace pitch {

@@ -118,11 +118,11 @@ def test_config5_v_share(q):
 @pytest.mark.parametrize("method,d,bits", [("polarQuant", 128, 4), ("turboQuant", 64, 4), ("polarQuant", 64, 3),
                                            ("turboQuant", 64, 3)])
 def test_long_calls_oversubscribed_grid(q, method, d, bits):
-    """The staged encoder runs calls of at least 32 resident rounds as one launch of about 8 blocks per workgroup
-    (encode_grid): 2^21 vectors are 32,768 blocks of 64, past 32 rounds of 768 resident workgroups on a 256-CU
+    """The staged encoder runs calls of at least 56 resident rounds as one launch of about 8 blocks per workgroup
+    (encode_grid): 3 * 2^20 vectors are 49,152 blocks of 64, 64 rounds of 768 resident workgroups on a 256-CU
     device. Sampled rows match the oracle, and the slice per_vector_full encodes through byte offsets (100,003
     vectors, a persistent grid) gives the same bytes as the long call."""
-    per_vector_full(q, method, 1 << 21, d, bits, 7000 + d + bits, "t5")
+    per_vector_full(q, method, 3 << 20, d, bits, 7000 + d + bits, "t5")
 
 
 def test_more_than_2_32_floats_in_one_call(q):
