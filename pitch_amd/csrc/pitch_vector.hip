@@ -2532,17 +2532,25 @@ hipError_t launch_batch(VecBatchArgs a, hipStream_t s) {
   constexpr uint64_t vpb = enc_vectors_per_block<D, POLAR, PITCH_IO>();
   if constexpr (k == EncKind::kStaged) {
     const void* kp = (const void*)&vec_encode_hs_batch<D, B, POLAR, PITCH_IO>;
-    const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) { return encode_grid(kp, t, kBlock); }));
+    bool persistent = false;
+    const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) {
+      const uint64_t g = encode_grid(kp, t, kBlock);
+      persistent = g == persistent_grid(kp, t, kBlock);
+      return g;
+    }));
+    a.common.fair = persistent ? 1u : 0u;
     fill_hs_flips<D, hs_team<D>()>(a.common.seed, a.common.lane_flips);
     hipLaunchKernelGGL((vec_encode_hs_batch<D, B, POLAR, PITCH_IO>), grid, dim3(kBlock), 0, s, a);
   } else if constexpr (k == EncKind::kTransposed) {
     const void* kp = (const void*)&vec_encode_lt_batch<D, B, POLAR>;
     const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) { return persistent_grid(kp, t); }));
+    a.common.fair = 1u;
     fill_lt_flips<D>(a.common.seed, a.common.lane_flips);
     hipLaunchKernelGGL((vec_encode_lt_batch<D, B, POLAR>), grid, dim3(kBlock), 0, s, a);
   } else if constexpr (k == EncKind::kLanePerVector) {
     const void* kp = (const void*)&tq_encode_lpv_batch<D, B, PITCH_IO>;
     const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) { return persistent_grid(kp, t, 64); }));
+    a.common.fair = 1u;
     hipLaunchKernelGGL((tq_encode_lpv_batch<D, B, PITCH_IO>), grid, dim3(64), 0, s, a);
   } else {
     const void* kp = (const void*)&vec_encode_batch<D, B, POLAR, PITCH_IO>;
