@@ -250,7 +250,11 @@ constexpr uint64_t kChanSliceRoundsDec = 1;
 // at full occupancy; two repeats, identical bytes): decode 1M tokens (8 rounds of 32-channel slabs) 6.06 -> 6.35-6.40,
 // 2M (8 rounds) 6.50 -> 6.38-6.43, 4M (16 rounds) 5.45-5.48 -> 6.04-6.11; encode 1M (11 rounds) 5.34-5.38 ->
 // 4.99-5.01, 2M (16 rounds) 5.63-5.67 -> 5.98-6.01, config 3 (8 x 32768 tokens at d = 64, 2-4 rounds) 5.25-5.34 ->
-// 4.24-4.29. Hence one launch from 8 rounds for the decoder and from 16 for the encoder.
+// 4.24-4.29. Hence one launch from 8 rounds for the decoder and from 16 for the encoder. The encoder's 32-channel slabs
+// (calls of at most 32,768 (group, 64-channel) items) run one launch at their full 4 per CU from 4 rounds: d = 64 at
+// 2^19 - 2^21 tokens 65-67 -> 70.5-73.3 % of peak, d = 128 at 2^18 - 2^20 65-66 -> 72.1-72.5 % (two repeats, identical
+// bytes; at 2 per CU 53-63 %, at 3 per CU 62-71 %); at 2 rounds (config 3) the balanced persistent grid stays (65.5
+// against 64.5 %), and the 64-channel slabs of longer calls keep 2 per CU from 16 rounds (71-73 % against 70 % at 4).
 #ifndef PITCH_KIVI_DEC_ONE_LAUNCH
 #define PITCH_KIVI_DEC_ONE_LAUNCH 1  // float32 decode calls of PITCH_KIVI_DEC_MIN_ROUNDS+ rounds: one launch
 #endif
@@ -268,6 +272,12 @@ constexpr uint64_t kChanSliceRoundsDec = 1;
 #endif
 #ifndef PITCH_KIVI_ENC_MIN_ROUNDS
 #define PITCH_KIVI_ENC_MIN_ROUNDS 16  // resident rounds (balanced grid) from which the one-launch encode runs
+#endif
+#ifndef PITCH_KIVI_ENC_MIN_ROUNDS32
+#define PITCH_KIVI_ENC_MIN_ROUNDS32 4  // the same for 32-channel slabs
+#endif
+#ifndef PITCH_KIVI_ENC_WG_PER_CU32
+#define PITCH_KIVI_ENC_WG_PER_CU32 0  // resident workgroups per CU of 32-channel one-launch encodes (0: no cap)
 #endif
 #ifndef PITCH_KIVI_NT
 #define PITCH_KIVI_NT 1  // the wave encoder reads keys with non-temporal loads
@@ -715,12 +725,14 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       // bound by their arithmetic and keep every resident wave
       const uint64_t grid = persistent_grid(k, (items + 3) / 4, kBlock, PITCH_KIVI_BALANCE && IO == 0);
       const uint64_t need = (items + 3) / 4;
-      if (PITCH_KIVI_ENC_ONE_LAUNCH && IO == 0 && need >= PITCH_KIVI_ENC_MIN_ROUNDS * grid) {
+      const uint64_t min_rounds = SW == 32 ? PITCH_KIVI_ENC_MIN_ROUNDS32 : PITCH_KIVI_ENC_MIN_ROUNDS;
+      const int cap = SW == 32 ? PITCH_KIVI_ENC_WG_PER_CU32 : PITCH_KIVI_ENC_WG_PER_CU;
+      if (PITCH_KIVI_ENC_ONE_LAUNCH && IO == 0 && need >= min_rounds * grid) {
         // long float32 calls: one launch of one item per wave, far more workgroups than the CUs hold (config-5 keys,
         // 341 rounds: 5.52 TB/s against 5.41 for launches of two rounds, three repeats each, before the cap)
         const uint64_t g = need < 0x7FFFFFFFull ? need : 0x7FFFFFFFull;
         hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)g), dim3(kBlock),
-                           lds_cap_bytes(k, PITCH_KIVI_ENC_WG_PER_CU), s, a);
+                           lds_cap_bytes(k, cap), s, a);
         return;
       }
       const uint64_t slabs = (a.dim + SW - 1) / SW, rounds = slice_rounds(kChanSliceRoundsEnc);

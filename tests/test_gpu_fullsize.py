@@ -245,27 +245,37 @@ def test_kivi_long_decode_one_launch_matches_slices(q, d, bits, n):
 
 @pytest.mark.parametrize("bits", [4, 3])
 def test_kivi_long_encode_one_launch_partial_group(q, bits):
-    """A float32 KIVI encode of 16+ resident rounds (one launch at a capped residency) ending in a partial group:
-    2^22 + 37 tokens at d = 128 are 131,074 (group, 64-channel) items. Codes and ranges equal, byte for byte, those
-    of the same keys encoded in slices of 2^18 tokens (a few rounds, launches of two rounds or one), and the last
-    (37-token) group and the first one match the oracle bit for bit."""
+    """A float32 KIVI encode of 16+ resident rounds (one launch at a capped residency, 64-channel slabs) ending in a
+    partial group: 2^22 + 37 tokens at d = 128 are 131,074 (group, 64-channel) items. Codes and ranges equal, byte
+    for byte, those of the same keys encoded in slices of 2^18 tokens (32-channel slabs, one launch at full
+    residency), and the last (37-token) group and the first one match the oracle bit for bit."""
+    kivi_encode_vs_slices(q, 128, bits, (1 << 22) + 37, 1 << 18, 5400 + bits)
+
+
+@pytest.mark.parametrize("d,bits", [(64, 4), (128, 3), (64, 2)])
+def test_kivi_mid_encode_one_launch_partial_group(q, d, bits):
+    """A float32 KIVI encode of 4-16 resident rounds of 32-channel slabs (one launch at the encoder's full
+    residency): 2^19 + 37 tokens. Codes and ranges equal, byte for byte, those of slices of 2^17 tokens (the
+    balanced persistent grid), and the first and last (37-token) groups match the oracle bit for bit."""
+    kivi_encode_vs_slices(q, d, bits, (1 << 19) + 37, 1 << 17, 5500 + d + bits)
+
+
+def kivi_encode_vs_slices(q, d, bits, n, per, seed):
     import torch
     import pitch_amd as P
     from pitch_amd import workloads as W
-    d, G = 128, 64
-    n = (1 << 22) + 37
+    G = 64
     dev = q.device
-    print(f"long KIVI encode d={d} b={bits} tokens={n}", flush=True)
+    print(f"KIVI encode d={d} b={bits} tokens={n} against slices of {per}", flush=True)
     cfg = P.ChannelQuantConfig(d, bits, G)
     groups = cfg.groupCount(n)
-    gk = torch.Generator(device=dev).manual_seed(5400 + bits)
+    gk = torch.Generator(device=dev).manual_seed(seed)
     x = W.biased_keys(torch, gk, dev, 1, n, d).reshape(n, d).contiguous()
     c1 = torch.zeros(n * cfg.codeStride, dtype=torch.uint8, device=dev)
     r1 = torch.full((groups * 2 * d,), float("nan"), dtype=torch.float16, device=dev)
     c2 = torch.zeros_like(c1)
     r2 = torch.full_like(r1, float("nan"))
     q.enqueuePerChannelEncode(x, c1, r1, n, cfg)
-    per = 1 << 18
     for t0 in range(0, n, per):
         m = min(per, n - t0)
         q.enqueuePerChannelEncode(x, c2, r2, m, cfg, inputOffset=t0 * d * 4, codesOffset=t0 * cfg.codeStride,
