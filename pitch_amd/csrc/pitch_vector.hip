@@ -1436,13 +1436,22 @@ __device__ __forceinline__ void chunk_floats(const u32x4& w, float (&f)[Io<IO>::
 // with it). Both arguments are wave-uniform.
 struct FairPriority {
   bool on;
-  uint32_t total, left;
-  __device__ FairPriority(bool on_, uint64_t blocks)
-      : on(on_), total(blocks < 1 ? 1u : (blocks > 0xFFFFFFu ? 0xFFFFFFu : (uint32_t)blocks)), left(total) {}
+  float inv;      // 4 / the wave's blocks
+  uint32_t left;  // blocks still to do
+  // rem: vectors from the wave's first block to the end of its segment; stride: vectors between its blocks. The
+  // block count ceil(rem / stride) is taken in float32 (to within one, which a priority level does not need better),
+  // and only in a persistent launch: on a call's critical path a 64-bit division costs more than the priority saves.
+  __device__ FairPriority(bool on_, uint64_t rem, uint64_t stride) : on(PITCH_ENC_FAIR && on_), inv(0.f), left(0u) {
+    if (on) {
+      const float blocks = __builtin_fmaxf(1.f, __builtin_ceilf((float)rem * __builtin_amdgcn_rcpf((float)stride)));
+      inv = 4.f * __builtin_amdgcn_rcpf(blocks);
+      left = (uint32_t)blocks;
+    }
+  }
   // before each block
   __device__ __forceinline__ void next() {
-    if (PITCH_ENC_FAIR && on) {
-      const uint32_t level = __builtin_amdgcn_readfirstlane((left * 4u) / total);
+    if (on) {
+      const uint32_t level = __builtin_amdgcn_readfirstlane(min(3u, (uint32_t)((float)left * inv)));
       if (level >= 3) __builtin_amdgcn_s_setprio(3);
       else if (level == 2) __builtin_amdgcn_s_setprio(2);
       else if (level == 1) __builtin_amdgcn_s_setprio(1);
@@ -1484,7 +1493,7 @@ __device__ __forceinline__ void lpv_run(const VecArgs& p, const EncSeg sg, uint6
   for (int r = 0; r < K; ++r)
     smask[r] = sign_is_negative(p.seed, (uint32_t)(K * (lane % Lp::QPV) + r)) ? 0x80000000u : 0u;
   __syncthreads();
-  FairPriority fair(p.fair != 0, block * V < sg.count ? (sg.count - block * V + nblocks * V - 1) / (nblocks * V) : 0);
+  FairPriority fair(p.fair != 0, block * V < sg.count ? sg.count - block * V : 0, nblocks * V);
   for (uint64_t base = block * V; base < sg.count; base += nblocks * V) {
     fair.next();
     // stage the wave's block of V vectors in LDS with coalesced loads
@@ -1997,24 +2006,23 @@ __device__ __forceinline__ void hs_run(const VecArgs& p, const EncSeg sg, uint64
   // Software pipeline with PFD blocks of loads in flight. The loop is rotated so that each block's loads are
   // waited for in straight-line code after exactly the stores of the block before (two or so operations):
   // an iteration issues the loads of block k + PFD, computes and stores block k, then stages block k + 1.
-  // The waves' first loads go out before the table set-up, whose loads queue behind them: one load latency
-  // before the first block instead of the table's and then the block's.
+  // The waves' first loads are issued after the table set-up, so no other load is pending at that point (issued
+  // before it, with the table's loads queued behind them, small calls measured 2-13 % slower).
   constexpr int PFD = hs_pfd<D, B, KBIAS>();
   static_assert(PFD == 1 || PFD == 2, "prefetch depth");
-  HsChunk<IO> pfa[H::QPL];
-  HsChunk<IO> pfb[PFD > 1 ? H::QPL : 1];
-  // every fetch is unconditional, like the stores: a block past the end re-reads the last vector (a cache hit;
-  // every call has at least one vector), also in a wave that has no block and leaves after the barrier
-  hs_fetch<D, T, IO>(in, base, sg.count, lane, pfa);
-  if constexpr (PFD > 1) hs_fetch<D, T, IO>(in, base + stride, sg.count, lane, pfb);
   if constexpr (!POLAR) Q::template load<64 * H::WAVES>(s_q, threadIdx.x);
   else if constexpr (B <= 5 && PITCH_POLAR_OCT_TAB) octant_table_build<B>((uint8_t*)s_q.tab, threadIdx.x, 64 * H::WAVES);
   const uint64_t* neg = (const uint64_t*)p.lane_flips;  // fill_hs_flips; kernel arguments, read as scalars
   __syncthreads();
   if (base >= sg.count) return;
+  HsChunk<IO> pfa[H::QPL];
+  HsChunk<IO> pfb[PFD > 1 ? H::QPL : 1];
+  // every fetch is unconditional, like the stores: a block past the end re-reads the last vector (a cache hit)
+  hs_fetch<D, T, IO>(in, base, sg.count, lane, pfa);
+  if constexpr (PFD > 1) hs_fetch<D, T, IO>(in, base + stride, sg.count, lane, pfb);
   double* sx = s_x[wave];
   double x[E];
-  FairPriority fair(p.fair != 0, (sg.count - base + stride - 1) / stride);
+  FairPriority fair(p.fair != 0, sg.count - base, stride);
   hs_stage<D, T, KBIAS, IO>(p, sg.count, pfa, base, lane, neg, sx, x);
   auto step = [&](HsChunk<IO> (&refill)[H::QPL], HsChunk<IO> (&next)[H::QPL]) {
     fair.next();
@@ -2285,17 +2293,16 @@ __device__ __forceinline__ void lt_run(const VecArgs& p, const EncSeg sg, uint64
   static_assert(!POLAR || sizeof(s_q) >= (size_t)OctTab<B>::N, "the octant table fits the bucket table's space");
   // Software pipeline as in the staged-stage encoder: an iteration issues the loads of block k + 1, computes and
   // stores block k, then stages block k + 1 (past the end: re-reads of the last vector, staged, never computed).
-  // The first block's loads go out before the table set-up, as there.
-  uint32_t pf[32];
-  lt_fetch<D>(in, base, sg.count, lane, pf);
   if constexpr (!POLAR) Q::template load<kBlock>(s_q, threadIdx.x);
   else if constexpr (B <= 5 && PITCH_POLAR_OCT_TAB) octant_table_build<B>((uint8_t*)s_q.tab, threadIdx.x, kBlock);
   const uint32_t* neg = p.lane_flips;  // fill_lt_flips; kernel arguments, read as scalars
   __syncthreads();
   if (base >= sg.count) return;
+  uint32_t pf[32];
+  lt_fetch<D>(in, base, sg.count, lane, pf);
   double* sx = s_x[wave];
   double x[32];
-  FairPriority fair(p.fair != 0, (sg.count - base + stride - 1) / stride);
+  FairPriority fair(p.fair != 0, sg.count - base, stride);
   lt_stage<D, POLAR>(neg, pf, lane, sx, x);
   while (base < sg.count) {
     fair.next();
@@ -2375,7 +2382,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
       const uint64_t need = (a.count + H::WAVES * H::V - 1) / (H::WAVES * H::V);
       const void* k = (const void*)&vec_encode_hs<D, B, POLAR, KBIAS, IO>;
       const uint64_t grid = encode_grid(k, need, 64 * H::WAVES);
-      a.fair = grid == persistent_grid(k, need, 64 * H::WAVES) ? 1u : 0u;
+      a.fair = need > grid && grid == persistent_grid(k, need, 64 * H::WAVES) ? 1u : 0u;
       const uint64_t rounds = KBIAS ? 0 : slice_rounds(0);
       if (rounds && need > grid * rounds) {
         constexpr int NW = (D * B + 31) / 32;
@@ -2405,7 +2412,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
       // persistent at every size: the oversubscribed grid of encode_grid measured 3-4 % slower on the d = 1024
       // sweep (2^20 vectors, 43 rounds)
       const uint64_t grid = persistent_grid(k, need);
-      a.fair = 1u;
+      a.fair = need > grid ? 1u : 0u;
       hipLaunchKernelGGL((vec_encode_lt<D, B, POLAR>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
       return hipGetLastError();
     }
@@ -2416,7 +2423,7 @@ hipError_t launch_one(bool encode, const VecArgs& args, hipStream_t s) {
       const uint64_t need = (a.count + V - 1) / V;
       const void* k = (const void*)&tq_encode_lpv<D, B, IO, KBIAS>;
       const uint64_t grid = persistent_grid(k, need, 64);
-      a.fair = 1u;
+      a.fair = need > grid ? 1u : 0u;
       hipLaunchKernelGGL((tq_encode_lpv<D, B, IO, KBIAS>), dim3((uint32_t)grid), dim3(64), 0, s, a);
       return hipGetLastError();
     }
@@ -2532,25 +2539,35 @@ hipError_t launch_batch(VecBatchArgs a, hipStream_t s) {
   constexpr uint64_t vpb = enc_vectors_per_block<D, POLAR, PITCH_IO>();
   if constexpr (k == EncKind::kStaged) {
     const void* kp = (const void*)&vec_encode_hs_batch<D, B, POLAR, PITCH_IO>;
-    bool persistent = false;
+    bool fair = false;  // a persistent grid of more than one round
     const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) {
       const uint64_t g = encode_grid(kp, t, kBlock);
-      persistent = g == persistent_grid(kp, t, kBlock);
+      fair = t > g && g == persistent_grid(kp, t, kBlock);
       return g;
     }));
-    a.common.fair = persistent ? 1u : 0u;
+    a.common.fair = fair ? 1u : 0u;
     fill_hs_flips<D, hs_team<D>()>(a.common.seed, a.common.lane_flips);
     hipLaunchKernelGGL((vec_encode_hs_batch<D, B, POLAR, PITCH_IO>), grid, dim3(kBlock), 0, s, a);
   } else if constexpr (k == EncKind::kTransposed) {
     const void* kp = (const void*)&vec_encode_lt_batch<D, B, POLAR>;
-    const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) { return persistent_grid(kp, t); }));
-    a.common.fair = 1u;
+    bool fair = false;
+    const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) {
+      const uint64_t g = persistent_grid(kp, t);
+      fair = t > g;
+      return g;
+    }));
+    a.common.fair = fair ? 1u : 0u;
     fill_lt_flips<D>(a.common.seed, a.common.lane_flips);
     hipLaunchKernelGGL((vec_encode_lt_batch<D, B, POLAR>), grid, dim3(kBlock), 0, s, a);
   } else if constexpr (k == EncKind::kLanePerVector) {
     const void* kp = (const void*)&tq_encode_lpv_batch<D, B, PITCH_IO>;
-    const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) { return persistent_grid(kp, t, 64); }));
-    a.common.fair = 1u;
+    bool fair = false;
+    const dim3 grid(assign_blocks(a, vpb, [&](uint64_t t) {
+      const uint64_t g = persistent_grid(kp, t, 64);
+      fair = t > g;
+      return g;
+    }));
+    a.common.fair = fair ? 1u : 0u;
     hipLaunchKernelGGL((tq_encode_lpv_batch<D, B, PITCH_IO>), grid, dim3(64), 0, s, a);
   } else {
     const void* kp = (const void*)&vec_encode_batch<D, B, POLAR, PITCH_IO>;
