@@ -728,8 +728,9 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
       const uint64_t min_rounds = SW == 32 ? PITCH_KIVI_ENC_MIN_ROUNDS32 : PITCH_KIVI_ENC_MIN_ROUNDS;
       const int cap = SW == 32 ? PITCH_KIVI_ENC_WG_PER_CU32 : PITCH_KIVI_ENC_WG_PER_CU;
       if (PITCH_KIVI_ENC_ONE_LAUNCH && IO == 0 && need >= min_rounds * grid) {
-        // long float32 calls: one launch of one item per wave, far more workgroups than the CUs hold (config-5 keys,
-        // 341 rounds: 5.52 TB/s against 5.41 for launches of two rounds, three repeats each, before the cap)
+        // float32 calls of min_rounds+ rounds: one launch of one item per wave, far more workgroups than the CUs
+        // hold (config-5 keys, 341 rounds: 5.52 TB/s against 5.41 for launches of two rounds, three repeats each,
+        // before the cap), held at cap workgroups per CU (0: the kernel's full residency)
         const uint64_t g = need < 0x7FFFFFFFull ? need : 0x7FFFFFFFull;
         hipLaunchKernelGGL((chan_encode_w<B, IO, SW, DP>), dim3((uint32_t)g), dim3(kBlock),
                            lds_cap_bytes(k, cap), s, a);

@@ -49,8 +49,9 @@ struct VecArgs {
   // Rotation signs per team lane: bit e of lane_flips[t] is 1 when the coordinate held as element e by
   // team lane t has sign -1 (filled by the launcher from the seed).
   uint32_t lane_flips[32];
-  // Encoders: 1 when the launch is persistent (every wave keeps one fixed share of the blocks); the staged and
-  // transposed encoders then order their waves by the share still to do (FairPriority).
+  // Encoders: 1 when the launch is persistent (every wave keeps one fixed share of the blocks) and the shares are
+  // more than one block; the staged, transposed and lane-per-vector encoders then order their waves by the share
+  // still to do (FairPriority).
   uint32_t fair;
 };
 

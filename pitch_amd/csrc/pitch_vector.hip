@@ -1443,7 +1443,8 @@ struct FairPriority {
   // and only in a persistent launch: on a call's critical path a 64-bit division costs more than the priority saves.
   __device__ FairPriority(bool on_, uint64_t rem, uint64_t stride) : on(PITCH_ENC_FAIR && on_), inv(0.f), left(0u) {
     if (on) {
-      const float blocks = __builtin_fmaxf(1.f, __builtin_ceilf((float)rem * __builtin_amdgcn_rcpf((float)stride)));
+      const float q = __builtin_ceilf((float)rem * __builtin_amdgcn_rcpf((float)stride));
+      const float blocks = __builtin_fminf(__builtin_fmaxf(1.f, q), 16777216.f);  // a count uint32_t holds exactly
       inv = 4.f * __builtin_amdgcn_rcpf(blocks);
       left = (uint32_t)blocks;
     }
