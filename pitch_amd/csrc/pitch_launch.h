@@ -157,12 +157,13 @@ int device_cu_count();
 // proportion to the workgroups they run).
 uint64_t persistent_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256, bool balance_rounds = false);
 
-// Grid of the staged-stage encoder: persistent_grid, except for calls of at least 32 resident rounds,
+// Grid of the staged-stage encoder: persistent_grid, except for calls of at least PITCH_ENC_MIN_ROUNDS resident rounds,
 // which run about 8 blocks per workgroup in one launch (many more workgroups than the CUs hold at once, handed
 // out by the hardware as earlier ones finish). Measured on the config-5 value encode (524,288 blocks, 768
 // resident workgroups): 4.84 TB/s persistent, 5.21 / 5.29 / 5.26 / 4.90 TB/s at 43 / 11 / 5.3 / 2.7 blocks per
 // workgroup; on two more boxes, three repeats each, 8 blocks 1.5 % faster than 6, 10 or 12. Calls of fewer rounds
-// lose from it (config 2, 8 rounds: -5 to -15 %), so they stay persistent.
+// lose from it (config 2, 8 rounds: -5 to -15 %; with the fair wave priority of persistent launches, calls of up
+// to 48 rounds), so they stay persistent.
 uint64_t encode_grid(const void* kernel, uint64_t blocks_needed, int block_size = 256);
 
 // Dynamic LDS bytes that hold a launch of `kernel` to at most per_cu resident workgroups per CU: enough LDS per
