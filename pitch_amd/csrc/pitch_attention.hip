@@ -18,7 +18,8 @@
 // With equal key and value bit widths attn_chunk runs the scores and values phases in one kernel and keeps the
 // weights p in LDS (attn_scores and attn_values remain for unequal widths and for per-channel keys).
 // Query heads of one KV head (grouped-query attention) share every table read; their count is padded to
-// 1, 2, 4 or 8 (padded queries are zero and never written out).
+// 1, 2, 4 or 8 (padded queries are zero and never written out). With 4 or 8 the scores' and (at d = 128) the
+// values' products run on the matrix cores (v_mfma_f32_4x4x1f32, below).
 #include "pitch_device.h"
 
 #ifndef PITCH_DIM
@@ -32,7 +33,31 @@ constexpr int kMaxChunk = 1024;          // tokens per workgroup; a chunk's scor
 #ifndef PITCH_ATTN_FUSED
 #define PITCH_ATTN_FUSED 1  // keys and values of equal bit width: scores and values in one kernel (attn_chunk)
 #endif
+#ifndef PITCH_ATTN_MFMA
+#define PITCH_ATTN_MFMA 1  // four or eight query heads: their products on the matrix cores (below)
+#endif
 constexpr float kLn2 = 0x1.62e430p-1f;   // ln(2)
+
+// Matrix-core products for four or eight query heads per KV head. v_mfma_f32_4x4x1f32 computes 16 independent
+// 4 x 4 outer products per wave: D[v] of lane l += A(lane 4 (l / 4) + v) * B(lane l), in float32 (lane layout
+// checked on gfx950 with lane-numbered operands). Scores: A = the token's table value (one token per lane), B = the
+// rotated query of head l % 4 at the same coordinate, so D[v] of lane l accumulates the score of token
+// 4 (l / 4) + v for head l % 4. Values: A = the token's weight for head l % 4, B = the table value of coordinate
+// pair l of the token (d = 128: 64 pairs, one per lane), so D[v] of lane l accumulates head v's weighted sum of
+// that coordinate. One instruction replaces four per-lane fmas at half their issue cycles, on a unit of its own.
+typedef float v4f __attribute__((ext_vector_type(4)));
+template <int NQ>
+constexpr bool attn_mfma() { return PITCH_ATTN_MFMA && (NQ == 4 || NQ == 8); }
+__device__ __forceinline__ v4f mfma4(float a, float b, v4f c) { return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0); }
+// x of lane 4 (lane / 4) + V (a DPP quad broadcast)
+template <int V>
+__device__ __forceinline__ float quad_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), V * 0x55, 0xF, 0xF, true));
+}
+#ifndef PITCH_ATTN_VTOK
+#define PITCH_ATTN_VTOK 8  // matrix-core values phase: tokens per step (4, 8 or 16)
+#endif
+constexpr int kQStride = 4;  // padding of an LDS query row (floats): rows stay 16-byte aligned
 
 // Workspace regions (floats): rotated queries [kv][D/2][nqp][2], weights p [kv][T][nqp],
 // chunk (max, sum) [kv][nqp][chunks][2], chunk accumulators [kv][nqp][chunks][D], and for key-bias removal the
@@ -208,12 +233,16 @@ __device__ __forceinline__ void key_bias_scores(const AttnArgs& a, const float* 
 // weights p = 2^(s - m) and their sum l. (m, l) go to the workspace; the weights overwrite s_s, or with
 // WRITE_P go to the workspace for a separate values kernel. The table s_tab holds the key codes' pair values.
 // qp (the rotated queries of this KV head, read-only here) is passed separately so its wave-uniform reads can
-// be scalar loads.
+// be scalar loads. With four or eight query heads (attn_mfma) the products run on the matrix cores instead, and
+// s_q (NQ rows of D + kQStride floats, 16-byte aligned, which nothing else uses until the phase ends) holds the
+// queries as [head][coordinate].
 template <int D, int B, int NQ, bool WRITE_P, bool KB = false>
 __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __restrict__ qp_all, const float2* s_tab,
-                                             float* s_s, float* s_red, uint32_t kv, uint32_t c) {
+                                             float* s_s, float* s_red, float* s_q, uint32_t kv, uint32_t c) {
   using P = PairLut<D, B>;
   constexpr int NW = D * B / 32;
+  constexpr bool kMfma = attn_mfma<NQ>() && !KB;
+  constexpr int QS = D + kQStride;
   const int tid = threadIdx.x;
   const uint64_t t0 = (uint64_t)c * a.chunk;
   const uint32_t n = (uint32_t)min((uint64_t)a.chunk, a.tokens - t0);
@@ -228,6 +257,13 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
   uint32_t wn[NW];
   float nkn;
   fetch(tid, wn, nkn);
+  if constexpr (kMfma) {
+    for (int x = tid; x < D * NQ; x += kBlock) {
+      const int h = x / D, j = x % D;
+      s_q[h * QS + j] = qp[((j >> 1) * NQ + h) * 2 + (j & 1)];
+    }
+    __syncthreads();
+  }
   for (uint32_t i0 = 0; i0 < n; i0 += kBlock) {
     const uint32_t i = i0 + tid;
     const bool valid = i < n;
@@ -236,6 +272,41 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
     for (int k = 0; k < NW; ++k) w[k] = wn[k];
     const float nk = nkn;
     if (i0 + kBlock < n) fetch(i + kBlock, wn, nkn);
+    if constexpr (kMfma) {
+      // c (even coordinates) and e (odd ones): two independent chains per group of four heads
+      const int lane = tid & 63;
+      const float* q0 = s_q + (lane & 3) * QS;
+      v4f c0 = {0.f, 0.f, 0.f, 0.f}, e0 = c0, c1 = c0, e1 = c0;
+#pragma unroll
+      for (int p = 0; p < D / 2; p += 2) {
+        const v4f qa = *(const v4f*)(q0 + 2 * p);  // coordinates 2p .. 2p + 3 of head lane % 4
+        v4f qb = qa;
+        if constexpr (NQ == 8) qb = *(const v4f*)(q0 + 4 * QS + 2 * p);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int pos = 2 * B * (p + u), wi = pos >> 5, sh = pos & 31;
+          const uint32_t bits = (sh + 2 * B <= 32) ? (w[wi] >> sh) : __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh);
+          const float2 t = P::get(s_tab, bits);
+          c0 = mfma4(t.x, qa[2 * u], c0);
+          e0 = mfma4(t.y, qa[2 * u + 1], e0);
+          if constexpr (NQ == 8) {
+            c1 = mfma4(t.x, qb[2 * u], c1);
+            e1 = mfma4(t.y, qb[2 * u + 1], e1);
+          }
+        }
+      }
+      // lane l holds the scores of tokens 4 (l / 4) + v for head l % 4 (and l % 4 + 4); each takes its token's scale
+      const float nv[4] = {quad_bcast<0>(nk), quad_bcast<1>(nk), quad_bcast<2>(nk), quad_bcast<3>(nk)};
+      const uint32_t ib = i0 + (uint32_t)(tid & ~3);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (ib + v < n) {
+          s_s[(ib + v) * NQ + (lane & 3)] = (c0[v] + e0[v]) * nv[v];
+          if constexpr (NQ == 8) s_s[(ib + v) * NQ + 4 + (lane & 3)] = (c1[v] + e1[v]) * nv[v];
+        }
+      }
+      continue;
+    }
     float acc[NQ];
 #pragma unroll
     for (int h = 0; h < NQ; ++h) acc[h] = 0.f;
@@ -311,11 +382,13 @@ template <int D, int B, int NQ, bool KB>
 __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* __restrict__ qp_all) {
   using P = PairLut<D, B>;
   __shared__ float2 s_tab[P::N];
-  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ];
+  // the scores and, behind them, the query rows of the matrix-core form: one array, so that the compiler keeps the
+  // query reads inside the token loop (from a separate array it hoists all D * NQ of them into registers)
+  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ + (attn_mfma<NQ>() && !KB ? NQ * (D + kQStride) : 0)];
   __shared__ float s_red[4 * NQ];
   P::build(s_tab, a.kpolar != 0);
   __syncthreads();
-  scores_phase<D, B, NQ, true, KB>(a, qp_all, s_tab, s_s, s_red, blockIdx.y, blockIdx.x);
+  scores_phase<D, B, NQ, true, KB>(a, qp_all, s_tab, s_s, s_red, s_s + kMaxChunk * NQ, blockIdx.y, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------------------------- scores, KIVI keys
@@ -459,13 +532,21 @@ struct ValuesLayout {
   static constexpr int NW = D * B / 32;
   static constexpr int RS = NW + 1;  // staged row stride in words (odd: consecutive rows start on other banks)
   static constexpr int kCodeWords = kBlock * RS + 4;
+  static constexpr int WS = kBlock + 4;  // row stride of the weights staged as [head][token] (matrix-core form)
+  template <int NQ>
+  static constexpr int weight_floats() { return NQ * WS; }
 };
+// With four or eight query heads at d = 128 (matrix-core form) the weights are staged as [head][token], wave w
+// takes tokens 64 w .. 64 w + 63 of the block PITCH_ATTN_VTOK at a time, and lane l holds code pair l of each
+// token: its matrix-core accumulators hold coordinates 2 l and 2 l + 1 of every head.
 template <int D, int B, int NQ, bool P_LDS>
 __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_tab, const float* s_p,
                                              uint32_t* s_code, float* s_w, float* s_acc, uint32_t kv, uint32_t c) {
   using P = PairLut<D, B>;
   constexpr int NW = ValuesLayout<D, B>::NW;
   constexpr int RS = ValuesLayout<D, B>::RS;
+  constexpr int WS = ValuesLayout<D, B>::WS;
+  constexpr bool kMfma = attn_mfma<NQ>() && D == 128;
   constexpr int PPL = D / 32;        // code pairs per lane
   constexpr int LB = PPL * 2 * B;    // code bits per lane
   static_assert(LB <= 64, "a lane's codes fit two words after alignment");
@@ -482,6 +563,9 @@ __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_
   for (int h = 0; h < NQ; ++h)
 #pragma unroll
     for (int e = 0; e < 2 * PPL; ++e) acc[h][e] = 0.f;
+  v4f m0 = {0.f, 0.f, 0.f, 0.f}, m1 = m0, m2 = m0, m3 = m0;  // matrix-core form: heads 0-3 and 4-7, x and y
+  const int mw = (2 * B * lane) >> 5;
+  const uint32_t msh = (uint32_t)((2 * B * lane) & 31);
 
   // software pipeline: each thread loads the code row, scale and weights of its token of the next block while
   // the current block is accumulated
@@ -502,10 +586,42 @@ __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_
 #pragma unroll
     for (int k = 0; k < NW; ++k) s_code[tid * RS + k] = rown[k];
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) s_w[tid * NQ + h] = wtn[h];
+    for (int h = 0; h < NQ; ++h) s_w[kMfma ? h * WS + tid : tid * NQ + h] = wtn[h];
     __syncthreads();
     if (i0 + kBlock < n) fetch(i0 + kBlock + tid, rown, wtn);
     const uint32_t nt = min((uint32_t)kBlock, n - i0);
+    if constexpr (kMfma) {
+      // every one of the block's 256 slots was staged (tokens past the end with weight 0), so the last group of
+      // four may run past nt; the loop bounds are wave-uniform
+      constexpr int VT = PITCH_ATTN_VTOK;  // tokens per step: their LDS reads are issued together
+      static_assert(VT % 4 == 0 && 64 % VT == 0, "steps of whole weight quads within a wave's 64 tokens");
+      const uint32_t s1 = min(64u * (uint32_t)wid + 64u, nt);
+      for (uint32_t s0 = 64u * (uint32_t)wid; s0 < s1; s0 += VT) {
+        v4f wa[VT / 4], wb[VT / 4];
+#pragma unroll
+        for (int k = 0; k < VT / 4; ++k) {
+          wa[k] = *(const v4f*)(s_w + (lane & 3) * WS + s0 + 4 * k);
+          wb[k] = wa[k];
+          if constexpr (NQ == 8) wb[k] = *(const v4f*)(s_w + (4 + (lane & 3)) * WS + s0 + 4 * k);
+        }
+        float2 t[VT];
+#pragma unroll
+        for (int u = 0; u < VT; ++u) {
+          const uint32_t* row = s_code + (s0 + u) * RS + mw;  // row[1] exists: rows have a padding word
+          t[u] = P::get(s_tab, __builtin_amdgcn_alignbit(row[1], row[0], msh));
+        }
+#pragma unroll
+        for (int u = 0; u < VT; ++u) {
+          m0 = mfma4(wa[u / 4][u % 4], t[u].x, m0);
+          m1 = mfma4(wa[u / 4][u % 4], t[u].y, m1);
+          if constexpr (NQ == 8) {
+            m2 = mfma4(wb[u / 4][u % 4], t[u].x, m2);
+            m3 = mfma4(wb[u / 4][u % 4], t[u].y, m3);
+          }
+        }
+      }
+      continue;
+    }
     for (uint32_t s0 = 0; s0 < nt; s0 += 16) {
       const uint32_t tok = s0 + wid * 4 + r;
       if (tok < nt) {
@@ -541,20 +657,29 @@ __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_
       }
     }
   }
-  // sum over the four token rows of the wave (lanes g, g + 16, g + 32, g + 48), then over the waves
+  if constexpr (kMfma) {
+    __syncthreads();  // staging reads are done (s_acc may alias s_code)
 #pragma unroll
-  for (int h = 0; h < NQ; ++h)
-#pragma unroll
-    for (int e = 0; e < 2 * PPL; ++e) {
-      acc[h][e] += __shfl_xor(acc[h][e], 16);
-      acc[h][e] += __shfl_xor(acc[h][e], 32);
+    for (int v = 0; v < 4; ++v) {
+      *(float2*)(s_acc + (wid * NQ + v) * D + 2 * lane) = make_float2(m0[v], m1[v]);
+      if constexpr (NQ == 8) *(float2*)(s_acc + (wid * NQ + 4 + v) * D + 2 * lane) = make_float2(m2[v], m3[v]);
     }
-  __syncthreads();  // staging reads are done (s_acc may alias s_code)
-  if (r == 0) {
+  } else {
+    // sum over the four token rows of the wave (lanes g, g + 16, g + 32, g + 48), then over the waves
 #pragma unroll
     for (int h = 0; h < NQ; ++h)
 #pragma unroll
-      for (int e = 0; e < 2 * PPL; ++e) s_acc[(wid * NQ + h) * D + 2 * PPL * g + e] = acc[h][e];
+      for (int e = 0; e < 2 * PPL; ++e) {
+        acc[h][e] += __shfl_xor(acc[h][e], 16);
+        acc[h][e] += __shfl_xor(acc[h][e], 32);
+      }
+    __syncthreads();  // staging reads are done (s_acc may alias s_code)
+    if (r == 0) {
+#pragma unroll
+      for (int h = 0; h < NQ; ++h)
+#pragma unroll
+        for (int e = 0; e < 2 * PPL; ++e) s_acc[(wid * NQ + h) * D + 2 * PPL * g + e] = acc[h][e];
+    }
   }
   __syncthreads();
   float* A = a.ws + L.acc;
@@ -571,7 +696,7 @@ __global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
   using P = PairLut<D, B>;
   __shared__ float2 s_tab[P::N];
   __shared__ uint32_t s_code[ValuesLayout<D, B>::kCodeWords];
-  __shared__ __attribute__((aligned(16))) float s_w[kBlock * NQ];
+  __shared__ __attribute__((aligned(16))) float s_w[ValuesLayout<D, B>::template weight_floats<NQ>()];
   __shared__ float s_acc[4 * NQ * D];
   P::build(s_tab, a.vpolar != 0);
   values_phase<D, B, NQ, false>(a, s_tab, nullptr, s_code, s_w, s_acc, blockIdx.y, blockIdx.x);
@@ -584,7 +709,7 @@ __global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
 // space also holds the four waves' partial accumulators at the end.
 template <int D, int B, int NQ>
 struct FusedLds {
-  static constexpr int kStageBytes = ValuesLayout<D, B>::kCodeWords * 4 + kBlock * NQ * 4;
+  static constexpr int kStageBytes = ValuesLayout<D, B>::kCodeWords * 4 + ValuesLayout<D, B>::template weight_floats<NQ>() * 4;
   static constexpr int kAccBytes = 4 * NQ * D * 4;
   static constexpr int kRegionBytes = kStageBytes > kAccBytes ? kStageBytes : kAccBytes;
   static constexpr int kStaticBytes = PairLut<D, B>::N * 8 + 4 * NQ * 4;
@@ -602,7 +727,9 @@ __global__ __launch_bounds__(kBlock) void attn_chunk(AttnArgs a, const float* __
   static_assert(ValuesLayout<D, B>::kCodeWords % 4 == 0, "weights staging stays 16-byte aligned");
   P::build(s_tab, a.kpolar != 0);
   __syncthreads();
-  scores_phase<D, B, NQ, false>(a, qp_all, s_tab, s_s, s_red, blockIdx.y, blockIdx.x);
+  // the query rows of the scores phase use the values staging space, which is free until then
+  static_assert(NQ * (D + kQStride) <= ValuesLayout<D, B>::kCodeWords, "query rows fit the staging space");
+  scores_phase<D, B, NQ, false>(a, qp_all, s_tab, s_s, s_red, (float*)s_code, blockIdx.y, blockIdx.x);
   // the scores phase ended with a barrier after its last table read; the values phase begins with one
   if (a.vpolar != a.kpolar) P::build(s_tab, a.vpolar != 0);
   values_phase<D, B, NQ, true>(a, s_tab, s_s, s_code, s_w, (float*)s_code, blockIdx.y, blockIdx.x);

@@ -8,6 +8,9 @@
 #ifndef PITCH_ATTN_CHUNK
 #define PITCH_ATTN_CHUNK 0  // attention tokens per chunk: 0 = by call size (attention_chunk_tokens)
 #endif
+#ifndef PITCH_ATTN_MIN_WG
+#define PITCH_ATTN_MIN_WG 512  // attention_chunk_tokens halves the chunk until the call has this many workgroups
+#endif
 #ifndef PITCH_SLICE_ROUNDS
 #define PITCH_SLICE_ROUNDS -1  // rounds per launch of every sliced call: -1 = each kernel's own default
 #endif
