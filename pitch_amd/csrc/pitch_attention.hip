@@ -12,6 +12,7 @@
 // so no token is transformed: per token and coordinate pair the kernels do one LDS table read and a few FMAs
 // on the codes as stored. Kernels of one call (flash-decoding over chunks of a KV head's tokens):
 //   attn_prep     q'' = H(s_K (.) q) * scale * log2(e) / sqrt(d), per (KV head, query head), into the workspace
+//                 (with 4 or 8 padded query heads and no key-bias term the scores kernels compute it themselves)
 //   attn_scores   one thread per token: scores in log2 units into LDS, chunk max m_c, p = 2^(s - m_c), l_c
 //   attn_values   16 lanes per token: a_c = sum_t p_t n_t t[c_t] in the rotated domain
 //   attn_combine  merges the chunks, divides by the softmax sum, inverse rotation, output and log-sum-exp
@@ -235,7 +236,7 @@ __device__ __forceinline__ void key_bias_scores(const AttnArgs& a, const float* 
 // qp (the rotated queries of this KV head, read-only here) is passed separately so its wave-uniform reads can
 // be scalar loads. With four or eight query heads (attn_mfma) the products run on the matrix cores instead, and
 // s_q (NQ rows of D + kQStride floats, 16-byte aligned, which nothing else uses until the phase ends) holds the
-// queries as [head][coordinate].
+// rotated queries as [head][coordinate], computed by the phase itself (qp_all is not read).
 template <int D, int B, int NQ, bool WRITE_P, bool KB = false>
 __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __restrict__ qp_all, const float2* s_tab,
                                              float* s_s, float* s_red, float* s_q, uint32_t kv, uint32_t c) {
@@ -258,9 +259,21 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
   float nkn;
   fetch(tid, wn, nkn);
   if constexpr (kMfma) {
-    for (int x = tid; x < D * NQ; x += kBlock) {
-      const int h = x / D, j = x % D;
-      s_q[h * QS + j] = qp[((j >> 1) * NQ + h) * 2 + (j & 1)];
+    // the rotated queries, computed here as attn_prep computes them (no prep launch for these calls): wave w
+    // rotates heads w and w + 4
+    constexpr int E = D / 64;
+    const int lane = tid & 63;
+    for (int h = tid >> 6; h < NQ; h += kBlock / 64) {
+      float v[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int j = lane * E + e;
+        const float x = h < (int)a.nq ? a.q[((uint64_t)kv * a.nq + h) * D + j] : 0.f;
+        v[e] = sign_is_negative(a.kseed, (uint32_t)j) ? -x : x;
+      }
+      fwht_contig<E, 64, float>(v, lane);
+#pragma unroll
+      for (int e = 0; e < E; ++e) s_q[h * QS + lane * E + e] = v[e] * a.qscale;
     }
     __syncthreads();
   }
@@ -872,7 +885,10 @@ hipError_t PITCH_CAT(launch_attention_d, PITCH_DIM)(const AttnArgs& a, hipStream
   if (a.k_ranges && (a.k_group == 0 || a.k_group % 64 != 0 || a.head_stride % a.k_group != 0 || a.token_stride != 1))
     return hipErrorInvalidValue;
   if (a.kb_cos && (a.k_ranges || !a.kb_bias || !a.kb_sin)) return hipErrorInvalidValue;
-  if (!a.k_ranges) hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
+  // four or eight query heads without the key-bias term: the scores kernels rotate the queries themselves
+  const bool rotate_inside = (a.nqp == 4 && attn_mfma<4>()) || (a.nqp == 8 && attn_mfma<8>());
+  if (!a.k_ranges && !(rotate_inside && !a.kb_cos))
+    hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
   hipError_t e;
   switch (a.nqp) {
     case 1: e = launch_nq<1>(a, s); break;
