@@ -12,7 +12,7 @@
 // so no token is transformed: per token and coordinate pair the kernels do one LDS table read and a few FMAs
 // on the codes as stored. Kernels of one call (flash-decoding over chunks of a KV head's tokens):
 //   attn_prep     q'' = H(s_K (.) q) * scale * log2(e) / sqrt(d), per (KV head, query head), into the workspace
-//                 (with 4 or 8 padded query heads and no key-bias term the scores kernels compute it themselves)
+//                 (only for the key-bias term: otherwise the scores kernels compute it themselves)
 //   attn_scores   one thread per token: scores in log2 units into LDS, chunk max m_c, p = 2^(s - m_c), l_c
 //   attn_values   16 lanes per token: a_c = sum_t p_t n_t t[c_t] in the rotated domain
 //   attn_combine  merges the chunks, divides by the softmax sum, inverse rotation, output and log-sum-exp
@@ -49,6 +49,12 @@ constexpr float kLn2 = 0x1.62e430p-1f;   // ln(2)
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <int NQ>
 constexpr bool attn_mfma() { return PITCH_ATTN_MFMA && (NQ == 4 || NQ == 8); }
+#ifndef PITCH_ATTN_QLDS
+#define PITCH_ATTN_QLDS 1  // one or two query heads: rotated queries in LDS, read as broadcasts (no prep launch)
+#endif
+// Whether the scores kernels (without the key-bias term) rotate the queries themselves.
+template <int NQ>
+constexpr bool attn_rotates() { return attn_mfma<NQ>() || PITCH_ATTN_QLDS; }
 __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) { return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0); }
 // x of lane 4 (lane / 4) + V (a DPP quad broadcast)
 template <int V>
@@ -233,16 +239,18 @@ __device__ __forceinline__ void key_bias_scores(const AttnArgs& a, const float* 
 // Scores of chunk c of KV head kv, one thread per token, into s_s in log2 units; then the chunk maximum m, the
 // weights p = 2^(s - m) and their sum l. (m, l) go to the workspace; the weights overwrite s_s, or with
 // WRITE_P go to the workspace for a separate values kernel. The table s_tab holds the key codes' pair values.
-// qp (the rotated queries of this KV head, read-only here) is passed separately so its wave-uniform reads can
-// be scalar loads. With four or eight query heads (attn_mfma) the products run on the matrix cores instead, and
-// s_q (NQ rows of D + kQStride floats, 16-byte aligned, which nothing else uses until the phase ends) holds the
-// rotated queries as [head][coordinate], computed by the phase itself (qp_all is not read).
+// Without the key-bias term (attn_rotates) the phase computes the rotated queries itself into s_q (NQ rows of
+// D + kQStride floats, 16-byte aligned, which nothing else uses until the phase ends) as [head][coordinate]:
+// with four or eight query heads (attn_mfma) the products run on the matrix cores, with one or two each lane
+// reads the query pairs from s_q (the same address in every lane: broadcast reads). With the key-bias term the
+// rotated queries come from attn_prep through qp_all, whose wave-uniform reads can be scalar loads.
 template <int D, int B, int NQ, bool WRITE_P, bool KB = false>
 __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __restrict__ qp_all, const float2* s_tab,
                                              float* s_s, float* s_red, float* s_q, uint32_t kv, uint32_t c) {
   using P = PairLut<D, B>;
   constexpr int NW = D * B / 32;
   constexpr bool kMfma = attn_mfma<NQ>() && !KB;
+  constexpr bool kRot = attn_rotates<NQ>() && !KB;  // the phase rotates the queries into s_q
   constexpr int QS = D + kQStride;
   const int tid = threadIdx.x;
   const uint64_t t0 = (uint64_t)c * a.chunk;
@@ -258,7 +266,7 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
   uint32_t wn[NW];
   float nkn;
   fetch(tid, wn, nkn);
-  if constexpr (kMfma) {
+  if constexpr (kRot) {
     // the rotated queries, computed here as attn_prep computes them (no prep launch for these calls): wave w
     // rotates heads w and w + 4
     constexpr int E = D / 64;
@@ -330,8 +338,11 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
       const float2 t = P::get(s_tab, bits);
 #pragma unroll
       for (int h = 0; h < NQ; ++h) {
-        acc[h] = __builtin_fmaf(qp[(p * NQ + h) * 2], t.x, acc[h]);
-        acc[h] = __builtin_fmaf(qp[(p * NQ + h) * 2 + 1], t.y, acc[h]);
+        float2 q2;
+        if constexpr (kRot) q2 = *(const float2*)(s_q + h * QS + 2 * p);  // the same address in every lane
+        else q2 = make_float2(qp[(p * NQ + h) * 2], qp[(p * NQ + h) * 2 + 1]);
+        acc[h] = __builtin_fmaf(q2.x, t.x, acc[h]);
+        acc[h] = __builtin_fmaf(q2.y, t.y, acc[h]);
       }
     }
     if constexpr (KB) {  // key-bias removal: + q . o_t (position of a token past the chunk's end: its first)
@@ -397,7 +408,7 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
   __shared__ float2 s_tab[P::N];
   // the scores and, behind them, the query rows of the matrix-core form: one array, so that the compiler keeps the
   // query reads inside the token loop (from a separate array it hoists all D * NQ of them into registers)
-  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ + (attn_mfma<NQ>() && !KB ? NQ * (D + kQStride) : 0)];
+  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ + (attn_rotates<NQ>() && !KB ? NQ * (D + kQStride) : 0)];
   __shared__ float s_red[4 * NQ];
   P::build(s_tab, a.kpolar != 0);
   __syncthreads();
@@ -885,8 +896,9 @@ hipError_t PITCH_CAT(launch_attention_d, PITCH_DIM)(const AttnArgs& a, hipStream
   if (a.k_ranges && (a.k_group == 0 || a.k_group % 64 != 0 || a.head_stride % a.k_group != 0 || a.token_stride != 1))
     return hipErrorInvalidValue;
   if (a.kb_cos && (a.k_ranges || !a.kb_bias || !a.kb_sin)) return hipErrorInvalidValue;
-  // four or eight query heads without the key-bias term: the scores kernels rotate the queries themselves
-  const bool rotate_inside = (a.nqp == 4 && attn_mfma<4>()) || (a.nqp == 8 && attn_mfma<8>());
+  // without the key-bias term the scores kernels rotate the queries themselves (attn_rotates)
+  const bool rotate_inside = (a.nqp == 1 && attn_rotates<1>()) || (a.nqp == 2 && attn_rotates<2>()) ||
+                             (a.nqp == 4 && attn_rotates<4>()) || (a.nqp == 8 && attn_rotates<8>());
   if (!a.k_ranges && !(rotate_inside && !a.kb_cos))
     hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
   hipError_t e;
