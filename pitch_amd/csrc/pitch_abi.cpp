@@ -523,7 +523,7 @@ int device_cu_count() {
 
 uint32_t attention_chunk_tokens(uint64_t tokens, uint32_t kv_heads) {
   // The largest chunk that still gives at least PITCH_ATTN_MIN_WG workgroups (512: two per compute unit; 1024 and
-  // 2048 measured 1-50 % slower), between 128 and 1024 tokens; PITCH_ATTN_CHUNK (a compile-time tuning macro:
+  // 2048 measured 0-51 % slower), between 128 and 1024 tokens; PITCH_ATTN_CHUNK (a compile-time tuning macro:
   // 64 ... 1024, a power of two) fixes it instead.
   static_assert(PITCH_ATTN_CHUNK == 0 ||
                     (PITCH_ATTN_CHUNK >= 64 && PITCH_ATTN_CHUNK <= 1024 && (PITCH_ATTN_CHUNK & (PITCH_ATTN_CHUNK - 1)) == 0),
