@@ -19,8 +19,8 @@
 // With equal key and value bit widths attn_chunk runs the scores and values phases in one kernel and keeps the
 // weights p in LDS (attn_scores and attn_values remain for unequal widths and for per-channel keys).
 // Query heads of one KV head (grouped-query attention) share every table read; their count is padded to
-// 1, 2, 4 or 8 (padded queries are zero and never written out). With 4 or 8 the scores' and (at d = 128) the
-// values' products run on the matrix cores (v_mfma_f32_4x4x1f32, below).
+// 1, 2, 4 or 8 (padded queries are zero and never written out). With 4 or 8 the scores' and the values' products
+// run on the matrix cores (v_mfma_f32_4x4x1f32, below).
 #include "pitch_device.h"
 
 #ifndef PITCH_DIM
@@ -44,8 +44,8 @@ constexpr float kLn2 = 0x1.62e430p-1f;   // ln(2)
 // checked on gfx950 with lane-numbered operands). Scores: A = the token's table value (one token per lane), B = the
 // rotated query of head l % 4 at the same coordinate, so D[v] of lane l accumulates the score of token
 // 4 (l / 4) + v for head l % 4. Values: A = the token's weight for head l % 4, B = the table value of coordinate
-// pair l of the token (d = 128: 64 pairs, one per lane), so D[v] of lane l accumulates head v's weighted sum of
-// that coordinate. One instruction replaces four per-lane fmas at half their issue cycles, on a unit of its own.
+// pair l of the token (d = 128: 64 pairs, one per lane; d = 64: lanes 32-63 take pair l - 32 of the next token),
+// so D[v] of lane l accumulates head v's weighted sum of that coordinate. One instruction replaces four per-lane fmas at half their issue cycles, on a unit of its own.
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <int NQ>
 constexpr bool attn_mfma() { return PITCH_ATTN_MFMA && (NQ == 4 || NQ == 8); }
@@ -560,9 +560,10 @@ struct ValuesLayout {
   template <int NQ>
   static constexpr int weight_floats() { return NQ * WS; }
 };
-// With four or eight query heads at d = 128 (matrix-core form) the weights are staged as [head][token], wave w
+// With four or eight query heads (matrix-core form) the weights are staged as [head][token], wave w
 // takes tokens 64 w .. 64 w + 63 of the block PITCH_ATTN_VTOK at a time, and lane l holds code pair l of each
-// token: its matrix-core accumulators hold coordinates 2 l and 2 l + 1 of every head.
+// token (d = 64: pair l mod 32 of every second token, from token l / 32): its matrix-core accumulators hold
+// coordinates 2 (l mod D/2) and 2 (l mod D/2) + 1 of every head.
 template <int D, int B, int NQ, bool P_LDS>
 __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_tab, const float* s_p,
                                              uint32_t* s_code, float* s_w, float* s_acc, uint32_t kv, uint32_t c) {
@@ -570,7 +571,8 @@ __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_
   constexpr int NW = ValuesLayout<D, B>::NW;
   constexpr int RS = ValuesLayout<D, B>::RS;
   constexpr int WS = ValuesLayout<D, B>::WS;
-  constexpr bool kMfma = attn_mfma<NQ>() && D == 128;
+  constexpr bool kMfma = attn_mfma<NQ>();
+  constexpr int TPI = 128 / D;  // matrix-core form: tokens per instruction (d = 64: lanes 32-63 take the second)
   constexpr int PPL = D / 32;        // code pairs per lane
   constexpr int LB = PPL * 2 * B;    // code bits per lane
   static_assert(LB <= 64, "a lane's codes fit two words after alignment");
@@ -588,8 +590,9 @@ __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_
 #pragma unroll
     for (int e = 0; e < 2 * PPL; ++e) acc[h][e] = 0.f;
   v4f m0 = {0.f, 0.f, 0.f, 0.f}, m1 = m0, m2 = m0, m3 = m0;  // matrix-core form: heads 0-3 and 4-7, x and y
-  const int mw = (2 * B * lane) >> 5;
-  const uint32_t msh = (uint32_t)((2 * B * lane) & 31);
+  const int pl = lane % (D / 2), hi = lane / (D / 2);  // matrix-core form: code pair and token of the lane
+  const int mw = (2 * B * pl) >> 5;
+  const uint32_t msh = (uint32_t)((2 * B * pl) & 31);
 
   // software pipeline: each thread loads the code row, scale and weights of its token of the next block while
   // the current block is accumulated
@@ -628,19 +631,23 @@ __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_
           wb[k] = wa[k];
           if constexpr (NQ == 8) wb[k] = *(const v4f*)(s_w + (4 + (lane & 3)) * WS + s0 + 4 * k);
         }
-        float2 t[VT];
+        float2 t[VT / TPI];
 #pragma unroll
-        for (int u = 0; u < VT; ++u) {
-          const uint32_t* row = s_code + (s0 + u) * RS + mw;  // row[1] exists: rows have a padding word
+        for (int u = 0; u < VT / TPI; ++u) {
+          // token s0 + TPI u + hi; row[1] exists: rows have a padding word
+          const uint32_t* row = s_code + (s0 + TPI * u + hi) * RS + mw;
           t[u] = P::get(s_tab, __builtin_amdgcn_alignbit(row[1], row[0], msh));
         }
 #pragma unroll
-        for (int u = 0; u < VT; ++u) {
-          m0 = mfma4(wa[u / 4][u % 4], t[u].x, m0);
-          m1 = mfma4(wa[u / 4][u % 4], t[u].y, m1);
+        for (int u = 0; u < VT / TPI; ++u) {
+          const int k = TPI * u;  // the lane's token is s0 + k + hi
+          const float w0 = (TPI == 2 && hi) ? wa[(k + 1) / 4][(k + 1) % 4] : wa[k / 4][k % 4];
+          m0 = mfma4(w0, t[u].x, m0);
+          m1 = mfma4(w0, t[u].y, m1);
           if constexpr (NQ == 8) {
-            m2 = mfma4(wb[u / 4][u % 4], t[u].x, m2);
-            m3 = mfma4(wb[u / 4][u % 4], t[u].y, m3);
+            const float w1 = (TPI == 2 && hi) ? wb[(k + 1) / 4][(k + 1) % 4] : wb[k / 4][k % 4];
+            m2 = mfma4(w1, t[u].x, m2);
+            m3 = mfma4(w1, t[u].y, m3);
           }
         }
       }
@@ -682,11 +689,24 @@ __device__ __forceinline__ void values_phase(const AttnArgs& a, const float2* s_
     }
   }
   if constexpr (kMfma) {
-    __syncthreads();  // staging reads are done (s_acc may alias s_code)
+    if constexpr (TPI == 2) {  // lanes l and l + 32 summed different tokens of the same coordinates
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      *(float2*)(s_acc + (wid * NQ + v) * D + 2 * lane) = make_float2(m0[v], m1[v]);
-      if constexpr (NQ == 8) *(float2*)(s_acc + (wid * NQ + 4 + v) * D + 2 * lane) = make_float2(m2[v], m3[v]);
+      for (int v = 0; v < 4; ++v) {
+        m0[v] += __shfl_xor(m0[v], 32);
+        m1[v] += __shfl_xor(m1[v], 32);
+        if constexpr (NQ == 8) {
+          m2[v] += __shfl_xor(m2[v], 32);
+          m3[v] += __shfl_xor(m3[v], 32);
+        }
+      }
+    }
+    __syncthreads();  // staging reads are done (s_acc may alias s_code)
+    if (hi == 0) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        *(float2*)(s_acc + (wid * NQ + v) * D + 2 * pl) = make_float2(m0[v], m1[v]);
+        if constexpr (NQ == 8) *(float2*)(s_acc + (wid * NQ + 4 + v) * D + 2 * pl) = make_float2(m2[v], m3[v]);
+      }
     }
   } else {
     // sum over the four token rows of the wave (lanes g, g + 16, g + 32, g + 48), then over the waves
