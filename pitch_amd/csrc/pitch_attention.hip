@@ -249,8 +249,10 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
                                              float* s_s, float* s_red, float* s_q, uint32_t kv, uint32_t c) {
   using P = PairLut<D, B>;
   constexpr int NW = D * B / 32;
-  constexpr bool kMfma = attn_mfma<NQ>() && !KB;
-  constexpr bool kRot = attn_rotates<NQ>() && !KB;  // the phase rotates the queries into s_q
+  constexpr bool kMfma = attn_mfma<NQ>();
+  // the phase rotates the queries into s_q (with the key-bias term only in the matrix-core form, which also
+  // puts the bias products U = q (.) b and W = q (.) rotate_half(b), times kscale, in rows NQ .. 3 NQ - 1)
+  constexpr bool kRot = attn_rotates<NQ>() && (!KB || kMfma);
   constexpr int QS = D + kQStride;
   const int tid = threadIdx.x;
   const uint64_t t0 = (uint64_t)c * a.chunk;
@@ -278,6 +280,12 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
         const int j = lane * E + e;
         const float x = h < (int)a.nq ? a.q[((uint64_t)kv * a.nq + h) * D + j] : 0.f;
         v[e] = sign_is_negative(a.kseed, (uint32_t)j) ? -x : x;
+        if constexpr (KB) {  // as attn_prep: rotate_half(b)_j = -b_(j+D/2) for j < D/2 and b_(j-D/2) above
+          const float* bb = a.kb_bias + (uint64_t)kv * D;
+          const float rh = j < D / 2 ? -bb[j + D / 2] : bb[j - D / 2];
+          s_q[(NQ + h) * QS + j] = x * bb[j] * a.kscale;
+          s_q[(2 * NQ + h) * QS + j] = x * rh * a.kscale;
+        }
       }
       fwht_contig<E, 64, float>(v, lane);
 #pragma unroll
@@ -294,8 +302,39 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
     const float nk = nkn;
     if (i0 + kBlock < n) fetch(i + kBlock, wn, nkn);
     if constexpr (kMfma) {
-      // c (even coordinates) and e (odd ones): two independent chains per group of four heads
       const int lane = tid & 63;
+      // key-bias term q . o_t = sum_j U_hj cos_tj + W_hj sin_tj on the matrix cores too: A = the cos or sin row
+      // of the lane's token's position (a token past the chunk's end: its first), B = U or W of head l % 4
+      v4f bc0 = {0.f, 0.f, 0.f, 0.f}, bs0 = bc0, bc1 = bc0, bs1 = bc0;
+      if constexpr (KB) {
+        const uint64_t pos = a.kb_first + t0 + (valid ? i : 0u);
+        const f32x4* cr = (const f32x4*)(a.kb_cos + pos * D);
+        const f32x4* sr = (const f32x4*)(a.kb_sin + pos * D);
+        const float* u0 = s_q + (NQ + (lane & 3)) * QS;
+        const float* w0 = s_q + (2 * NQ + (lane & 3)) * QS;
+#pragma unroll 4
+        for (int j4 = 0; j4 < D / 4; ++j4) {
+          const f32x4 c4 = cr[j4], n4 = sr[j4];
+          const v4f ua = *(const v4f*)(u0 + 4 * j4), wa = *(const v4f*)(w0 + 4 * j4);
+          v4f ub = ua, wb = wa;
+          if constexpr (NQ == 8) {
+            ub = *(const v4f*)(u0 + 4 * QS + 4 * j4);
+            wb = *(const v4f*)(w0 + 4 * QS + 4 * j4);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            bc0 = mfma4(c4[r], ua[r], bc0);
+            bs0 = mfma4(n4[r], wa[r], bs0);
+            if constexpr (NQ == 8) {
+              bc1 = mfma4(c4[r], ub[r], bc1);
+              bs1 = mfma4(n4[r], wb[r], bs1);
+            }
+          }
+        }
+        // keeps the scores' LDS reads below: the scheduler otherwise issues all of them before these loads
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // c (even coordinates) and e (odd ones): two independent chains per group of four heads
       const float* q0 = s_q + (lane & 3) * QS;
       v4f c0 = {0.f, 0.f, 0.f, 0.f}, e0 = c0, c1 = c0, e1 = c0;
 #pragma unroll
@@ -322,8 +361,8 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         if (ib + v < n) {
-          s_s[(ib + v) * NQ + (lane & 3)] = (c0[v] + e0[v]) * nv[v];
-          if constexpr (NQ == 8) s_s[(ib + v) * NQ + 4 + (lane & 3)] = (c1[v] + e1[v]) * nv[v];
+          s_s[(ib + v) * NQ + (lane & 3)] = __builtin_fmaf(c0[v] + e0[v], nv[v], bc0[v] + bs0[v]);
+          if constexpr (NQ == 8) s_s[(ib + v) * NQ + 4 + (lane & 3)] = __builtin_fmaf(c1[v] + e1[v], nv[v], bc1[v] + bs1[v]);
         }
       }
       continue;
@@ -408,7 +447,7 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
   __shared__ float2 s_tab[P::N];
   // the scores and, behind them, the query rows of the matrix-core form: one array, so that the compiler keeps the
   // query reads inside the token loop (from a separate array it hoists all D * NQ of them into registers)
-  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ + (attn_rotates<NQ>() && !KB ? NQ * (D + kQStride) : 0)];
+  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ + (!attn_rotates<NQ>() || (KB && !attn_mfma<NQ>()) ? 0 : (KB ? 3 : 1) * NQ * (D + kQStride))];
   __shared__ float s_red[4 * NQ];
   P::build(s_tab, a.kpolar != 0);
   __syncthreads();
@@ -916,10 +955,12 @@ hipError_t PITCH_CAT(launch_attention_d, PITCH_DIM)(const AttnArgs& a, hipStream
   if (a.k_ranges && (a.k_group == 0 || a.k_group % 64 != 0 || a.head_stride % a.k_group != 0 || a.token_stride != 1))
     return hipErrorInvalidValue;
   if (a.kb_cos && (a.k_ranges || !a.kb_bias || !a.kb_sin)) return hipErrorInvalidValue;
-  // without the key-bias term the scores kernels rotate the queries themselves (attn_rotates)
+  // the scores kernels rotate the queries themselves (attn_rotates), with the key-bias term only in the
+  // matrix-core form (attn_mfma)
   const bool rotate_inside = (a.nqp == 1 && attn_rotates<1>()) || (a.nqp == 2 && attn_rotates<2>()) ||
                              (a.nqp == 4 && attn_rotates<4>()) || (a.nqp == 8 && attn_rotates<8>());
-  if (!a.k_ranges && !(rotate_inside && !a.kb_cos))
+  const bool mfma = (a.nqp == 4 && attn_mfma<4>()) || (a.nqp == 8 && attn_mfma<8>());
+  if (!a.k_ranges && !(rotate_inside && (!a.kb_cos || mfma)))
     hipLaunchKernelGGL((attn_prep<D>), dim3(a.kv_heads * a.nqp), dim3(64), 0, s, a);
   hipError_t e;
   switch (a.nqp) {
