@@ -12,7 +12,8 @@
 // so no token is transformed: per token and coordinate pair the kernels do one LDS table read and a few FMAs
 // on the codes as stored. Kernels of one call (flash-decoding over chunks of a KV head's tokens):
 //   attn_prep     q'' = H(s_K (.) q) * scale * log2(e) / sqrt(d), per (KV head, query head), into the workspace
-//                 (only for the key-bias term: otherwise the scores kernels compute it themselves)
+//                 (only for the key-bias term with 1 or 2 padded query heads: otherwise the scores kernels
+//                 compute it themselves)
 //   attn_scores   one thread per token: scores in log2 units into LDS, chunk max m_c, p = 2^(s - m_c), l_c
 //   attn_values   16 lanes per token: a_c = sum_t p_t n_t t[c_t] in the rotated domain
 //   attn_combine  merges the chunks, divides by the softmax sum, inverse rotation, output and log-sum-exp
