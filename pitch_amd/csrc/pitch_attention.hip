@@ -469,7 +469,11 @@ __global__ __launch_bounds__(kBlock) void attn_scores_chan(AttnArgs a) {
   const float levels = (float)((1 << B) - 1);
   __shared__ float s_s[kMaxChunk * NQ];
   __shared__ float s_red[4 * NQ];
-  __shared__ __attribute__((aligned(16))) float s_qs[4][D * NQ];   // per wave: [coordinate][query]
+  // four or eight query heads: the products on the matrix cores (as in scores_phase), the query products per wave
+  // as [query][coordinate] rows of D + kQStride; otherwise per-lane fmas over [coordinate][query]
+  constexpr bool kM = attn_mfma<NQ>();
+  constexpr int QS = D + kQStride;
+  __shared__ __attribute__((aligned(16))) float s_qs[4][kM ? NQ * QS : D * NQ];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const uint32_t kv = blockIdx.y, c = blockIdx.x;
   const uint64_t t0 = (uint64_t)c * a.chunk;
@@ -505,7 +509,7 @@ __global__ __launch_bounds__(kBlock) void attn_scores_chan(AttnArgs a) {
           step = step == 0.f ? 1.f : step;
 #pragma unroll
           for (int h = 0; h < NQ; ++h) {
-            qs[j * NQ + h] = qv[h][e] * step;
+            qs[kM ? h * QS + j : j * NQ + h] = qv[h][e] * step;
             beta[h] = __builtin_fmaf(qv[h][e], lo, beta[h]);
           }
         }
@@ -522,6 +526,46 @@ __global__ __launch_bounds__(kBlock) void attn_scores_chan(AttnArgs a) {
       const uint64_t row = (uint64_t)kv * a.head_stride + t0 + (valid ? i : wfirst);
       uint32_t w[NW];
       load_row<NW>(a.k_codes + row * NW, w);
+      if constexpr (kM) {
+        // D[v] of lane l: token wfirst + 4 (l / 4) + v, head l % 4 (c: even coordinates, e: odd ones)
+        const float* q0 = qs + (lane & 3) * QS;
+        v4f c0 = {0.f, 0.f, 0.f, 0.f}, e0 = c0, c1 = c0, e1 = c0;
+#pragma unroll
+        for (int j = 0; j < D; j += 4) {
+          const v4f qa = *(const v4f*)(q0 + j);
+          v4f qb = qa;
+          if constexpr (NQ == 8) qb = *(const v4f*)(q0 + 4 * QS + j);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int pos = B * (j + r), wi = pos >> 5, sh = pos & 31;
+            const uint32_t bits = (sh + B <= 32) ? (w[wi] >> sh) : __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh);
+            const float cf = (float)(bits & kMask);
+            if (r & 1) {
+              e0 = mfma4(cf, qa[r], e0);
+              if constexpr (NQ == 8) e1 = mfma4(cf, qb[r], e1);
+            } else {
+              c0 = mfma4(cf, qa[r], c0);
+              if constexpr (NQ == 8) c1 = mfma4(cf, qb[r], c1);
+            }
+          }
+        }
+        const int hl = lane & 3;
+        float b0 = beta[0], b1 = beta[NQ == 8 ? 4 : 0];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) {
+          b0 = hl == k ? beta[k] : b0;
+          if constexpr (NQ == 8) b1 = hl == k ? beta[4 + k] : b1;
+        }
+        const uint32_t ib = wfirst + (uint32_t)(lane & ~3);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          if (ib + v < n) {
+            s_s[(ib + v) * NQ + hl] = (c0[v] + e0[v]) + b0;
+            if constexpr (NQ == 8) s_s[(ib + v) * NQ + 4 + hl] = (c1[v] + e1[v]) + b1;
+          }
+        }
+        continue;
+      }
       float acc[NQ];
 #pragma unroll
       for (int h = 0; h < NQ; ++h) acc[h] = beta[h];
