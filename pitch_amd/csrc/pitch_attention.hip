@@ -239,14 +239,14 @@ __device__ __forceinline__ void key_bias_scores(const AttnArgs& a, const float* 
 // ---------------------------------------------------------------------------------------------- scores
 // Scores of chunk c of KV head kv, one thread per token, into s_s in log2 units; then the chunk maximum m, the
 // weights p = 2^(s - m) and their sum l. (m, l) go to the workspace; the weights overwrite s_s, or with
-// WRITE_P go to the workspace for a separate values kernel. The table s_tab holds the key codes' pair values.
+// WRITE_P go to the workspace for a separate values kernel. The phase builds the key codes' pair table in s_tab.
 // Without the key-bias term (attn_rotates) the phase computes the rotated queries itself into s_q (NQ rows of
 // D + kQStride floats, 16-byte aligned, which nothing else uses until the phase ends) as [head][coordinate]:
 // with four or eight query heads (attn_mfma) the products run on the matrix cores, with one or two each lane
 // reads the query pairs from s_q (the same address in every lane: broadcast reads). With the key-bias term the
 // rotated queries come from attn_prep through qp_all, whose wave-uniform reads can be scalar loads.
 template <int D, int B, int NQ, bool WRITE_P, bool KB = false>
-__device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __restrict__ qp_all, const float2* s_tab,
+__device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __restrict__ qp_all, float2* s_tab,
                                              float* s_s, float* s_red, float* s_q, uint32_t kv, uint32_t c) {
   using P = PairLut<D, B>;
   constexpr int NW = D * B / 32;
@@ -269,6 +269,8 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
   uint32_t wn[NW];
   float nkn;
   fetch(tid, wn, nkn);
+  // the pair table, its loads issued after the first code rows' (one barrier below covers table and queries)
+  P::build(s_tab, a.kpolar != 0);
   if constexpr (kRot) {
     // the rotated queries, computed here as attn_prep computes them (no prep launch for these calls): wave w
     // rotates heads w and w + 4
@@ -292,8 +294,8 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
 #pragma unroll
       for (int e = 0; e < E; ++e) s_q[h * QS + lane * E + e] = v[e] * a.qscale;
     }
-    __syncthreads();
   }
+  __syncthreads();
   for (uint32_t i0 = 0; i0 < n; i0 += kBlock) {
     const uint32_t i = i0 + tid;
     const bool valid = i < n;
@@ -450,8 +452,6 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
   // query reads inside the token loop (from a separate array it hoists all D * NQ of them into registers)
   __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ + (!attn_rotates<NQ>() || (KB && !attn_mfma<NQ>()) ? 0 : (KB ? 3 : 1) * NQ * (D + kQStride))];
   __shared__ float s_red[4 * NQ];
-  P::build(s_tab, a.kpolar != 0);
-  __syncthreads();
   scores_phase<D, B, NQ, true, KB>(a, qp_all, s_tab, s_s, s_red, s_s + kMaxChunk * NQ, blockIdx.y, blockIdx.x);
 }
 
@@ -853,8 +853,6 @@ __global__ __launch_bounds__(kBlock) void attn_chunk(AttnArgs a, const float* __
   uint32_t* s_code = (uint32_t*)(s_dyn + (size_t)a.chunk * NQ);
   float* s_w = (float*)(s_code + ValuesLayout<D, B>::kCodeWords);  // 16-byte aligned: kCodeWords % 4 == 0
   static_assert(ValuesLayout<D, B>::kCodeWords % 4 == 0, "weights staging stays 16-byte aligned");
-  P::build(s_tab, a.kpolar != 0);
-  __syncthreads();
   // the query rows of the scores phase use the values staging space, which is free until then
   static_assert(NQ * (D + kQStride) <= ValuesLayout<D, B>::kCodeWords, "query rows fit the staging space");
   scores_phase<D, B, NQ, false>(a, qp_all, s_tab, s_s, s_red, (float*)s_code, blockIdx.y, blockIdx.x);
