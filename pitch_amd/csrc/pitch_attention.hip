@@ -46,7 +46,8 @@ constexpr float kLn2 = 0x1.62e430p-1f;   // ln(2)
 // rotated query of head l % 4 at the same coordinate, so D[v] of lane l accumulates the score of token
 // 4 (l / 4) + v for head l % 4. Values: A = the token's weight for head l % 4, B = the table value of coordinate
 // pair l of the token (d = 128: 64 pairs, one per lane; d = 64: lanes 32-63 take pair l - 32 of the next token),
-// so D[v] of lane l accumulates head v's weighted sum of that coordinate. One instruction replaces four per-lane fmas at half their issue cycles, on a unit of its own.
+// so D[v] of lane l accumulates head v's weighted sum of that coordinate. One instruction replaces four per-lane
+// fmas at half their issue cycles, on a unit of its own.
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <int NQ>
 constexpr bool attn_mfma() { return PITCH_ATTN_MFMA && (NQ == 4 || NQ == 8); }
@@ -365,7 +366,8 @@ __device__ __forceinline__ void scores_phase(const AttnArgs& a, const float* __r
       for (int v = 0; v < 4; ++v) {
         if (ib + v < n) {
           s_s[(ib + v) * NQ + (lane & 3)] = __builtin_fmaf(c0[v] + e0[v], nv[v], bc0[v] + bs0[v]);
-          if constexpr (NQ == 8) s_s[(ib + v) * NQ + 4 + (lane & 3)] = __builtin_fmaf(c1[v] + e1[v], nv[v], bc1[v] + bs1[v]);
+          if constexpr (NQ == 8)
+            s_s[(ib + v) * NQ + 4 + (lane & 3)] = __builtin_fmaf(c1[v] + e1[v], nv[v], bc1[v] + bs1[v]);
         }
       }
       continue;
