@@ -57,7 +57,9 @@ constexpr bool attn_mfma() { return PITCH_ATTN_MFMA && (NQ == 4 || NQ == 8); }
 // Whether the scores kernels (without the key-bias term) rotate the queries themselves.
 template <int NQ>
 constexpr bool attn_rotates() { return attn_mfma<NQ>() || PITCH_ATTN_QLDS; }
-__device__ __forceinline__ v4f mfma4(float a, float b, v4f c) { return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+}
 // x of lane 4 (lane / 4) + V (a DPP quad broadcast)
 template <int V>
 __device__ __forceinline__ float quad_bcast(float x) {
@@ -452,7 +454,8 @@ __global__ __launch_bounds__(kBlock) void attn_scores(AttnArgs a, const float* _
   __shared__ float2 s_tab[P::N];
   // the scores and, behind them, the query rows of the matrix-core form: one array, so that the compiler keeps the
   // query reads inside the token loop (from a separate array it hoists all D * NQ of them into registers)
-  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ + (!attn_rotates<NQ>() || (KB && !attn_mfma<NQ>()) ? 0 : (KB ? 3 : 1) * NQ * (D + kQStride))];
+  constexpr bool kRot = attn_rotates<NQ>() && (!KB || attn_mfma<NQ>());  // as in scores_phase
+  __shared__ __attribute__((aligned(16))) float s_s[kMaxChunk * NQ + (kRot ? (KB ? 3 : 1) * NQ * (D + kQStride) : 0)];
   __shared__ float s_red[4 * NQ];
   scores_phase<D, B, NQ, true, KB>(a, qp_all, s_tab, s_s, s_red, s_s + kMaxChunk * NQ, blockIdx.y, blockIdx.x);
 }
@@ -839,7 +842,8 @@ __global__ __launch_bounds__(kBlock) void attn_values(AttnArgs a) {
 // space also holds the four waves' partial accumulators at the end.
 template <int D, int B, int NQ>
 struct FusedLds {
-  static constexpr int kStageBytes = ValuesLayout<D, B>::kCodeWords * 4 + ValuesLayout<D, B>::template weight_floats<NQ>() * 4;
+  static constexpr int kStageBytes =
+      ValuesLayout<D, B>::kCodeWords * 4 + ValuesLayout<D, B>::template weight_floats<NQ>() * 4;
   static constexpr int kAccBytes = 4 * NQ * D * 4;
   static constexpr int kRegionBytes = kStageBytes > kAccBytes ? kStageBytes : kAccBytes;
   static constexpr int kStaticBytes = PairLut<D, B>::N * 8 + 4 * NQ * 4;
