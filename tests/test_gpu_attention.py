@@ -73,6 +73,10 @@ CASES = [
     ("turboQuant", "turboQuant", 4, 4, 128, 4, 1, 7),
     ("turboQuant", "turboQuant", 4, 4, 128, 4, 2, 70000),  # many chunks, 512-token chunks
     ("turboQuant", "turboQuant", 3, 3, 64, 2, 3, 140000),  # 1024-token chunks
+    # unequal widths with 4 or 8 padded query heads: the separate scores and values kernels in matrix-core form
+    ("turboQuant", "turboQuant", 4, 2, 64, 8, 2, 3000),
+    ("polarQuant", "turboQuant", 3, 4, 128, 7, 1, 1500),
+    ("turboQuant", "polarQuant", 2, 3, 64, 3, 2, 900),
 ]
 
 
