@@ -236,6 +236,15 @@ constexpr int kGroupMaxW = 64;   // largest group the wave encoder takes
 // showed the same gain from short launches). Calls of up to this many rounds keep one launch.
 constexpr uint64_t kChanSliceRoundsEnc = 2;
 constexpr uint64_t kChanSliceRoundsDec = 1;
+#ifndef PITCH_KIVI_DEC_CPL8
+// 16-bit decodes at B <= 4 of whole 64-channel slabs: eight channels per lane from this many (group, slab) items
+// (d = 64, b = 4, float16 and bfloat16, two interleaved repeats: 4M tokens 57.2-58.3 -> 59.0-60.6 % of peak, 1M
+// 54.8-57.3 -> 55.1-57.9 %, but config 3's 262K tokens 49.2-49.7 -> 47.9-48.5 %: each lane's range set-up doubles)
+#define PITCH_KIVI_DEC_CPL8 1
+#endif
+#ifndef PITCH_KIVI_DEC_CPL8_MIN_ITEMS
+#define PITCH_KIVI_DEC_CPL8_MIN_ITEMS 16384u
+#endif
 #ifndef PITCH_KIVI_DEC_NTS
 // The wave decoder writes keys with non-temporal stores (cached stores measured 7.5 % slower at config 5's keys and
 // 23 % slower at config 3's, two repeats each).
@@ -597,12 +606,15 @@ __global__ __launch_bounds__(kBlock) void chan_decode4(ChanArgs p) {
 }
 
 // Group size a multiple of 64: one wave per (group, slab of SW channels), four independent waves per
-// workgroup. A lane loads the fp16 ranges of its four channels once, then for each 64-token chunk of the
-// group issues all its code-word loads before decoding; lane (r, c) holds channels 4c .. 4c+3 of tokens
-// r, r + 64 / TPL, ..., so one store instruction writes 256 / SW whole slab rows of SW * 4 bytes.
-template <int B, int SW, int IO>
+// workgroup. A lane loads the fp16 ranges of its CPL channels once, then for each 64-token chunk of the
+// group issues all its code-word loads before decoding; lane (r, c) holds channels CPL c .. CPL c + CPL - 1 of
+// tokens r, r + 64 / TPL, ..., so one store instruction writes 64 CPL / SW whole slab rows. CPL = 8 (16-bit
+// output, B <= 4, a dimension of whole slabs only: every lane's eight channels exist) stores 16 bytes per lane
+// from one code word, as the float32 path's CPL = 4 does.
+template <int B, int SW, int IO, int CPL = 4>
 __global__ __launch_bounds__(kBlock) void chan_decode_w(ChanArgs p) {
-  constexpr int QW = SW / 4;        // lanes per slab row
+  static_assert(CPL == 4 || (CPL == 8 && IO != 0 && B <= 4), "eight channels per lane: 16-bit output, one code word");
+  constexpr int QW = SW / CPL;      // lanes per slab row
   constexpr int RPI = 64 / QW;      // rows per store instruction
   constexpr int TPL = 64 / RPI;     // tokens per lane per 64-token chunk
   constexpr uint32_t kMask = (1u << B) - 1u;
@@ -619,20 +631,23 @@ __global__ __launch_bounds__(kBlock) void chan_decode_w(ChanArgs p) {
     const uint32_t g = (uint32_t)(it / slabs), sl = (uint32_t)(it - (uint64_t)g * slabs);
     const uint32_t first = g * G, n = min(G, p.count - first);
     const uint32_t ch0 = sl * SW, cw = min((uint32_t)SW, dim - ch0);
-    const bool cact = 4u * c < cw;
-    const uint32_t ch = ch0 + (cact ? 4u * c : 0u);
+    const bool cact = (uint32_t)CPL * c < cw;
+    const uint32_t ch = ch0 + (cact ? (uint32_t)CPL * c : 0u);
     const uint16_t* rg = p.ranges_in + (uint64_t)g * 2u * dim + ch;
-    const u32x2 lw = *(const u32x2*)rg, hw = *(const u32x2*)(rg + dim);
-    const uint16_t l16[4] = {(uint16_t)lw.x, (uint16_t)(lw.x >> 16), (uint16_t)lw.y, (uint16_t)(lw.y >> 16)};
-    const uint16_t h16[4] = {(uint16_t)hw.x, (uint16_t)(hw.x >> 16), (uint16_t)hw.y, (uint16_t)(hw.y >> 16)};
-    float bs[4], st[4];
+    float bs[CPL], st[CPL];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      bs[k] = h2f(l16[k]);
-      st[k] = kivi_step(bs[k], h2f(h16[k]), levels);
+    for (int q = 0; q < CPL / 4; ++q) {
+      const u32x2 lw = *(const u32x2*)(rg + 4 * q), hw = *(const u32x2*)(rg + dim + 4 * q);
+      const uint16_t l16[4] = {(uint16_t)lw.x, (uint16_t)(lw.x >> 16), (uint16_t)lw.y, (uint16_t)(lw.y >> 16)};
+      const uint16_t h16[4] = {(uint16_t)hw.x, (uint16_t)(hw.x >> 16), (uint16_t)hw.y, (uint16_t)(hw.y >> 16)};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        bs[4 * q + k] = h2f(l16[k]);
+        st[4 * q + k] = kivi_step(bs[4 * q + k], h2f(h16[k]), levels);
+      }
     }
     const uint32_t pos = ch * B, wi = pos >> 5, sh = pos & 31u;
-    const bool straddle = sh + 4u * B > 32u;
+    const bool straddle = sh + (uint32_t)CPL * B > 32u;
     for (uint32_t t0 = 0; t0 < n; t0 += 64) {
       // float32 output, a full 64-token chunk of a full slab: every lane is active and no row is clamped, so each
       // load and store is a wave-uniform row base plus the lane's 32-bit byte offset (config-3 decode +5 %; with
@@ -652,10 +667,10 @@ __global__ __launch_bounds__(kBlock) void chan_decode_w(ChanArgs p) {
 #pragma unroll
         for (int i = 0; i < TPL; ++i) {
           const uint32_t bits = __builtin_amdgcn_alignbit(hi[i], lo[i], sh);
-          float o[4];
+          float o[CPL];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) o[k] = (float)((bits >> (B * k)) & kMask) * st[k] + bs[k];
-          store_elems<IO, 4>(ob + (uint64_t)(RPI * i) * dim * ES + ol, 0, o, PITCH_KIVI_DEC_NTS);
+          for (int k = 0; k < CPL; ++k) o[k] = (float)((bits >> (B * k)) & kMask) * st[k] + bs[k];
+          store_elems<IO, CPL>(ob + (uint64_t)(RPI * i) * dim * ES + ol, 0, o, PITCH_KIVI_DEC_NTS);
         }
         continue;
       }
@@ -673,10 +688,10 @@ __global__ __launch_bounds__(kBlock) void chan_decode_w(ChanArgs p) {
         const uint32_t tk = t0 + r + RPI * i;
         if (tk < n && cact) {
           const uint32_t bits = __builtin_amdgcn_alignbit(hi[i], lo[i], sh);
-          float o[4];
+          float o[CPL];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) o[k] = (float)((bits >> (B * k)) & kMask) * st[k] + bs[k];
-          store_elems<IO, 4>(p.out, (uint64_t)(first + tk) * dim + ch, o, PITCH_KIVI_DEC_NTS);
+          for (int k = 0; k < CPL; ++k) o[k] = (float)((bits >> (B * k)) & kMask) * st[k] + bs[k];
+          store_elems<IO, CPL>(p.out, (uint64_t)(first + tk) * dim + ch, o, PITCH_KIVI_DEC_NTS);
         }
       }
     }
@@ -777,16 +792,16 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
     // 64-channel slabs (a 32-channel slab's rows are 64 bytes: 22 % slower)
     const uint64_t groups = ((uint64_t)a.count + a.group - 1) / a.group;
     const uint64_t items64 = groups * ((a.dim + kSlab - 1) / kSlab);
-    auto go = [&](auto sw_c) {
-      constexpr int SW = decltype(sw_c)::value;
+    auto go = [&](auto sw_c, auto cpl_c) {
+      constexpr int SW = decltype(sw_c)::value, CPL = decltype(cpl_c)::value;
       const uint64_t items = groups * ((a.dim + SW - 1) / SW);
-      const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, SW, IO>, (items + 3) / 4);
+      const uint64_t grid = persistent_grid((const void*)&chan_decode_w<B, SW, IO, CPL>, (items + 3) / 4);
       if (IO == 0 && PITCH_KIVI_DEC_ONE_LAUNCH && (items + 3) / 4 >= PITCH_KIVI_DEC_MIN_ROUNDS * grid) {
         // one launch of one item per wave at a capped residency (above); the kernel's grid-stride loop covers
         // any items past 2^31 - 1 workgroups
         const uint64_t need = (items + 3) / 4, g = need < 0x7FFFFFFFull ? need : 0x7FFFFFFFull;
-        const void* k = (const void*)&chan_decode_w<B, SW, IO>;
-        hipLaunchKernelGGL((chan_decode_w<B, SW, IO>), dim3((uint32_t)g), dim3(kBlock),
+        const void* k = (const void*)&chan_decode_w<B, SW, IO, CPL>;
+        hipLaunchKernelGGL((chan_decode_w<B, SW, IO, CPL>), dim3((uint32_t)g), dim3(kBlock),
                            lds_cap_bytes(k, PITCH_KIVI_DEC_WG_PER_CU), s, a);
         return;
       }
@@ -802,14 +817,21 @@ hipError_t launch_b(bool encode, const ChanArgs& a, hipStream_t s) {
           b.ranges_in = a.ranges_in + g0 * 2 * a.dim;
           b.out = (char*)a.out + t0 * a.dim * ES;
           const uint64_t gb = ((uint64_t)b.count + a.group - 1) / a.group, nb = (gb * slabs + 3) / 4;
-          hipLaunchKernelGGL((chan_decode_w<B, SW, IO>), dim3((uint32_t)(nb < grid ? nb : grid)), dim3(kBlock), 0, s, b);
+          hipLaunchKernelGGL((chan_decode_w<B, SW, IO, CPL>), dim3((uint32_t)(nb < grid ? nb : grid)), dim3(kBlock), 0, s, b);
         }
         return;
       }
-      hipLaunchKernelGGL((chan_decode_w<B, SW, IO>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((chan_decode_w<B, SW, IO, CPL>), dim3((uint32_t)grid), dim3(kBlock), 0, s, a);
     };
-    if (PITCH_KIVI_DEC_SLAB32 && IO == 0 && items64 <= PITCH_KIVI_DEC_SLAB32_MAX) go(std::integral_constant<int, 32>{});
-    else go(std::integral_constant<int, kSlab>{});
+    // 16-bit output at B <= 4 with whole slabs, long calls: eight channels per lane (16-byte stores from one code
+    // word); same output bits as four
+    constexpr int kCpl16 = IO != 0 && B <= 4 && PITCH_KIVI_DEC_CPL8 ? 8 : 4;
+    using Cpl4 = std::integral_constant<int, 4>;
+    if (PITCH_KIVI_DEC_SLAB32 && IO == 0 && items64 <= PITCH_KIVI_DEC_SLAB32_MAX)
+      go(std::integral_constant<int, 32>{}, Cpl4{});
+    else if (kCpl16 == 8 && a.dim % kSlab == 0u && items64 >= PITCH_KIVI_DEC_CPL8_MIN_ITEMS)
+      go(std::integral_constant<int, kSlab>{}, std::integral_constant<int, kCpl16>{});
+    else go(std::integral_constant<int, kSlab>{}, Cpl4{});
   } else if (vec4) {
     const uint32_t P = kBlock / (a.dim >> 2);
     const uint64_t need = ((uint64_t)a.count + P * kDecR - 1) / (P * kDecR);

@@ -123,7 +123,9 @@ def test_per_vector_decode_16bit(q, method, d, bits, io):
     assert max_rel_diff(O.from_io_bits(ours, io), ref, d) < REL_L2_BAR + HALF_ULP[io]
 
 
-CHANNEL = [(64, 64, 4), (128, 64, 2), (12, 7, 3), (128, 100, 8), (64, 128, 4), (33, 64, 5), (1024, 64, 4)]
+CHANNEL = [(64, 64, 4), (128, 64, 2), (12, 7, 3), (128, 100, 8), (64, 128, 4), (33, 64, 5), (1024, 64, 4),
+           # eight channels per lane in the wave decoder: b = 3 rows straddle code words; d = 96 keeps four
+           (128, 64, 3), (192, 128, 2), (96, 64, 4)]
 
 
 @pytest.mark.parametrize("io", IO_DTYPES)
@@ -219,3 +221,29 @@ def test_function_mirrors_keep_16bit(q):
     kc, kr = P.channel_encode(x.to(torch.float16), 4)
     dec = P.channel_decode(kc, kr, 4, dtype=torch.float16)
     assert dec.dtype == torch.float16
+
+
+@pytest.mark.parametrize("io", IO_DTYPES)
+@pytest.mark.parametrize("d,bits", [(64, 4), (128, 3), (192, 2)])
+def test_channel_16bit_long_decode(q, d, bits, io):
+    """A 16-bit per-channel decode of several launches' worth of tokens (partial last group; long enough for the
+    wave decoder's eight channels per lane) equals the float32 decode of the same codes rounded to the 16-bit
+    type, bit for bit (torch's casts round to nearest even, as
+    the oracle's 16-bit rules do)."""
+    import torch
+    import pitch_amd as P
+    n, G = (1 << 20) + 37, 64
+    print(f"KIVI long decode {io} d={d} b={bits} n={n}", flush=True)
+    cfg = P.ChannelQuantConfig(d, bits, G)
+    g = torch.Generator(device=q.device)
+    g.manual_seed(n + d + bits)
+    x = torch.randn(n, d, generator=g, device=q.device) * 4
+    codes = torch.empty(n * cfg.codeStride, dtype=torch.uint8, device=q.device)
+    ranges = torch.empty(cfg.groupCount(n) * 2 * d, dtype=torch.float16, device=q.device)
+    q.enqueuePerChannelEncode(x, codes, ranges, n, cfg)
+    out32 = torch.empty(n, d, dtype=torch.float32, device=q.device)
+    out16 = torch.empty(n, d, dtype=_tdtype(io), device=q.device)
+    q.enqueuePerChannelDecode(codes, ranges, out32, n, cfg)
+    q.enqueuePerChannelDecode(codes, ranges, out16, n, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(out16.view(torch.int16), out32.to(_tdtype(io)).view(torch.int16))
