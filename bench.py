@@ -1332,6 +1332,28 @@ def run_io16(torch, q, P, W, timer, gen, dev, args, x, keys4) -> dict:
                                               "encode_pct_peak": round(kb / ms_e / 1e6 / PEAK_GBPS * 100, 1),
                                               "decode_pct_peak": round(kb / ms_d / 1e6 / PEAK_GBPS * 100, 1)}
         del kb_list
+        # a long 16-bit decode (16x config 3's tokens, two buffer sets past the Infinity Cache), which the wave
+        # decoder runs with eight channels per lane; gate: equal to the float32 decode rounded to the 16-bit type
+        nl = 16 * nt
+        long_list = []
+        for s in range(2):
+            c = torch.empty(nl * ccfg.codeStride, dtype=torch.uint8, device=dev)
+            r = torch.empty(ccfg.groupCount(nl) * 2 * 64, dtype=torch.float16, device=dev)
+            q.enqueuePerChannelEncode(torch.randn(nl, 64, generator=gen, device=dev) * 3, c, r, nl, ccfg)
+            long_list.append((c, r, torch.empty(nl, 64, dtype=dt, device=dev)))
+        ms_l = timer.time(lambda i: q.enqueuePerChannelDecode(long_list[i % 2][0], long_list[i % 2][1],
+                                                              long_list[i % 2][2], nl, ccfg), steps, warm)
+        o32 = torch.empty(nl, 64, dtype=torch.float32, device=dev)
+        q.enqueuePerChannelDecode(long_list[0][0], long_list[0][1], o32, nl, ccfg)
+        q.enqueuePerChannelDecode(long_list[0][0], long_list[0][1], long_list[0][2], nl, ccfg)
+        same = bool(torch.equal(long_list[0][2].view(torch.int16), o32.to(dt).view(torch.int16)))
+        kl = kivi_bytes(nl, 64, 4, 64, elem=2)
+        out[f"kivi_d64_b4_G64_{nl}_tokens_decode_{io}"] = {
+            "decode_gbps": round(kl / ms_l / 1e6, 1), "decode_ms": round(ms_l, 5),
+            "decode_pct_peak": round(kl / ms_l / 1e6 / PEAK_GBPS * 100, 1), "equals_rounded_float32_decode": same}
+        if not same:
+            raise SystemExit(f"16-bit KIVI long decode ({io}) differs from the rounded float32 decode")
+        del long_list, o32
     return out
 
 
